@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Benchmark of the decode hot path on one MI355X.
+
+Workload: paged GQA decode attention at the Qwen3-8B
+attention shape -- 32 q heads / 8 kv heads, head_dim 128, bf16, batch 64,
+context lengths U[512, 4096], 16-token pages, block tables a random
+permutation of a pool 1.25x the pages needed.  One "step" is one decode
+attention call over the batch (split-KV kernel + split merge).  Four layers'
+worth of KV pools are cycled so that a step never finds its KV in the 256 MB
+MALL, as in a real multi-layer decode step.
+
+Prints one JSON line.  value = algorithmic HBM bytes per call / time per call
+(GB/s).  roofline uses the same numbers against the 8 TB/s HBM peak.
+cpu_baseline = the numpy oracle (tests' checker) timed on a bounded sample of
+the same workload on the host, one thread.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
+
+HBM_PEAK_GBS = 8000.0
+HQ, HKV, D, PAGE = 32, 8, 128, 16
+
+
+def algo_bytes(ctx: list[int], hq=HQ, hkv=HKV, d=D) -> int:
+    """sum ctx*Hkv*D*2(K,V)*2B + q and o (2*B*Hq*D*2B) + block-table ints + seqlens."""
+    kv = sum(ctx) * hkv * d * 2 * 2
+    qo = 2 * len(ctx) * hq * d * 2
+    bt = sum((c + PAGE - 1) // PAGE for c in ctx) * 4
+    return kv + qo + bt + 4 * len(ctx)
+
+
+def make_case(torch, ctx: list[int], layers: int, dev, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    need = [(c + PAGE - 1) // PAGE for c in ctx]
+    pool = math.ceil(1.25 * sum(need))
+    max_blocks = max(need)
+    cases = []
+    for layer in range(layers):
+        perm = torch.randperm(pool, generator=g)
+        bt = torch.full((len(ctx), max_blocks), -1, dtype=torch.int32)
+        o = 0
+        for b, n in enumerate(need):
+            bt[b, :n] = perm[o : o + n].to(torch.int32)
+            o += n
+        gd = torch.Generator(device=dev).manual_seed(seed * 100 + layer)
+        kc = torch.randn((pool, PAGE, HKV, D), generator=gd, device=dev).to(torch.bfloat16)
+        vc = torch.randn((pool, PAGE, HKV, D), generator=gd, device=dev).to(torch.bfloat16)
+        q = torch.randn((len(ctx), HQ * D), generator=gd, device=dev).to(torch.bfloat16)
+        cases.append((q, kc, vc, bt.to(dev), torch.tensor(ctx, dtype=torch.int32, device=dev)))
+    return cases
+
+
+def time_decode(torch, cases, steps: int, warmup: int):
+    from xvllm.layers.attention import paged_decode_attention
+
+    outs = [torch.empty_like(c[0]) for c in cases]
+
+    def step(i):
+        q, kc, vc, bt, sl = cases[i % len(cases)]
+        paged_decode_attention(q, kc, vc, bt, sl, HQ, HKV, D, out=outs[i % len(cases)])
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for i in range(steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return e0.elapsed_time(e1) / steps, wall
+
+
+def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
+    """numpy oracle on host cores, one BLAS thread, over a prefix of the
+    config-2 batch until the time budget is used (at least one sequence)."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    import oracle.ops as O
+
+    rng = np.random.default_rng(7)
+    done, nbytes, t_used = [], 0, 0.0
+    with threadpool_limits(limits=1):
+        for c in ctx_all:
+            npg = (c + PAGE - 1) // PAGE
+            kc = rng.standard_normal((npg, PAGE, HKV, D), dtype=np.float32)
+            vc = rng.standard_normal((npg, PAGE, HKV, D), dtype=np.float32)
+            q = rng.standard_normal((1, HQ, D), dtype=np.float32)
+            bt = rng.permutation(npg)[None, :]
+            t0 = time.perf_counter()
+            O.paged_decode_attention(q, kc, vc, bt, np.array([c]))
+            t_used += time.perf_counter() - t0
+            done.append(c)
+            if t_used >= budget_s:
+                break
+    nbytes = algo_bytes(done)
+    return {
+        "value": nbytes / t_used / 1e9,
+        "unit": "GB/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": f"numpy oracle, first {len(done)} of the 64 config-2 sequences "
+                  f"({sum(done)} tokens), {t_used:.1f} s",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); run with --gpus 1"}))
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        return 1
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(args.seed)
+    ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
+    cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1)
+    ms, wall = time_decode(torch, cases, args.steps, args.warmup)
+    nbytes = algo_bytes(ctx)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    sweep = {}
+    if not args.no_sweep:
+        for bsz in (1, 8, 64, 256):
+            c2 = [2048] * bsz
+            cs = make_case(torch, c2, layers=4 if bsz <= 64 else 2, dev=dev, seed=args.seed + bsz)
+            m2, _ = time_decode(torch, cs, 50, 10)
+            sweep[f"B{bsz}_ctx2048"] = {"us": round(m2 * 1e3, 2), "GB/s": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9, 1),
+                                        "frac": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            del cs
+        torch.cuda.empty_cache()
+
+    line = {
+        "metric": "decode attn HBM GB/s (% of 8 TB/s) + decode tok/s, Qwen3-8B bs=64, 1 GPU",
+        "value": round(gbs, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/K/V, random page permutation)",
+        "config": {
+            "workload": "config 2: paged GQA decode attention, Hq 32 / Hkv 8 / D 128, B 64, ctx U[512,4096], 16-token pages",
+            "batch": 64,
+            "total_ctx_tokens": sum(ctx),
+            "kv_pools_cycled": 4,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes_per_call": nbytes,
+            "kernel": "paged_decode_kernel<4> + merge_splits_kernel (one call)",
+        },
+        "sweep": sweep,
+        "wall_s_timed_region": round(wall, 4),
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(ctx)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,190 @@
+/*
+ * xv_kernels.h -- C ABI of the MI355X (gfx950) decode hot-path kernels.
+ *
+ * Every entry point takes raw device pointers, element strides (in elements,
+ * not bytes) and sizes, launches on `stream`, never allocates, never
+ * synchronises and never reads device memory on the host, so every call can
+ * be recorded into a hipGraph.  The return value is a hipError_t: 0 on
+ * success, hipErrorInvalidValue (1) for arguments the kernels do not support,
+ * otherwise the launch error.  All activations are bf16 (raw 16-bit words),
+ * arithmetic is fp32.
+ *
+ * Each declaration names the reference interface it replaces
+ * (xixii421/xixi-vllm, paths relative to the repository root).
+ */
+#ifndef XV_KERNELS_H
+#define XV_KERNELS_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Human readable text for a code returned by any xv_* entry point. */
+const char* xv_error_string(int code);
+
+/* ABI version; bumped whenever a signature below changes. */
+int xv_abi_version(void);
+
+/*
+ * KV store by slot mapping.
+ * Replaces store_kvcache / _store_kvcache_kernel, src/compute/kv_ops.py:8-62.
+ *   k_cache[slot[i], h, :] = key[i, h, :];  v_cache[slot[i], h, :] = value[i, h, :]
+ *   for every i in [0, num_tokens) with slot[i] >= 0 (slot -1 is skipped, kv_ops.py:22-23).
+ * key/value rows: element (i, h, d) at i*key_stride_tok + h*key_stride_head + d.
+ * cache element (slot, h, d) at slot*cache_stride_slot + h*cache_stride_head + d
+ * (for the pool layout [NB, BS, Hkv, D]: slot = page*BS + offset).
+ * head_dim must be a multiple of 8 and all row starts 16-byte aligned.
+ */
+int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                     const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                     void* k_cache, void* v_cache,
+                     int64_t cache_stride_slot, int64_t cache_stride_head,
+                     const int32_t* slot_mapping, int64_t num_tokens,
+                     int num_kv_heads, int head_dim, hipStream_t stream);
+
+/*
+ * Paged GQA decode attention (one query token per sequence, causal = attends
+ * to every cached token including the one stored this step).
+ * Replaces the decode branch of vllm::attention -> flash_attn_with_kvcache,
+ * src/compute/layers/attention.py:91-99.
+ *   q      : element (b, h, d) at b*q_stride_tok + h*q_stride_head + d   [B, Hq, D]
+ *   caches : element (page, t, kvh, d) at page*page_stride + t*tok_stride + kvh*head_stride + d
+ *   block_tables : int32 [B, bt_stride]; only the first ceil(seqlen/block_size) entries are read
+ *   cache_seqlens: int32 [B]; 0 marks a padding row whose output is written as zeros
+ *   out    : element (b, h, d) at b*out_stride_tok + h*D + d
+ *   workspace: at least xv_paged_decode_workspace_size(...) bytes (fp32 split partials)
+ * Query head h reads kv head h / (Hq / Hkv).  scale multiplies q.k (1/sqrt(D) in the reference).
+ * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16.
+ */
+size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                      int max_blocks_per_seq, int block_size, int head_dim);
+int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                              const void* k_cache, const void* v_cache,
+                              int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                              const int32_t* block_tables, int64_t bt_stride,
+                              const int32_t* cache_seqlens,
+                              void* out, int64_t out_stride_tok,
+                              void* workspace, size_t workspace_bytes,
+                              int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                              int block_size, int max_blocks_per_seq, float scale,
+                              hipStream_t stream);
+
+/*
+ * Varlen causal prefill attention, optionally reading K/V through the paged
+ * cache (chunked prefill / cached prefix).  Causal masking is bottom-right
+ * aligned: query i of sequence b (of q_len_b queries) sees keys
+ * j <= (k_len_b - q_len_b) + i.
+ * Replaces the prefill branch of vllm::attention -> flash_attn_varlen_func,
+ * src/compute/layers/attention.py:74-90.
+ *   q   : element (tok, h, d) at tok*q_stride_tok + h*q_stride_head + d, tok in [0, cu_q[B])
+ *   paged (block_tables != NULL): keys of sequence b are cache tokens 0..k_len_b-1
+ *         gathered through block_tables like the decode kernel.
+ *   dense (block_tables == NULL): key token j of sequence b is row cu_k[b]+j of k/v,
+ *         element (row, kvh, d) at row*kv_stride_tok + kvh*kv_stride_head + d.
+ *   out : element (tok, h, d) at tok*out_stride_tok + h*D + d.
+ * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 when paged.
+ */
+int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                         const void* k, const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
+                         const void* k_cache, const void* v_cache,
+                         int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                         const int32_t* block_tables, int64_t bt_stride,
+                         const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                         void* out, int64_t out_stride_tok,
+                         int batch, int max_seqlen_q, int num_q_heads, int num_kv_heads,
+                         int head_dim, int block_size, float scale, hipStream_t stream);
+
+/*
+ * RMSNorm into a new buffer.
+ * Replaces vllm::rmsnorm, src/compute/layers/ops.py:59-64 (flashinfer.norm.rmsnorm).
+ *   out[r, :] = x[r, :] * rsqrt(mean(x[r, :]^2) + eps) * w
+ * Row r = (o, i) with o in [0, n_outer), i in [0, n_inner); input row start
+ * o*x_stride_outer + i*x_stride_inner (so [T, H, D] views of a fused qkv work
+ * without a copy); output rows are contiguous (row r at r*hidden).
+ * hidden must be a multiple of 8, at most 16384.
+ */
+int xv_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
+               const void* weight, void* out, int64_t n_outer, int64_t n_inner,
+               int hidden, float eps, hipStream_t stream);
+
+/*
+ * In-place fused residual add + RMSNorm.
+ * Replaces vllm::fused_add_rmsnorm, src/compute/layers/ops.py:72-79.
+ *   s = x + residual (fp32);  residual <- bf16(s);  x <- bf16(s * rsqrt(mean(s^2)+eps) * w)
+ */
+int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+                         const void* weight, int64_t rows, int hidden, float eps,
+                         hipStream_t stream);
+
+/*
+ * NeoX rotary embedding from an fp32 cos||sin table [max_pos, D] into new buffers.
+ * Replaces vllm::rotary_embedding, src/compute/layers/ops.py:31-51
+ * (flashinfer apply_rope_with_cos_sin_cache, is_neox=True) with the table of
+ * build_cos_sin_cache, src/compute/layers/rotary.py:7-20.
+ *   o[:D/2] = x1*cos - x2*sin;  o[D/2:] = x2*cos + x1*sin
+ * q element (t, h, d) at t*q_stride_tok + h*q_stride_head + d; k likewise;
+ * q_out [T, Hq, D] and k_out [T, Hkv, D] contiguous.  positions int64 [T].
+ */
+int xv_rotary_embedding(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                        const int64_t* positions, const float* cos_sin_cache,
+                        void* q_out, void* k_out, int64_t num_tokens,
+                        int num_q_heads, int num_kv_heads, int head_dim, hipStream_t stream);
+
+/*
+ * Qwen3 per-head q/k RMSNorm fused with NeoX RoPE (one pass over q and k).
+ * Replaces Qwen3Attention._split_norm_rope, src/compute/models/qwen3.py:117-128
+ * (vllm::rmsnorm on the q and k head views, then vllm::rotary_embedding).
+ * The normed value is rounded to bf16 before the rotation, as the two
+ * reference ops do.  Layouts as xv_rotary_embedding; q_weight/k_weight [D].
+ */
+int xv_qk_norm_rope(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                    const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                    const void* q_weight, const void* k_weight, float eps,
+                    const int64_t* positions, const float* cos_sin_cache,
+                    void* q_out, void* k_out, int64_t num_tokens,
+                    int num_q_heads, int num_kv_heads, int head_dim, hipStream_t stream);
+
+/*
+ * SiLU-and-mul.
+ * Replaces vllm::silu_and_mul, src/compute/layers/ops.py:20-23 (gate first, up second).
+ *   out[t, i] = silu(x[t, i]) * x[t, I + i]
+ * x row t at t*x_stride, out row t at t*out_stride; inter_size multiple of 8.
+ */
+int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,
+                    int64_t num_tokens, int inter_size, hipStream_t stream);
+
+/*
+ * Batched sampler over bf16 logits [B, V] (row b at b*logits_stride).
+ * Replaces Sampler.forward, src/compute/sampler.py:27-119, and the greedy
+ * ParallelLMHead.argmax, src/compute/layers/vocab_parallel.py:180-216.
+ * Per row: temperature <= 1e-5 (or flag XV_SAMPLE_ALL_GREEDY) -> argmax of the
+ * logits, lowest index on ties.  Otherwise x = logit / temperature; candidates
+ * are ordered by descending x, ties by ascending id; the kept set is the
+ * shortest prefix satisfying top-k (top_ks[b] < V), top-p (a candidate is
+ * dropped when the mass strictly before it exceeds top_p of the top-k mass)
+ * and min-p (dropped when its probability is below min_p times the largest);
+ * the first candidate is always kept.  The token is then drawn by inverse CDF
+ * over the kept set in ascending id order with the explicit uniform
+ * uniforms[b] in [0, 1), masses in 2^-40 fixed point (exact integer sums).
+ * flags: XV_SAMPLE_* bits mirroring the reference's host-side switches.
+ * workspace: at least xv_sampler_workspace_size(B, V) bytes.
+ */
+#define XV_SAMPLE_ALL_GREEDY 1
+#define XV_SAMPLE_USE_TOP_K  2
+#define XV_SAMPLE_USE_TOP_P  4
+#define XV_SAMPLE_USE_MIN_P  8
+size_t xv_sampler_workspace_size(int batch, int vocab);
+int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
+              const float* temperatures, const float* top_ps, const int32_t* top_ks,
+              const float* min_ps, const float* uniforms, int flags,
+              int64_t* out_ids, void* workspace, size_t workspace_bytes,
+              hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XV_KERNELS_H */

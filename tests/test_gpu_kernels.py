@@ -1,0 +1,167 @@
+"""GPU parity of every hot-path kernel against the CPU oracle, through the
+C ABI (xvllm ops are thin ctypes wrappers).  Tolerances: bit-exact for the KV
+store; rtol/atol 2e-2 (bf16 output, fp32 accumulate) for attention and norms."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle.ops as O
+from helpers import f32, gen, make_paged, randn_bf16
+
+pytestmark = pytest.mark.gpu
+
+RTOL = ATOL = 2e-2
+
+
+def _close(got, want, rtol=RTOL, atol=ATOL):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    assert np.isfinite(got).all(), "non-finite output"
+    err = np.abs(got - want) - (atol + rtol * np.abs(want))
+    assert (err <= 0).all(), f"max excess {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+@pytest.mark.parametrize("n,hkv,d,strided", [(37, 8, 128, False), (64, 8, 128, True), (5, 2, 64, False)])
+def test_store_kvcache_bitexact(dev, n, hkv, d, strided):
+    from xvllm.kv_ops import store_kvcache
+
+    g = gen(1)
+    nb, page = 16, 16
+    if strided:  # k/v as views of a fused qkv row, like Qwen3Attention
+        qkv = randn_bf16((n, (32 + 2 * hkv) * d), g)
+        key = qkv[:, 32 * d : (32 + hkv) * d].view(n, hkv, d)
+        val = qkv[:, (32 + hkv) * d :].view(n, hkv, d)
+    else:
+        key, val = randn_bf16((n, hkv, d), g), randn_bf16((n, hkv, d), g)
+    slots = torch.randperm(nb * page, generator=g)[:n].to(torch.int32)
+    slots[::7] = -1
+    kc = randn_bf16((nb, page, hkv, d), g)
+    vc = randn_bf16((nb, page, hkv, d), g)
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    O.store_kvcache(key, val, kc_ref, vc_ref, slots)  # torch tensors index like numpy here
+    kg, vg = kc.to(dev), vc.to(dev)
+    store_kvcache(key.to(dev), val.to(dev), kg.view(-1, hkv, d), vg.view(-1, hkv, d), slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kg.cpu().view(torch.int16), kc_ref.view(torch.int16))
+    assert torch.equal(vg.cpu().view(torch.int16), vc_ref.view(torch.int16))
+
+
+@pytest.mark.parametrize(
+    "hq,hkv,ctx",
+    [
+        (32, 8, [1, 17, 300, 513, 16, 2048, 0, 77]),  # Qwen3-8B heads, pad row (0)
+        (16, 8, [128, 511, 256, 300]),                 # Qwen3-0.6B heads (group 2)
+        (64, 8, [1000, 33, 4096]),                     # Qwen3-32B heads (group 8)
+        (8, 8, [5, 260]),                              # MHA
+    ],
+)
+def test_paged_decode_attention(dev, hq, hkv, ctx):
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = gen(hq + len(ctx))
+    d = 128
+    need = sum((c + 15) // 16 for c in ctx)
+    kc, vc, bt, sl = make_paged(ctx, int(need * 1.25) + 4, hkv, d, g)
+    q = randn_bf16((len(ctx), hq, d), g)
+    want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
+    out = paged_decode_attention(q.view(len(ctx), -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), hq, hkv, d)
+    torch.cuda.synchronize()
+    _close(f32(out).reshape(len(ctx), hq, d), want)
+
+
+def test_paged_decode_config2_full_size(dev):
+    """Config 2 at full size (B 64, ctx U[512,4096]); a sample of rows is
+    checked against the oracle, every row for finiteness."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = gen(2024)
+    ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
+    need = sum((c + 15) // 16 for c in ctx)
+    kc, vc, bt, sl = make_paged(ctx, math.ceil(need * 1.25), 8, 128, g, fill_nan=False)
+    q = randn_bf16((64, 32, 128), g)
+    out = paged_decode_attention(q.view(64, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), 32, 8, 128)
+    got = f32(out).reshape(64, 32, 128)
+    rows = [0, 17, 63]
+    want = O.paged_decode_attention(f32(q)[rows], f32(kc), f32(vc), bt.numpy()[rows], sl.numpy()[rows])
+    _close(got[rows], want)
+    assert np.isfinite(got).all()
+
+
+@pytest.mark.parametrize("rows,hidden", [(7, 4096), (64, 1024), (33, 128), (3, 5120), (2, 4104)])
+def test_rmsnorm(dev, rows, hidden):
+    g = gen(rows)
+    x = randn_bf16((rows, hidden), g)
+    w = randn_bf16((hidden,), g, std=0.1, mean=1.0)
+    out = torch.ops.vllm.rmsnorm(x.to(dev), w.to(dev), 1e-6)
+    _close(f32(out), O.rmsnorm(f32(x), f32(w), 1e-6))
+
+
+def test_rmsnorm_head_view(dev):
+    """q/k head norm on a [T, H, D] view of a fused qkv row (no copy)."""
+    g = gen(5)
+    t, hq, d = 9, 32, 128
+    qkv = randn_bf16((t, 48 * d), g).to(dev)
+    q = qkv[:, : hq * d].view(t, hq, d)
+    w = randn_bf16((d,), g, std=0.1, mean=1.0)
+    out = torch.ops.vllm.rmsnorm(q, w.to(dev), 1e-6)
+    _close(f32(out), O.rmsnorm(f32(q), f32(w), 1e-6))
+
+
+@pytest.mark.parametrize("rows,hidden", [(7, 4096), (64, 1024), (1, 5120)])
+def test_fused_add_rmsnorm(dev, rows, hidden):
+    g = gen(rows + 1)
+    x, r = randn_bf16((rows, hidden), g), randn_bf16((rows, hidden), g)
+    w = randn_bf16((hidden,), g, std=0.1, mean=1.0)
+    xg, rg = x.to(dev), r.to(dev)
+    torch.ops.vllm.fused_add_rmsnorm(xg, rg, w.to(dev), 1e-6)
+    want_x, want_r = O.fused_add_rmsnorm(f32(x), f32(r), f32(w), 1e-6)
+    # the residual sum of two bf16 values rounded once is exact to the bit
+    assert np.array_equal(f32(rg), want_r)
+    _close(f32(xg), want_x)
+
+
+def _rope_inputs(g, t, hq, hkv, d=128, max_pos=32768):
+    qkv = randn_bf16((t, (hq + 2 * hkv) * d), g)
+    pos = torch.randint(0, max_pos, (t,), generator=g)
+    cs = torch.from_numpy(O.build_cos_sin_cache(d, max_pos, 1e6))
+    return qkv, pos, cs
+
+
+def test_rotary_embedding(dev):
+    g = gen(11)
+    t, hq, hkv, d = 19, 32, 8, 128
+    qkv, pos, cs = _rope_inputs(g, t, hq, hkv)
+    qg = qkv.to(dev)
+    q = qg[:, : hq * d].view(t, hq, d)
+    k = qg[:, hq * d : (hq + hkv) * d].view(t, hkv, d)
+    qo, ko = torch.ops.vllm.rotary_embedding(q, k, pos.to(dev), cs.to(dev), d)
+    _close(f32(qo), O.rope_neox(f32(q), pos.numpy(), cs.numpy()))
+    _close(f32(ko), O.rope_neox(f32(k), pos.numpy(), cs.numpy()))
+
+
+@pytest.mark.parametrize("t,hq,hkv", [(23, 32, 8), (8, 16, 8), (3, 64, 8)])
+def test_qk_norm_rope(dev, t, hq, hkv):
+    import xvllm.layers.ops  # noqa: F401
+
+    g = gen(t * hq)
+    d = 128
+    qkv, pos, cs = _rope_inputs(g, t, hq, hkv)
+    qw = randn_bf16((d,), g, std=0.1, mean=1.0)
+    kw = randn_bf16((d,), g, std=0.1, mean=1.0)
+    qg = qkv.to(dev)
+    q = qg[:, : hq * d].view(t, hq, d)
+    k = qg[:, hq * d : (hq + hkv) * d].view(t, hkv, d)
+    qo, ko = torch.ops.xv.qk_norm_rope(q, k, qw.to(dev), kw.to(dev), 1e-6, pos.to(dev), cs.to(dev))
+    wq, wk = O.qk_norm_rope(f32(q), f32(k), f32(qw), f32(kw), 1e-6, pos.numpy(), cs.numpy())
+    _close(f32(qo), wq)
+    _close(f32(ko), wk)
+
+
+@pytest.mark.parametrize("t,inter", [(5, 3072), (64, 12288), (3, 8)])
+def test_silu_and_mul(dev, t, inter):
+    g = gen(t)
+    x = randn_bf16((t, 2 * inter), g)
+    out = torch.ops.vllm.silu_and_mul(x.to(dev))
+    _close(f32(out), O.silu_and_mul(f32(x)))

@@ -1,0 +1,329 @@
+// HBM-streaming kernels of the decode hot path: KV store by slot mapping,
+// RMSNorm, fused residual-add + RMSNorm, NeoX RoPE, Qwen3 q/k-norm + RoPE,
+// SiLU-and-mul.  All move bf16 in 16-byte vectors (global_load_dwordx4),
+// accumulate in fp32 and reduce across lanes with DPP, so each element is
+// read once from HBM and written once.
+#include "xv_common.h"
+#include "../../include/xv_kernels.h"
+
+// --------------------------------------------------------------------------
+// KV store: one thread moves one 16-byte chunk of K and the matching chunk of V.
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void store_kvcache_kernel(
+    const bf16_t* __restrict__ key, int64_t ks_tok, int64_t ks_head,
+    const bf16_t* __restrict__ value, int64_t vs_tok, int64_t vs_head,
+    bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    int64_t cs_slot, int64_t cs_head, const int32_t* __restrict__ slots,
+    int64_t total_chunks, int chunks_per_tok, int chunks_per_head) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total_chunks) return;
+  int64_t tok = idx / chunks_per_tok;
+  int c = (int)(idx - tok * chunks_per_tok);
+  int32_t slot = slots[tok];
+  if (slot < 0) return;  // padding token (slot -1) writes nothing
+  int h = c / chunks_per_head;
+  int d = (c - h * chunks_per_head) * 8;
+  Vec8 kv = load_vec8_nt(key + tok * ks_tok + h * ks_head + d);
+  Vec8 vv = load_vec8_nt(value + tok * vs_tok + h * vs_head + d);
+  int64_t dst = (int64_t)slot * cs_slot + h * cs_head + d;
+  store_vec8(k_cache + dst, kv);
+  store_vec8(v_cache + dst, vv);
+}
+
+extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                                const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                                void* k_cache, void* v_cache,
+                                int64_t cache_stride_slot, int64_t cache_stride_head,
+                                const int32_t* slot_mapping, int64_t num_tokens,
+                                int num_kv_heads, int head_dim, hipStream_t stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8) return (int)hipErrorInvalidValue;
+  if (num_tokens == 0) return 0;
+  int cph = head_dim / 8;
+  int cpt = cph * num_kv_heads;
+  int64_t total = num_tokens * cpt;
+  int64_t blocks = (total + 255) / 256;
+  store_kvcache_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(
+      (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok,
+      value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_stride_slot, cache_stride_head,
+      slot_mapping, total, cpt, cph);
+  XV_CHECK_LAUNCH();
+  return 0;
+}
+
+// --------------------------------------------------------------------------
+// RMSNorm family.  TPR lanes own one row (16 = a DPP row, 64 = a wave); each
+// lane keeps up to VPT 8-element vectors of the row in registers.
+// --------------------------------------------------------------------------
+template <int TPR>
+XV_INLINE float row_sum(float x) {
+  if constexpr (TPR == 16) return row16_sum(x);
+  else return wave_sum(x);
+}
+
+template <int TPR, int VPT>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(
+    const bf16_t* __restrict__ x, int64_t s_outer, int64_t s_inner, const bf16_t* __restrict__ w,
+    bf16_t* __restrict__ out, int64_t n_outer, int64_t n_inner, int hidden, float eps) {
+  const int rows_per_block = 256 / TPR;
+  int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / TPR;
+  int lane = threadIdx.x % TPR;
+  int64_t rows = n_outer * n_inner;
+  bool active = row < rows;
+  int64_t o = active ? row / n_inner : 0;
+  int64_t i = active ? row - o * n_inner : 0;
+  const bf16_t* xr = x + o * s_outer + i * s_inner;
+  int nvec = hidden >> 3;
+  float v[VPT][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (active && vi < nvec) {
+      unpack8(load_vec8(xr + vi * 8), v[k]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[k][e] * v[k][e];
+    }
+  }
+  ss = row_sum<TPR>(ss);
+  if (!active) return;
+  float rcp = rsqrtf(ss / (float)hidden + eps);
+  bf16_t* orow = out + row * hidden;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (vi < nvec) {
+      float wf[8], r[8];
+      unpack8(load_vec8(w + vi * 8), wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
+      store_vec8(orow + vi * 8, pack8(r));
+    }
+  }
+}
+
+template <int TPR, int VPT>
+__global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
+    bf16_t* __restrict__ x, int64_t xs, bf16_t* __restrict__ res, int64_t rs,
+    const bf16_t* __restrict__ w, int64_t rows, int hidden, float eps) {
+  const int rows_per_block = 256 / TPR;
+  int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / TPR;
+  int lane = threadIdx.x % TPR;
+  bool active = row < rows;
+  bf16_t* xr = x + (active ? row : 0) * xs;
+  bf16_t* rr = res + (active ? row : 0) * rs;
+  int nvec = hidden >> 3;
+  float v[VPT][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (active && vi < nvec) {
+      float a[8], b[8];
+      unpack8(load_vec8_nt(xr + vi * 8), a);
+      unpack8(load_vec8_nt(rr + vi * 8), b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { v[k][e] = a[e] + b[e]; ss += v[k][e] * v[k][e]; }
+      store_vec8(rr + vi * 8, pack8(v[k]));
+    }
+  }
+  ss = row_sum<TPR>(ss);
+  if (!active) return;
+  float rcp = rsqrtf(ss / (float)hidden + eps);
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (vi < nvec) {
+      float wf[8], r[8];
+      unpack8(load_vec8(w + vi * 8), wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
+      store_vec8(xr + vi * 8, pack8(r));
+    }
+  }
+}
+
+template <template <int, int> class Launcher, typename... Args>
+static int dispatch_norm(int64_t rows, int hidden, hipStream_t stream, Args... args) {
+  if (hidden <= 0 || hidden % 8 || hidden > 16384) return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  int nvec = hidden / 8;
+  if (nvec <= 16) return Launcher<16, 1>::run(rows, stream, args...);
+  if (nvec <= 32) return Launcher<16, 2>::run(rows, stream, args...);
+  if (nvec <= 64) return Launcher<16, 4>::run(rows, stream, args...);
+  if (nvec <= 128) return Launcher<64, 2>::run(rows, stream, args...);
+  if (nvec <= 256) return Launcher<64, 4>::run(rows, stream, args...);
+  if (nvec <= 512) return Launcher<64, 8>::run(rows, stream, args...);
+  if (nvec <= 1024) return Launcher<64, 16>::run(rows, stream, args...);
+  return Launcher<64, 32>::run(rows, stream, args...);
+}
+
+template <int TPR, int VPT>
+struct RmsLaunch {
+  static int run(int64_t rows, hipStream_t stream, const bf16_t* x, int64_t so, int64_t si,
+                 const bf16_t* w, bf16_t* out, int64_t no, int64_t ni, int hidden, float eps) {
+    int64_t blocks = (rows + (256 / TPR) - 1) / (256 / TPR);
+    rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, so, si, w, out, no, ni, hidden, eps);
+    XV_CHECK_LAUNCH();
+    return 0;
+  }
+};
+template <int TPR, int VPT>
+struct AddRmsLaunch {
+  static int run(int64_t rows, hipStream_t stream, bf16_t* x, int64_t xs, bf16_t* r, int64_t rs,
+                 const bf16_t* w, int hidden, float eps) {
+    int64_t blocks = (rows + (256 / TPR) - 1) / (256 / TPR);
+    fused_add_rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, xs, r, rs, w, rows, hidden, eps);
+    XV_CHECK_LAUNCH();
+    return 0;
+  }
+};
+
+extern "C" int xv_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
+                          const void* weight, void* out, int64_t n_outer, int64_t n_inner,
+                          int hidden, float eps, hipStream_t stream) {
+  if (n_outer < 0 || n_inner < 0) return (int)hipErrorInvalidValue;
+  return dispatch_norm<RmsLaunch>(n_outer * n_inner, hidden, stream, (const bf16_t*)x, x_stride_outer,
+                                  x_stride_inner, (const bf16_t*)weight, (bf16_t*)out, n_outer, n_inner,
+                                  hidden, eps);
+}
+
+extern "C" int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, int64_t residual_stride,
+                                    const void* weight, int64_t rows, int hidden, float eps,
+                                    hipStream_t stream) {
+  if (rows < 0) return (int)hipErrorInvalidValue;
+  return dispatch_norm<AddRmsLaunch>(rows, hidden, stream, (bf16_t*)x, x_stride, (bf16_t*)residual,
+                                     residual_stride, (const bf16_t*)weight, hidden, eps);
+}
+
+// --------------------------------------------------------------------------
+// NeoX RoPE (optionally preceded by the per-head RMSNorm of Qwen3).
+// 16 lanes own one head of D = 128: lane j holds elements [8j, 8j+8); the
+// rotation partner of lane j is lane j^8 (same DPP row, fetched by row_ror:8).
+// --------------------------------------------------------------------------
+template <bool NORM>
+__global__ __launch_bounds__(256) void rope_kernel(
+    const bf16_t* __restrict__ q, int64_t qs_tok, int64_t qs_head,
+    const bf16_t* __restrict__ k, int64_t ks_tok, int64_t ks_head,
+    const bf16_t* __restrict__ qw, const bf16_t* __restrict__ kw, float eps,
+    const int64_t* __restrict__ positions, const float* __restrict__ cos_sin,
+    bf16_t* __restrict__ q_out, bf16_t* __restrict__ k_out,
+    int64_t num_tokens, int hq, int hkv) {
+  constexpr int D = 128;
+  const int heads = hq + hkv;
+  int64_t gh = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
+  int lane = threadIdx.x & 15;
+  bool active = gh < num_tokens * heads;
+  int64_t tok = active ? gh / heads : 0;
+  int h = active ? (int)(gh - tok * heads) : 0;
+  const bool is_q = h < hq;
+  const bf16_t* src = is_q ? q + tok * qs_tok + (int64_t)h * qs_head
+                           : k + tok * ks_tok + (int64_t)(h - hq) * ks_head;
+  float x[8];
+  unpack8(load_vec8(src + lane * 8), x);
+  if constexpr (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+    ss = row16_sum(ss);
+    float rcp = rsqrtf(ss / (float)D + eps);
+    float wf[8];
+    unpack8(load_vec8((is_q ? qw : kw) + lane * 8), wf);
+    // round to bf16 between the norm and the rotation, as the two separate ops do
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16((x[e] * rcp) * wf[e]));
+  }
+  float partner[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) partner[e] = dpp_f<0x128>(x[e]);
+  if (!active) return;
+  int64_t pos = positions[tok];
+  const float* cs = cos_sin + pos * D + (lane & 7) * 8;
+  float4 c0 = *reinterpret_cast<const float4*>(cs);
+  float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
+  float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
+  float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
+  float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float r[8];
+  if (lane < 8) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = x[e] * c[e] - partner[e] * s[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = x[e] * c[e] + partner[e] * s[e];
+  }
+  bf16_t* dst = is_q ? q_out + (tok * hq + h) * D : k_out + (tok * hkv + (h - hq)) * D;
+  store_vec8(dst + lane * 8, pack8(r));
+}
+
+static int launch_rope(bool norm, const void* q, int64_t qst, int64_t qsh, const void* k, int64_t kst,
+                       int64_t ksh, const void* qw, const void* kw, float eps, const int64_t* positions,
+                       const float* cs, void* q_out, void* k_out, int64_t T, int hq, int hkv, int D,
+                       hipStream_t stream) {
+  if (D != 128 || hq <= 0 || hkv < 0 || T < 0) return (int)hipErrorInvalidValue;
+  if (T == 0) return 0;
+  int64_t heads = T * (hq + hkv);
+  unsigned blocks = (unsigned)((heads + 15) / 16);
+  if (norm)
+    rope_kernel<true><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
+                                                  (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
+                                                  (bf16_t*)q_out, (bf16_t*)k_out, T, hq, hkv);
+  else
+    rope_kernel<false><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
+                                                   nullptr, nullptr, 0.f, positions, cs, (bf16_t*)q_out,
+                                                   (bf16_t*)k_out, T, hq, hkv);
+  XV_CHECK_LAUNCH();
+  return 0;
+}
+
+extern "C" int xv_rotary_embedding(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                   const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                   const int64_t* positions, const float* cos_sin_cache,
+                                   void* q_out, void* k_out, int64_t num_tokens,
+                                   int num_q_heads, int num_kv_heads, int head_dim, hipStream_t stream) {
+  return launch_rope(false, q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, nullptr, nullptr,
+                     0.f, positions, cos_sin_cache, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
+                     head_dim, stream);
+}
+
+extern "C" int xv_qk_norm_rope(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                               const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                               const void* q_weight, const void* k_weight, float eps,
+                               const int64_t* positions, const float* cos_sin_cache,
+                               void* q_out, void* k_out, int64_t num_tokens,
+                               int num_q_heads, int num_kv_heads, int head_dim, hipStream_t stream) {
+  return launch_rope(true, q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, q_weight, k_weight,
+                     eps, positions, cos_sin_cache, q_out, k_out, num_tokens, num_q_heads, num_kv_heads,
+                     head_dim, stream);
+}
+
+// --------------------------------------------------------------------------
+// SiLU-and-mul: one thread per 8 outputs.
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void silu_and_mul_kernel(const bf16_t* __restrict__ x, int64_t xs,
+                                                           bf16_t* __restrict__ out, int64_t os,
+                                                           int64_t total_vec, int vec_per_row, int inter) {
+  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total_vec) return;
+  int64_t row = idx / vec_per_row;
+  int c = (int)(idx - row * vec_per_row) * 8;
+  const bf16_t* xr = x + row * xs;
+  float g[8], u[8], r[8];
+  unpack8(load_vec8_nt(xr + c), g);
+  unpack8(load_vec8_nt(xr + inter + c), u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
+  store_vec8(out + row * os + c, pack8(r));
+}
+
+extern "C" int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,
+                               int64_t num_tokens, int inter_size, hipStream_t stream) {
+  if (num_tokens < 0 || inter_size <= 0 || inter_size % 8) return (int)hipErrorInvalidValue;
+  if (num_tokens == 0) return 0;
+  int vpr = inter_size / 8;
+  int64_t total = num_tokens * vpr;
+  silu_and_mul_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, stream>>>(
+      (const bf16_t*)x, x_stride, (bf16_t*)out, out_stride, total, vpr, inter_size);
+  XV_CHECK_LAUNCH();
+  return 0;
+}

@@ -1,0 +1,92 @@
+// Shared device helpers for the gfx950 kernels: bf16 <-> fp32, 16-byte vector
+// access, wave64 cross-lane reductions built on DPP row operations.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define XV_INLINE __device__ __forceinline__
+
+typedef uint16_t bf16_t;  // raw bf16 bits as stored in HBM
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+XV_INLINE float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+XV_INLINE float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+XV_INLINE float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// fp32 -> bf16 with round-to-nearest-even (torch's rounding); NaN stays NaN.
+XV_INLINE uint32_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+XV_INLINE uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+}
+
+// Eight bf16 values held as a 16-byte vector.
+struct alignas(16) Vec8 {
+  uint32_t w[4];
+};
+XV_INLINE Vec8 load_vec8(const bf16_t* p) {
+  uint4 v = *reinterpret_cast<const uint4*>(p);
+  Vec8 r; r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w; return r;
+}
+XV_INLINE void store_vec8(bf16_t* p, const Vec8& r) {
+  *reinterpret_cast<uint4*>(p) = make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]);
+}
+// Non-temporal streaming load for data read exactly once.
+XV_INLINE Vec8 load_vec8_nt(const bf16_t* p) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  Vec8 r; r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3]; return r;
+}
+XV_INLINE void unpack8(const Vec8& v, float* f) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) { f[2 * i] = bf16lo(v.w[i]); f[2 * i + 1] = bf16hi(v.w[i]); }
+}
+XV_INLINE Vec8 pack8(const float* f) {
+  Vec8 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r.w[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+  return r;
+}
+
+// ---- DPP cross-lane moves (wave64, rows of 16 lanes) ----
+// dpp_ctrl encodings (GCN/CDNA): quad_perm = 0x00-0xFF, row_ror:n = 0x120+n,
+// row_bcast:15 = 0x142, row_bcast:31 = 0x143.
+template <int CTRL>
+XV_INLINE float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+// Sum / max over the 16 lanes of a DPP row; every lane of the row gets the result.
+XV_INLINE float row16_sum(float x) {
+  x += dpp_f<0x128>(x);   // row_ror:8
+  x += dpp_f<0x124>(x);   // row_ror:4
+  x += dpp_f<0x4E>(x);    // quad_perm [2,3,0,1]
+  x += dpp_f<0xB1>(x);    // quad_perm [1,0,3,2]
+  return x;
+}
+XV_INLINE float row16_max(float x) {
+  x = fmaxf(x, dpp_f<0x128>(x));
+  x = fmaxf(x, dpp_f<0x124>(x));
+  x = fmaxf(x, dpp_f<0x4E>(x));
+  x = fmaxf(x, dpp_f<0xB1>(x));
+  return x;
+}
+// Full wave64 reductions (result valid in every lane).
+XV_INLINE float wave_sum(float x) {
+  x = row16_sum(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+XV_INLINE float wave_max(float x) {
+  x = row16_max(x);
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+#define XV_CHECK_LAUNCH() do { hipError_t e_ = hipGetLastError(); if (e_ != hipSuccess) return (int)e_; } while (0)

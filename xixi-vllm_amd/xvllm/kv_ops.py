@@ -1,0 +1,44 @@
+"""KV store by slot mapping (reference ``src/compute/kv_ops.py:35-62``)."""
+from __future__ import annotations
+
+import torch
+
+from . import _C
+from ._torch_glue import aligned16, ptr, require_bf16, require_cuda, stream_of
+
+
+def store_kvcache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> None:
+    """k_cache[slot[i]] = key[i]; v_cache[slot[i]] = value[i]; slot -1 is skipped.
+
+    key/value: [N, Hkv, D] (any row strides with a unit last stride; the
+    reference makes them contiguous first, kv_ops.py:42-45 -- here the kernel
+    reads the strided view directly).  k_cache/v_cache: [num_slots, Hkv, D]
+    views of the pool (or [NB, BS, Hkv, D]).
+    """
+    require_cuda(key, value, k_cache, v_cache, slot_mapping)
+    require_bf16(key, value, k_cache, v_cache)
+    n, num_heads, head_dim = key.shape
+    assert slot_mapping.numel() == n
+    for t in (key, value):
+        if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or not aligned16(t):
+            raise ValueError("key/value need a unit last stride and 16-byte aligned head rows")
+    kc = k_cache.reshape(-1, num_heads, head_dim)
+    vc = v_cache.reshape(-1, num_heads, head_dim)
+    if kc.stride() != vc.stride():
+        raise ValueError("k_cache and v_cache must share one layout")
+    slots = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
+    slots = slots.contiguous()
+    _C.check(
+        _C.lib().xv_store_kvcache(
+            ptr(key), key.stride(0), key.stride(1), ptr(value), value.stride(0), value.stride(1),
+            ptr(kc), ptr(vc), kc.stride(0), kc.stride(1), ptr(slots), n, num_heads, head_dim,
+            stream_of(key),
+        ),
+        "xv_store_kvcache",
+    )
