@@ -165,3 +165,99 @@ def test_silu_and_mul(dev, t, inter):
     x = randn_bf16((t, 2 * inter), g)
     out = torch.ops.vllm.silu_and_mul(x.to(dev))
     _close(f32(out), O.silu_and_mul(f32(x)))
+
+
+# ------------------------------------------------------------------ prefill attention
+@pytest.mark.parametrize(
+    "hq,hkv,qlens,klens,paged",
+    [
+        (32, 8, [37, 128, 1, 64], [37, 128, 1, 64], False),     # plain prefill (q_len == k_len)
+        (32, 8, [17, 64, 100], [300, 64, 612], True),           # chunked prefill over a cached prefix
+        (16, 8, [70, 5], [70, 200], True),                      # Qwen3-0.6B heads
+        (64, 8, [33], [129], True),                             # group 8
+        (8, 8, [20, 0, 9], [20, 0, 40], False),                 # MHA, an empty sequence
+    ],
+)
+def test_prefill_attention(dev, hq, hkv, qlens, klens, paged):
+    from xvllm.layers.attention import prefill_attention
+
+    g = gen(sum(qlens) + hq)
+    d = 128
+    cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    q = randn_bf16((int(cu_q[-1]), hq, d), g)
+    if paged:
+        need = sum((c + 15) // 16 for c in klens)
+        kc, vc, bt, _ = make_paged(klens, need + 5, hkv, d, g)
+        want = O.prefill_attention(f32(q), cu_q, cu_k, k_cache=f32(kc), v_cache=f32(vc), block_tables=bt.numpy())
+        out = prefill_attention(q.to(dev), None, None, torch.from_numpy(cu_q).to(dev), torch.from_numpy(cu_k).to(dev),
+                                max(qlens), hq, hkv, d, k_cache=kc.to(dev), v_cache=vc.to(dev), block_tables=bt.to(dev))
+    else:
+        k = randn_bf16((int(cu_k[-1]), hkv, d), g)
+        v = randn_bf16((int(cu_k[-1]), hkv, d), g)
+        want = O.prefill_attention(f32(q), cu_q, cu_k, k=f32(k), v=f32(v))
+        out = prefill_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(cu_q).to(dev),
+                                torch.from_numpy(cu_k).to(dev), max(qlens), hq, hkv, d)
+    torch.cuda.synchronize()
+    _close(f32(out).reshape(-1, hq, d), want)
+
+
+# ------------------------------------------------------------------ sampler
+def _sampler_case(g, b, v, std=2.0, ties=False):
+    x = torch.randn((b, v), generator=g) * std
+    if ties:
+        x = torch.round(x * 4) / 4  # few distinct values: ties everywhere
+    return x.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize(
+    "name,b,v,flags,temp,top_p,top_k,min_p,ties",
+    [
+        ("greedy", 8, 151936, 1, 1.0, 1.0, 0, 0.0, False),
+        ("greedy_ties", 4, 4096, 1, 1.0, 1.0, 0, 0.0, True),
+        ("temperature", 8, 151936, 0, 0.7, 1.0, 0, 0.0, False),
+        ("topk50_topp0.9", 16, 151936, 2 | 4, 0.7, 0.9, 50, 0.0, False),
+        ("topp0.95", 8, 151936, 4, 1.0, 0.95, 0, 0.0, False),
+        ("minp", 8, 151936, 8, 1.0, 1.0, 0, 0.1, False),
+        ("all_filters_ties", 8, 32000, 2 | 4 | 8, 0.8, 0.8, 300, 0.02, True),
+        ("odd_vocab", 5, 1003, 2 | 4, 1.1, 0.6, 7, 0.0, False),
+    ],
+)
+def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, ties):
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(b * 7 + v)
+    logits = _sampler_case(g, b, v, ties=ties)
+    temps = torch.full((b,), temp)
+    temps[::3] = 0.0 if name not in ("greedy", "greedy_ties") else temp  # mixed greedy rows
+    tps = torch.full((b,), top_p)
+    tks = torch.full((b,), top_k if top_k else v, dtype=torch.int32)
+    mps = torch.full((b,), min_p)
+    u = torch.rand(b, generator=g)
+    u[0] = 0.0
+    want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                    mps.numpy(), u.numpy(), flags)
+    got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev),
+                 all_greedy=bool(flags & 1), use_top_k=bool(flags & 2), use_top_p=bool(flags & 4),
+                 use_min_p=bool(flags & 8))
+    torch.cuda.synchronize()
+    assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
+
+
+def test_sampler_many_draws_bitexact(dev):
+    """One row, 256 stratified uniforms: every draw equals the oracle's."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(99)
+    v, n = 151936, 256
+    row = _sampler_case(g, 1, v, std=1.0)
+    logits = row.repeat(n, 1)
+    u = (torch.arange(n, dtype=torch.float32) + 0.5) / n
+    args = dict(temps=torch.full((n,), 0.7), tps=torch.full((n,), 0.9), tks=torch.full((n,), 50, dtype=torch.int32))
+    want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), args["temps"].numpy(), args["tps"].numpy(),
+                    args["tks"].numpy(), None, u.numpy(), 2 | 4)
+    got = sample(logits.to(dev), args["temps"].to(dev), args["tps"].to(dev), args["tks"].to(dev), None, u.to(dev),
+                 use_top_k=True, use_top_p=True)
+    assert np.array_equal(got.cpu().numpy(), want)

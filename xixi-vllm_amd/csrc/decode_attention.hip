@@ -1,21 +1,19 @@
 // Paged GQA decode attention for gfx950.
 //
-// Work unit: one wave64 workgroup per (sequence, group of GW query heads
-// sharing one kv head, KV split of `pps` 16-token pages).  The wave streams
-// its pages straight from HBM into registers in the operand layout of
-// v_mfma_f32_16x16x32_bf16, so no LDS is used:
-//   lane = 16*g + t  (t = token within the page, g = 0..3)
-//   K/V: lane loads 16-byte chunks c = 4*s + g (s = 0..3) of token row t, i.e.
-//        for each s the four lanes of a token read 64 contiguous bytes.
-//   Q:   A operand, row i = lane%16 holds query head i % GW (rows replicated),
-//        same chunk mapping, so MFMA step s contracts d in chunk 4s+g.
-//   S = Q K^T lands as acc[r] = S[row 4g+r][token t]  ->  head r % GW.
-// Every lane therefore holds the scores of its own token for all GW heads,
-// and P.V runs on the VALU against the V chunks the same lane loaded:
-//   o[h][d = 8*(4s+g)+e] += p[h] * v[s][e].
-// Softmax is online in the exp2 domain with the running max reduced over the
-// 16 tokens of a page by DPP (identical in all four lane rows).  The 16 token
-// lanes are summed once at the end of the split with DPP row reductions.
+// Work unit: one wave64 workgroup per (sequence, kv head, KV split of `pps`
+// 16-token pages); all G = Hq/Hkv query heads of the kv head are served by
+// the one pass over the pages.  Per page:
+//   K (HBM -> VGPR) is the A operand of S^T = K Q^T on v_mfma_f32_16x16x32_bf16:
+//     lane = 16*g + i: row i = token i, MFMA step s contracts d-chunk 4s+g, so
+//     the four lanes of a token read 64 contiguous bytes per load instruction.
+//   Q^T is the B operand: column c = lane%16 holds query head c % G.
+//   S^T lands as acc[r] = S[head c%G][token 4g+r]; the online softmax reduces
+//   the 4 tokens in-lane and the 4 lane rows with two cross-row shuffles.
+//   P (bf16) is then already the A operand of O = P V on
+//   v_mfma_f32_16x16x16_bf16 (row = head, k = token 4g+j): no shuffle.
+//   V (HBM -> VGPR -> LDS, rows padded to 288 B) is read back transposed with
+//   ds_read_b64_tr_b16 as the B operand (k = token, column = d), 8 d-tiles.
+//   O accumulates in the MFMA output layout: 8 tiles x 4 fp32 per lane.
 // Splits of one (sequence, head) are merged by a second kernel through an
 // fp32 workspace holding normalised partial outputs and their log2-sum-exp.
 #include "xv_common.h"
@@ -27,6 +25,10 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kPage = 16;
+constexpr int kLdsRow = 288;  // bytes per V row in LDS (256 + 32 pad: conflict-free transposed reads)
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4_t lds_short4;
 
 struct DecodeArgs {
   const bf16_t* q; int64_t q_st, q_sh;
@@ -50,9 +52,9 @@ XV_INLINE void load_page(PageRegs& r, const DecodeArgs& a, int page, int kvh, in
   const bf16_t* kp = a.kc + base + 8 * g;
   const bf16_t* vp = a.vc + base + 8 * g;
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.k[s] = load_vec8_nt(kp + 32 * s);
+  for (int s = 0; s < 4; ++s) r.k[s] = load_vec8(kp + 32 * s);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.v[s] = load_vec8_nt(vp + 32 * s);
+  for (int s = 0; s < 4; ++s) r.v[s] = load_vec8(vp + 32 * s);
 }
 
 XV_INLINE bf16x8_t as_bf16x8(const Vec8& v) {
@@ -61,73 +63,94 @@ XV_INLINE bf16x8_t as_bf16x8(const Vec8& v) {
   return r;
 }
 
-template <int GW>
 struct SplitState {
-  float m[GW];
-  float l[GW];
-  float o[GW][4][8];
+  float m;      // running max (log2 domain) of head c%G, identical across lane rows
+  float l;      // lane-local sum of p over this lane's tokens
+  floatx4_t o[8];  // O tile n: rows 4g+r (head (4g+r)%G), column d = 16n + lane%16
 };
 
-template <int GW>
-XV_INLINE void process_page(SplitState<GW>& st, PageRegs& r, const bf16x8_t (&qa)[4], int tok_idx,
-                            int ctx, bool last, float scale_log2) {
-  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[s], as_bf16x8(r.k[s]), acc, 0, 0, 0);
-  const bool valid = tok_idx < ctx;
-  if (last && !valid) {
-    // cache rows past the sequence end may hold anything (even NaN): zero them
+template <int G>
+XV_INLINE void process_page(SplitState& st, PageRegs& r, char* lds, const bf16x8_t (&qb)[4], int page_tok0,
+                            int ctx, bool last, float scale_log2, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  // ---- V -> LDS (zero rows past the sequence end: they may hold NaN) ----
+  if (last && page_tok0 + i >= ctx) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) r.v[s].w[0] = r.v[s].w[1] = r.v[s].w[2] = r.v[s].w[3] = 0u;
   }
 #pragma unroll
-  for (int h = 0; h < GW; ++h) {
-    float sc = valid ? acc[h] * scale_log2 : -INFINITY;
-    float mx = row16_max(sc);
-    float m_new = fmaxf(st.m[h], mx);
-    if (m_new > st.m[h]) {
-      float alpha = __builtin_amdgcn_exp2f(st.m[h] - m_new);
-      st.l[h] *= alpha;
+  for (int s = 0; s < 4; ++s)
+    *reinterpret_cast<uint4*>(lds + i * kLdsRow + 16 * (4 * s + g)) =
+        make_uint4(r.v[s].w[0], r.v[s].w[1], r.v[s].w[2], r.v[s].w[3]);
+  // ---- S^T = K Q^T ----
+  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r.k[s]), qb[s], acc, 0, 0, 0);
+  // ---- online softmax for head c%G over tokens 4g..4g+3 ----
+  float sc[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) st.o[h][s][e] *= alpha;
-      st.m[h] = m_new;
-    }
-    float p = __builtin_amdgcn_exp2f(sc - m_new);
-    st.l[h] += p;
+  for (int j = 0; j < 4; ++j) sc[j] = (page_tok0 + 4 * g + j < ctx) ? acc[j] * scale_log2 : -INFINITY;
+  float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+  mx = fmaxf(mx, __shfl_xor(mx, 16));
+  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  const float m_new = fmaxf(st.m, mx);
+  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+  st.m = m_new;
+  float p[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+  for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - m_new);
+  st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+  short4_t pa;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        st.o[h][s][2 * w] += p * bf16lo(r.v[s].w[w]);
-        st.o[h][s][2 * w + 1] += p * bf16hi(r.v[s].w[w]);
-      }
-    }
+  for (int j = 0; j < 4; ++j) pa[j] = (short)f32_to_bf16(p[j]);
+  // rescale O rows: row 4g+rr holds head (4g+rr)%G, whose alpha sits in lane (row base)|head
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) {
+    const int hsrc = (4 * g + rr) % G;
+    const float ar = __shfl(alpha, (lane & 48) | hsrc);
+#pragma unroll
+    for (int n = 0; n < 8; ++n) st.o[n][rr] *= ar;
+  }
+  // No barrier: the workgroup is one wave and a wave's LDS operations complete
+  // in order, so the transposed reads below see the rows just written (the
+  // compiler keeps the order: both access the same __shared__ array).  A
+  // __syncthreads here would also wait for the prefetched page.
+  // ---- O += P V, V^T tiles read transposed from LDS ----
+  const int rowt = 4 * g + (i >> 2);
+  const char* vb = lds + rowt * kLdsRow + 8 * (i & 3);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) {
+    short4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + 32 * n));
+    st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt, st.o[n], 0, 0, 0);
   }
 }
 
-template <int GW>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
-  const int lane = threadIdx.x;
-  const int t = lane & 15, g = lane >> 4;
-  const int hgroups = a.hkv * (a.group / GW);
-  const int b = blockIdx.x / hgroups;
-  const int hg = blockIdx.x - b * hgroups;
-  const int kvh = hg / (a.group / GW);
-  const int head0 = kvh * a.group + (hg - kvh * (a.group / GW)) * GW;
-  const int split = blockIdx.y;
+template <int G, int NBUF, int WPB>
+__global__ __launch_bounds__(64 * WPB) void paged_decode_kernel(DecodeArgs a, int units) {
+  __shared__ __attribute__((aligned(16))) char lds_all[WPB][kPage * kLdsRow];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  char* lds = lds_all[wave];
+  const int i = lane & 15, g = lane >> 4;
+  // unit = split * (B*Hkv) + (b*Hkv + kvh): the waves of a workgroup are
+  // independent units (no intra-workgroup synchronisation anywhere)
+  const int unit = blockIdx.x * WPB + wave;
+  if (unit >= units) return;
+  const int bh_count = units / a.max_splits;
+  const int split = unit / bh_count;
+  const int bh = unit - split * bh_count;
+  const int b = bh / a.hkv;
+  const int kvh = bh - b * a.hkv;
+  const int head0 = kvh * G;
   const int ctx = a.seqlens[b];
   const int npages = (ctx + kPage - 1) / kPage;
   const int nsplit = (npages + a.pps - 1) / a.pps;
 
   if (ctx <= 0) {
     // padding row: defined zero output, written once by split 0
-    if (split == 0 && t < GW) {
-      bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)(head0 + t) * kD + 8 * g;
-      Vec8 z; z.w[0] = z.w[1] = z.w[2] = z.w[3] = 0u;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) store_vec8(o + 32 * s, z);
+    if (split == 0) {
+      for (int e = lane; e < G * kD / 2; e += 64)
+        reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)head0 * kD)[e] = 0u;
     }
     return;
   }
@@ -139,68 +162,59 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   int pid = 0;
   if (lane < np) pid = a.bt[(int64_t)b * a.bt_stride + p0 + lane];
 
-  bf16x8_t qa[4];
+  bf16x8_t qb[4];
   {
-    const bf16_t* qp = a.q + (int64_t)b * a.q_st + (int64_t)(head0 + (t % GW)) * a.q_sh + 8 * g;
+    const bf16_t* qp = a.q + (int64_t)b * a.q_st + (int64_t)(head0 + (i % G)) * a.q_sh + 8 * g;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qa[s] = as_bf16x8(load_vec8(qp + 32 * s));
+    for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(load_vec8(qp + 32 * s));
   }
 
-  SplitState<GW> st;
+  SplitState st;
+  st.m = -INFINITY;
+  st.l = 0.f;
 #pragma unroll
-  for (int h = 0; h < GW; ++h) {
-    st.m[h] = -INFINITY;
-    st.l[h] = 0.f;
+  for (int n = 0; n < 8; ++n) st.o[n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+  // NBUF page buffers: NBUF-1 pages always in flight ahead of the one being
+  // processed.  Prefetches are issued unconditionally (clamped to the split's
+  // last page) so the outstanding-load count is the same on every path and
+  // the compiler's vmcnt waits stay partial.
+  PageRegs r[NBUF];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+  for (int k = 0; k < NBUF - 1; ++k) load_page(r[k], a, __builtin_amdgcn_readlane(pid, min(k, np - 1)), kvh, i, g);
+  for (int it = 0; it < np; it += NBUF) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) st.o[h][s][e] = 0.f;
+    for (int u = 0; u < NBUF; ++u) {
+      load_page(r[(u + NBUF - 1) % NBUF], a, __builtin_amdgcn_readlane(pid, min(it + u + NBUF - 1, np - 1)), kvh, i, g);
+      if (it + u < np)
+        process_page<G>(st, r[u], lds, qb, (p0 + it + u) * kPage, ctx, p0 + it + u == npages - 1, a.scale_log2, lane);
+    }
   }
 
-  PageRegs r0, r1;
-  load_page(r0, a, __builtin_amdgcn_readlane(pid, 0), kvh, t, g);
-  for (int i = 0; i < np; i += 2) {
-    if (i + 1 < np) load_page(r1, a, __builtin_amdgcn_readlane(pid, i + 1), kvh, t, g);
-    process_page<GW>(st, r0, qa, (p0 + i) * kPage + t, ctx, p0 + i == npages - 1, a.scale_log2);
-    if (i + 1 >= np) break;
-    if (i + 2 < np) load_page(r0, a, __builtin_amdgcn_readlane(pid, i + 2), kvh, t, g);
-    process_page<GW>(st, r1, qa, (p0 + i + 1) * kPage + t, ctx, p0 + i + 1 == npages - 1, a.scale_log2);
-  }
-
-  // sum the 16 token lanes of each row
+  // total p-sum of head c%G, then fetch it for the heads of this lane's O rows
+  float lsum = st.l;
+  lsum += __shfl_xor(lsum, 16);
+  lsum += __shfl_xor(lsum, 32);
+  // rows 4g+rr with 4g+rr < G hold distinct heads; the others are replicas
 #pragma unroll
-  for (int h = 0; h < GW; ++h) {
-    st.l[h] = row16_sum(st.l[h]);
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) st.o[h][s][e] = row16_sum(st.o[h][s][e]);
-  }
-
-#pragma unroll
-  for (int h = 0; h < GW; ++h) {
-    if (t != h) continue;
-    const float inv = 1.0f / st.l[h];
+  for (int rr = 0; rr < 4; ++rr) {
+    const int row = 4 * g + rr;
+    const int hsrc = row % G;
+    const float lh = __shfl(lsum, hsrc);
+    const float mh = __shfl(st.m, hsrc);
+    if (row >= G) continue;
+    const float inv = 1.0f / lh;
+    const int head = head0 + row;
     if (nsplit == 1) {
-      bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)(head0 + h) * kD + 8 * g;
+      bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float v[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = st.o[h][s][e] * inv;
-        store_vec8(o + 32 * s, pack8(v));
-      }
+      for (int n = 0; n < 8; ++n) o[16 * n] = (bf16_t)f32_to_bf16(st.o[n][rr] * inv);
     } else {
-      const int64_t row = ((int64_t)b * a.hq + head0 + h) * a.max_splits + split;
-      float* o = a.ws_o + row * kD + 8 * g;
+      const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_splits + split;
+      float* o = a.ws_o + wrow * kD + i;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        float4 v0 = make_float4(st.o[h][s][0] * inv, st.o[h][s][1] * inv, st.o[h][s][2] * inv, st.o[h][s][3] * inv);
-        float4 v1 = make_float4(st.o[h][s][4] * inv, st.o[h][s][5] * inv, st.o[h][s][6] * inv, st.o[h][s][7] * inv);
-        *reinterpret_cast<float4*>(o + 32 * s) = v0;
-        *reinterpret_cast<float4*>(o + 32 * s + 4) = v1;
-      }
-      if (g == 0) a.ws_lse[row] = st.m[h] + __log2f(st.l[h]);
+      for (int n = 0; n < 8; ++n) o[16 * n] = st.o[n][rr] * inv;
+      if (i == 0) a.ws_lse[wrow] = mh + __log2f(lh);
     }
   }
 }
@@ -238,6 +252,25 @@ int pages_per_split() {
     return v;
   }();
   return pps;
+}
+
+// Launch variants (page buffers x waves per workgroup); 0 is the default.
+int decode_variant() {
+  static int v = [] {
+    const char* e = getenv("XV_DECODE_VARIANT");
+    return e ? atoi(e) : 0;
+  }();
+  return v;
+}
+
+template <int G>
+void launch_group(const DecodeArgs& a, int units, int variant, hipStream_t stream) {
+  switch (variant) {
+    case 1: paged_decode_kernel<G, 2, 1><<<units, 64, 0, stream>>>(a, units); break;
+    case 2: paged_decode_kernel<G, 3, 1><<<units, 64, 0, stream>>>(a, units); break;
+    case 3: paged_decode_kernel<G, 2, 4><<<(units + 3) / 4, 256, 0, stream>>>(a, units); break;
+    default: paged_decode_kernel<G, 3, 4><<<(units + 3) / 4, 256, 0, stream>>>(a, units); break;
+  }
 }
 
 }  // namespace
@@ -281,12 +314,13 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   a.ws_lse = a.ws_o ? a.ws_o + (size_t)batch * num_q_heads * max_splits * kD : nullptr;
   a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.pps = pps; a.max_splits = max_splits;
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int gw = group >= 4 ? 4 : group;
-  dim3 grid((unsigned)(batch * num_kv_heads * (group / gw)), (unsigned)max_splits);
-  switch (gw) {
-    case 1: paged_decode_kernel<1><<<grid, 64, 0, stream>>>(a); break;
-    case 2: paged_decode_kernel<2><<<grid, 64, 0, stream>>>(a); break;
-    default: paged_decode_kernel<4><<<grid, 64, 0, stream>>>(a); break;
+  const int units = batch * num_kv_heads * max_splits;
+  const int variant = decode_variant();
+  switch (group) {
+    case 1: launch_group<1>(a, units, variant, stream); break;
+    case 2: launch_group<2>(a, units, variant, stream); break;
+    case 4: launch_group<4>(a, units, variant, stream); break;
+    default: launch_group<8>(a, units, variant, stream); break;
   }
   XV_CHECK_LAUNCH();
   if (max_splits > 1) {

@@ -1,0 +1,103 @@
+"""Batched token sampler with the interface of xixi-vllm's
+``src/compute/sampler.py:20-119`` (``Sampler.forward``), running the gfx950
+radix-select sampling kernel (one workgroup per row).
+
+Semantics follow the reference: temperature <= 1e-5 rows (or ``all_greedy``)
+take the argmax of the logits (lowest id on ties, as ``argmax``); otherwise
+the logits are divided by the temperature and filtered by top-k, then top-p
+and min-p over the renormalised top-k set, keeping at least the best token.
+The reference draws with ``torch.multinomial`` / exponential noise; here the
+draw is an explicit uniform per row (``uniforms``, or ``torch.rand`` from
+``generator`` when omitted) used as an inverse CDF over the kept tokens in
+ascending id order with exact fixed-point masses, so a given uniform always
+yields the same token -- the same distribution as the reference, made
+reproducible.
+"""
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from . import _C
+from ._torch_glue import ptr, require_bf16, require_cuda, stream_of
+
+
+def sample(
+    logits: torch.Tensor,
+    temperatures: torch.Tensor | None,
+    top_ps: torch.Tensor | None = None,
+    top_ks: torch.Tensor | None = None,
+    min_ps: torch.Tensor | None = None,
+    uniforms: torch.Tensor | None = None,
+    *,
+    all_greedy: bool = False,
+    use_top_k: bool = False,
+    use_top_p: bool = False,
+    use_min_p: bool = False,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Raw entry: bf16 logits [B, V] -> int64 ids [B] (graph-capturable)."""
+    require_cuda(logits)
+    require_bf16(logits)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    bsz, vocab = logits.shape
+    flags = 0
+    if all_greedy:
+        flags |= _C.XV_SAMPLE_ALL_GREEDY
+    if use_top_k:
+        flags |= _C.XV_SAMPLE_USE_TOP_K
+    if use_top_p:
+        flags |= _C.XV_SAMPLE_USE_TOP_P
+    if use_min_p:
+        flags |= _C.XV_SAMPLE_USE_MIN_P
+
+    def prep(t, dt):
+        if t is None:
+            return None
+        require_cuda(t)
+        t = t.to(dt)
+        return t if t.is_contiguous() else t.contiguous()
+
+    temps = prep(temperatures, torch.float32)
+    tps, tks, mps, us = prep(top_ps, torch.float32), prep(top_ks, torch.int32), prep(min_ps, torch.float32), prep(uniforms, torch.float32)
+    if out is None:
+        out = torch.empty(bsz, dtype=torch.int64, device=logits.device)
+    _C.check(
+        _C.lib().xv_sample(
+            ptr(logits), logits.stride(0), bsz, vocab, ptr(temps), ptr(tps), ptr(tks), ptr(mps), ptr(us), flags,
+            ptr(out), None, 0, stream_of(logits),
+        ),
+        "xv_sample",
+    )
+    return out
+
+
+class Sampler(nn.Module):
+    def forward(
+        self,
+        logits: torch.Tensor,
+        temperatures: torch.Tensor,
+        top_ps: torch.Tensor | None = None,
+        top_ks: torch.Tensor | None = None,
+        min_ps: torch.Tensor | None = None,
+        generator: torch.Generator | None = None,
+        *,
+        all_greedy: bool = False,
+        any_greedy: bool = False,
+        use_top_k: bool = False,
+        use_top_p: bool = False,
+        use_min_p: bool = False,
+        max_top_k: int = 0,
+        uniforms: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Returns [batch] token ids.  ``any_greedy`` and ``max_top_k`` are accepted
+        for interface parity (the kernel checks each row's temperature and
+        top-k itself)."""
+        del any_greedy, max_top_k
+        if uniforms is None and not all_greedy:
+            uniforms = torch.rand(logits.shape[0], generator=generator, device=logits.device)
+        return sample(
+            logits, temperatures, top_ps, top_ks, min_ps, uniforms,
+            all_greedy=all_greedy, use_top_k=use_top_k, use_top_p=use_top_p, use_min_p=use_min_p,
+        )
