@@ -1,8 +1,14 @@
 // Paged GQA decode attention for gfx950.
 //
-// Work unit: one wave64 workgroup per (sequence, kv head, KV split of `pps`
-// 16-token pages); all G = Hq/Hkv query heads of the kv head are served by
-// the one pass over the pages.  Per page:
+// Work split ("stream-K" over pages): the (sequence, kv head, page) space is
+// flattened in that order and cut into equal contiguous ranges of L pages,
+// one per resident single-wave workgroup, so every wave streams the same
+// number of pages and the whole grid is resident at once (no dispatch rounds,
+// no tail of late units).  A range may cover several (sequence, kv head)
+// segments; a segment cut by range boundaries yields one partial per wave,
+// merged by a second kernel through an fp32 workspace (normalised partial
+// output + log2-sum-exp).  A segment inside one range is written directly.
+// All G = Hq/Hkv query heads of a kv head are served by one pass.  Per page:
 //   K (HBM -> VGPR) is the A operand of S^T = K Q^T on v_mfma_f32_16x16x32_bf16:
 //     lane = 16*g + i: row i = token i, MFMA step s contracts d-chunk 4s+g, so
 //     the four lanes of a token read 64 contiguous bytes per load instruction.
@@ -14,10 +20,8 @@
 //   V (HBM -> VGPR -> LDS, rows padded to 288 B) is read back transposed with
 //   ds_read_b64_tr_b16 as the B operand (k = token, column = d), 8 d-tiles.
 //   O accumulates in the MFMA output layout: 8 tiles x 4 fp32 per lane.
-// Splits of one (sequence, head) are merged by a second kernel through an
-// fp32 workspace holding normalised partial outputs and their log2-sum-exp.
 #include "xv_common.h"
-#include "../../include/xv_kernels.h"
+#include "xv_kernels.h"
 #include <math.h>
 #include <stdlib.h>
 
@@ -25,7 +29,14 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kPage = 16;
-constexpr int kLdsRow = 288;  // bytes per V row in LDS (256 + 32 pad: conflict-free transposed reads)
+constexpr int kVPageBytes = 4096;  // one page's V rows of one kv head in LDS
+#ifndef XV_DECODE_NBUF
+#define XV_DECODE_NBUF 6
+#endif
+constexpr int kNbuf = XV_DECODE_NBUF;
+#ifndef XV_DECODE_WAVES_PER_CU
+#define XV_DECODE_WAVES_PER_CU 4  // one wave per SIMD: no oldest-first starvation between waves
+#endif  // pages in registers/LDS per wave (kNbuf-1 in flight ahead)
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4;
@@ -38,23 +49,53 @@ struct DecodeArgs {
   const int32_t* seqlens;
   bf16_t* out; int64_t out_st;
   float* ws_o; float* ws_lse;
-  int hq, hkv, group, pps, max_splits;
+  int batch, hq, hkv, group;
+  int lmin;       // minimum pages per wave range
+  int max_parts;  // partial slots per (sequence, head) in the workspace
+  int nwaves;     // workgroups of the main kernel (the range count)
   float scale_log2;
 };
 
 struct PageRegs {
-  Vec8 k[4];
-  Vec8 v[4];
+  Vec8 k[4];  // K rows of the page in MFMA A-operand layout (V goes straight to LDS)
 };
 
-XV_INLINE void load_page(PageRegs& r, const DecodeArgs& a, int page, int kvh, int t, int g) {
-  int64_t base = (int64_t)page * a.page_stride + (int64_t)t * a.tok_stride + (int64_t)kvh * a.head_stride;
-  const bf16_t* kp = a.kc + base + 8 * g;
-  const bf16_t* vp = a.vc + base + 8 * g;
+// A page's K rows are read with buffer loads into VGPRs and its V rows with
+// buffer loads straight into LDS (LDS-DMA: lane l's 16 bytes land at
+// base + 16*l), so V never occupies VGPRs.  The page base is wave uniform (a
+// scalar resource per page) and the per-lane offset
+// t*tok_stride + 8*g (+32*s) is the same for every page (any page layout with
+// 256-byte head rows works: [BS][Hkv][D] as the reference pool, or [Hkv][BS][D]).
+// The resource covers only the page's valid rows: rows past the sequence end
+// read as zeros, so garbage (even NaN) in unused cache slots never reaches P.V.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+// base and bytes are wave uniform: readfirstlane lets the compiler keep the
+// resource in SGPRs (otherwise it emits a per-lane "waterfall" loop).
+XV_INLINE __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t* base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* q = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// V LDS layout of one page (4 KB): chunk c = 4s+g of token t at s*1024 + g*256 + t*16.
+XV_INLINE void issue_page(PageRegs& r, char* vbuf, const DecodeArgs& a, int page, int kvh, int valid_rows,
+                          int lane_off) {
+  const int64_t base = (int64_t)page * a.page_stride + (int64_t)kvh * a.head_stride;
+  const uint32_t bytes = (uint32_t)(((int64_t)(valid_rows - 1) * a.tok_stride + kD) * 2);
+  const __amdgpu_buffer_rsrc_t rk = page_rsrc(a.kc + base, bytes);
+  const __amdgpu_buffer_rsrc_t rv = page_rsrc(a.vc + base, bytes);
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.k[s] = load_vec8(kp + 32 * s);
+  for (int s = 0; s < 4; ++s) {
+    u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off + 64 * s, 0, 0);
+    r.k[s].w[0] = v[0]; r.k[s].w[1] = v[1]; r.k[s].w[2] = v[2]; r.k[s].w[3] = v[3];
+  }
 #pragma unroll
-  for (int s = 0; s < 4; ++s) r.v[s] = load_vec8(vp + 32 * s);
+  for (int s = 0; s < 4; ++s)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vbuf + 1024 * s), 16, lane_off + 64 * s, 0, 0, 0);
 }
 
 XV_INLINE bf16x8_t as_bf16x8(const Vec8& v) {
@@ -70,18 +111,9 @@ struct SplitState {
 };
 
 template <int G>
-XV_INLINE void process_page(SplitState& st, PageRegs& r, char* lds, const bf16x8_t (&qb)[4], int page_tok0,
-                            int ctx, bool last, float scale_log2, int lane) {
+XV_INLINE void process_page(SplitState& st, const PageRegs& r, const char* vbuf, const bf16x8_t (&qb)[4],
+                            int page_tok0, int ctx, float scale_log2, int lane) {
   const int i = lane & 15, g = lane >> 4;
-  // ---- V -> LDS (zero rows past the sequence end: they may hold NaN) ----
-  if (last && page_tok0 + i >= ctx) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) r.v[s].w[0] = r.v[s].w[1] = r.v[s].w[2] = r.v[s].w[3] = 0u;
-  }
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    *reinterpret_cast<uint4*>(lds + i * kLdsRow + 16 * (4 * s + g)) =
-        make_uint4(r.v[s].w[0], r.v[s].w[1], r.v[s].w[2], r.v[s].w[3]);
   // ---- S^T = K Q^T ----
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -111,56 +143,44 @@ XV_INLINE void process_page(SplitState& st, PageRegs& r, char* lds, const bf16x8
 #pragma unroll
     for (int n = 0; n < 8; ++n) st.o[n][rr] *= ar;
   }
-  // No barrier: the workgroup is one wave and a wave's LDS operations complete
-  // in order, so the transposed reads below see the rows just written (the
-  // compiler keeps the order: both access the same __shared__ array).  A
-  // __syncthreads here would also wait for the prefetched page.
-  // ---- O += P V, V^T tiles read transposed from LDS ----
-  const int rowt = 4 * g + (i >> 2);
-  const char* vb = lds + rowt * kLdsRow + 8 * (i & 3);
+  // ---- O += P V, V^T tiles read transposed from the page's LDS copy ----
+  // tile n = d 16n..16n+15 = chunks 2n, 2n+1; lane (g, i) supplies token
+  // 4g + i/4, columns 16n + 4(i%4) .. +3
+  const char* vb = vbuf + ((i & 3) >> 1) * 256 + (4 * g + (i >> 2)) * 16 + 8 * (i & 1);
+  // The page's V arrived by LDS-DMA; the 8 VMEM operations of each of the
+  // kNbuf-1 pages issued after it may still be in flight: vmcnt(8*(kNbuf-1))
+  // waits exactly for this page.  The reads are one asm block so that the compiler, which
+  // cannot tell the two LDS buffers apart, does not wait for everything.
+  short4_t vt[8];
+  const uint32_t va = (uint32_t)reinterpret_cast<uintptr_t>(vb);
+  __asm__ __volatile__(
+      "s_waitcnt vmcnt(%9)\n\t"
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %8 offset:512\n\t"
+      "ds_read_b64_tr_b16 %2, %8 offset:1024\n\t"
+      "ds_read_b64_tr_b16 %3, %8 offset:1536\n\t"
+      "ds_read_b64_tr_b16 %4, %8 offset:2048\n\t"
+      "ds_read_b64_tr_b16 %5, %8 offset:2560\n\t"
+      "ds_read_b64_tr_b16 %6, %8 offset:3072\n\t"
+      "ds_read_b64_tr_b16 %7, %8 offset:3584\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]), "=&v"(vt[3]), "=&v"(vt[4]), "=&v"(vt[5]), "=&v"(vt[6]), "=&v"(vt[7])
+      : "v"(va), "n"(8 * (kNbuf - 1))
+      : "memory");
 #pragma unroll
-  for (int n = 0; n < 8; ++n) {
-    short4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + 32 * n));
-    st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt, st.o[n], 0, 0, 0);
-  }
+  for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
 }
 
-template <int G, int NBUF, int WPB>
-__global__ __launch_bounds__(64 * WPB) void paged_decode_kernel(DecodeArgs a, int units) {
-  __shared__ __attribute__((aligned(16))) char lds_all[WPB][kPage * kLdsRow];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  char* lds = lds_all[wave];
+// Attention of one (sequence b, kv head) over pages [pb, pe) of the sequence.
+// full: the range holds the whole sequence -> final bf16 output; otherwise the
+// normalised partial and its log2-sum-exp go to partial slot `part`.
+template <int G>
+XV_INLINE void decode_segment(const DecodeArgs& a, int b, int kvh, int pb, int pe, bool full, int part, char* lds,
+                              int lane) {
   const int i = lane & 15, g = lane >> 4;
-  // unit = split * (B*Hkv) + (b*Hkv + kvh): the waves of a workgroup are
-  // independent units (no intra-workgroup synchronisation anywhere)
-  const int unit = blockIdx.x * WPB + wave;
-  if (unit >= units) return;
-  const int bh_count = units / a.max_splits;
-  const int split = unit / bh_count;
-  const int bh = unit - split * bh_count;
-  const int b = bh / a.hkv;
-  const int kvh = bh - b * a.hkv;
   const int head0 = kvh * G;
   const int ctx = a.seqlens[b];
   const int npages = (ctx + kPage - 1) / kPage;
-  const int nsplit = (npages + a.pps - 1) / a.pps;
-
-  if (ctx <= 0) {
-    // padding row: defined zero output, written once by split 0
-    if (split == 0) {
-      for (int e = lane; e < G * kD / 2; e += 64)
-        reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)head0 * kD)[e] = 0u;
-    }
-    return;
-  }
-  if (split >= nsplit) return;
-  const int p0 = split * a.pps;
-  const int np = min(a.pps, npages - p0);
-
-  // page ids of this split, one per lane, broadcast with readlane
-  int pid = 0;
-  if (lane < np) pid = a.bt[(int64_t)b * a.bt_stride + p0 + lane];
 
   bf16x8_t qb[4];
   {
@@ -168,26 +188,38 @@ __global__ __launch_bounds__(64 * WPB) void paged_decode_kernel(DecodeArgs a, in
 #pragma unroll
     for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(load_vec8(qp + 32 * s));
   }
-
   SplitState st;
   st.m = -INFINITY;
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  // NBUF page buffers: NBUF-1 pages always in flight ahead of the one being
-  // processed.  Prefetches are issued unconditionally (clamped to the split's
-  // last page) so the outstanding-load count is the same on every path and
-  // the compiler's vmcnt waits stay partial.
-  PageRegs r[NBUF];
+  const int lane_off = (int)((int64_t)i * a.tok_stride * 2 + 16 * g);
+  for (int c0 = pb; c0 < pe; c0 += 64) {
+    const int np = min(64, pe - c0);
+    // page ids of this chunk, one per lane, broadcast with readlane
+    int pid = 0;
+    if (lane < np) pid = a.bt[(int64_t)b * a.bt_stride + c0 + lane];
+    // kNbuf page buffers (K in VGPRs, V in LDS): kNbuf-1 pages are always in
+    // flight ahead of the one being processed.  Prefetches are issued
+    // unconditionally (clamped to the chunk's last page) so the number of VMEM
+    // operations after any page is fixed, which the LDS wait in process_page
+    // relies on.
+    PageRegs r[kNbuf];
+    auto rows = [&](int pg) { return min(kPage, ctx - pg * kPage); };
 #pragma unroll
-  for (int k = 0; k < NBUF - 1; ++k) load_page(r[k], a, __builtin_amdgcn_readlane(pid, min(k, np - 1)), kvh, i, g);
-  for (int it = 0; it < np; it += NBUF) {
+    for (int k = 0; k < kNbuf - 1; ++k) {
+      const int nk = min(k, np - 1);
+      issue_page(r[k], lds + k * kVPageBytes, a, __builtin_amdgcn_readlane(pid, nk), kvh, rows(c0 + nk), lane_off);
+    }
+    for (int it = 0; it < np; it += kNbuf) {
 #pragma unroll
-    for (int u = 0; u < NBUF; ++u) {
-      load_page(r[(u + NBUF - 1) % NBUF], a, __builtin_amdgcn_readlane(pid, min(it + u + NBUF - 1, np - 1)), kvh, i, g);
-      if (it + u < np)
-        process_page<G>(st, r[u], lds, qb, (p0 + it + u) * kPage, ctx, p0 + it + u == npages - 1, a.scale_log2, lane);
+      for (int u = 0; u < kNbuf; ++u) {
+        const int ahead = (u + kNbuf - 1) % kNbuf;
+        const int na = min(it + u + kNbuf - 1, np - 1);
+        issue_page(r[ahead], lds + ahead * kVPageBytes, a, __builtin_amdgcn_readlane(pid, na), kvh, rows(c0 + na), lane_off);
+        if (it + u < np) process_page<G>(st, r[u], lds + u * kVPageBytes, qb, (c0 + it + u) * kPage, ctx, a.scale_log2, lane);
+      }
     }
   }
 
@@ -205,12 +237,12 @@ __global__ __launch_bounds__(64 * WPB) void paged_decode_kernel(DecodeArgs a, in
     if (row >= G) continue;
     const float inv = 1.0f / lh;
     const int head = head0 + row;
-    if (nsplit == 1) {
+    if (full) {
       bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
 #pragma unroll
       for (int n = 0; n < 8; ++n) o[16 * n] = (bf16_t)f32_to_bf16(st.o[n][rr] * inv);
     } else {
-      const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_splits + split;
+      const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_parts + part;
       float* o = a.ws_o + wrow * kD + i;
 #pragma unroll
       for (int n = 0; n < 8; ++n) o[16 * n] = st.o[n][rr] * inv;
@@ -219,68 +251,141 @@ __global__ __launch_bounds__(64 * WPB) void paged_decode_kernel(DecodeArgs a, in
   }
 }
 
-// Merge the split partials of one (sequence, query head): 64 lanes x 2 dims.
-__global__ __launch_bounds__(64) void merge_splits_kernel(DecodeArgs a) {
+constexpr int kMaxBatch = 256;  // sequences per launch (larger batches are launched in chunks)
+
+#ifndef XV_DECODE_WPE
+#define XV_DECODE_WPE 1  // waves per SIMD the register budget is fitted to
+#endif
+
+// Pages per wave range: identical in both kernels.
+XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
+  const int64_t per = (total + a.nwaves - 1) / a.nwaves;
+  return (int)max((int64_t)a.lmin, per);
+}
+
+template <int G>
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WPE, XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[kNbuf * kVPageBytes];
+  __shared__ int pref[kMaxBatch + 1];  // pages of sequences 0..b-1
+  const int lane = threadIdx.x;
+  // prefix sums of the page counts (every wave computes them; B <= 1024)
+  int carry = 0;
+  for (int c = 0; c < a.batch; c += 64) {
+    const int b = c + lane;
+    const int np = b < a.batch ? (max(a.seqlens[b], 0) + kPage - 1) / kPage : 0;
+    int inc = np;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o);
+      if (lane >= o) inc += y;
+    }
+    if (b < a.batch) pref[b + 1] = carry + inc;
+    carry += __shfl(inc, 63);
+  }
+  if (lane == 0) pref[0] = 0;
+  __syncthreads();  // single wave: orders the LDS prefix writes before the reads
+  const int64_t total = (int64_t)a.hkv * carry;
+  const int L = range_pages(a, total);
+  int64_t f = (int64_t)blockIdx.x * L;
+  const int64_t f1 = min(f + L, total);
+  while (f < f1) {
+    // sequence b holding flat page f: largest b with hkv*pref[b] <= f
+    int lo = 0, hi = a.batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if ((int64_t)a.hkv * pref[mid] <= f) lo = mid; else hi = mid - 1;
+    }
+    const int b = lo;
+    const int npb = pref[b + 1] - pref[b];
+    const int64_t base = (int64_t)a.hkv * pref[b];
+    const int kvh = (int)((f - base) / npb);
+    const int64_t seg0 = base + (int64_t)kvh * npb;
+    const int64_t seg1 = seg0 + npb;
+    const int64_t e = min(f1, seg1);
+    const bool full = (f == seg0) && (e == seg1);
+    const int part = (int)(blockIdx.x - seg0 / L);
+    decode_segment<G>(a, b, kvh, (int)(f - seg0), (int)(e - seg0), full, part, lds, lane);
+    f = e;
+  }
+}
+
+// Merge the partials of one (sequence, query head): 64 lanes x 2 dims.  Also
+// writes the zero output of padding rows (cache_seqlens 0).
+__global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int b = blockIdx.x / a.hq;
   const int h = blockIdx.x - b * a.hq;
-  const int ctx = a.seqlens[b];
-  const int npages = (ctx + kPage - 1) / kPage;
-  const int nsplit = (npages + a.pps - 1) / a.pps;
-  if (nsplit <= 1) return;
-  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_splits;
+  const int lane = threadIdx.x;
+  int before = 0, total = 0;
+  for (int c = lane; c < a.batch; c += 64) {
+    const int np = (max(a.seqlens[c], 0) + kPage - 1) / kPage;
+    total += np;
+    if (c < b) before += np;
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    before += __shfl_xor(before, o);
+    total += __shfl_xor(total, o);
+  }
+  const int npb = (max(a.seqlens[b], 0) + kPage - 1) / kPage;
+  const int d = lane * 2;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)h * kD + d);
+  if (npb == 0) {
+    *dst = 0u;
+    return;
+  }
+  const int L = range_pages(a, (int64_t)a.hkv * total);
+  const int64_t seg0 = (int64_t)a.hkv * before + (int64_t)(h / a.group) * npb;
+  const int n = (int)((seg0 + npb - 1) / L - seg0 / L) + 1;
+  if (n <= 1) return;
+  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
   float mx = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, a.ws_lse[row0 + s]);
+  for (int s = 0; s < n; ++s) mx = fmaxf(mx, a.ws_lse[row0 + s]);
   float den = 0.f, o0 = 0.f, o1 = 0.f;
-  const int d = threadIdx.x * 2;
-  for (int s = 0; s < nsplit; ++s) {
-    float w = __builtin_amdgcn_exp2f(a.ws_lse[row0 + s] - mx);
-    float2 v = *reinterpret_cast<const float2*>(a.ws_o + (row0 + s) * kD + d);
+  for (int s = 0; s < n; ++s) {
+    const float w = __builtin_amdgcn_exp2f(a.ws_lse[row0 + s] - mx);
+    const float2 v = *reinterpret_cast<const float2*>(a.ws_o + (row0 + s) * kD + d);
     den += w;
     o0 += w * v.x;
     o1 += w * v.y;
   }
   const float inv = 1.0f / den;
-  *reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)h * kD + d) = pack_bf16x2(o0 * inv, o1 * inv);
+  *dst = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
-int pages_per_split() {
-  static int pps = [] {
-    const char* e = getenv("XV_DECODE_PAGES_PER_SPLIT");
-    int v = e ? atoi(e) : 16;
-    if (v < 1) v = 1;
-    if (v > 64) v = 64;
-    return v;
-  }();
-  return pps;
-}
+// Minimum pages per wave range: bounds the partial count per (sequence, head).
+int min_range_pages(int max_blocks_per_seq) { return max(8, (max_blocks_per_seq + 31) / 32); }
 
-// Launch variants (page buffers x waves per workgroup); 0 is the default.
-int decode_variant() {
-  static int v = [] {
-    const char* e = getenv("XV_DECODE_VARIANT");
-    return e ? atoi(e) : 0;
-  }();
-  return v;
-}
-
-template <int G>
-void launch_group(const DecodeArgs& a, int units, int variant, hipStream_t stream) {
-  switch (variant) {
-    case 1: paged_decode_kernel<G, 2, 1><<<units, 64, 0, stream>>>(a, units); break;
-    case 2: paged_decode_kernel<G, 3, 1><<<units, 64, 0, stream>>>(a, units); break;
-    case 3: paged_decode_kernel<G, 2, 4><<<(units + 3) / 4, 256, 0, stream>>>(a, units); break;
-    default: paged_decode_kernel<G, 3, 4><<<(units + 3) / 4, 256, 0, stream>>>(a, units); break;
+int waves_for(int group) {
+  // resident single-wave workgroups: CUs x per-CU occupancy (queried once per device)
+  static int cached[4] = {0, 0, 0, 0};
+  const int slot = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3;
+  if (cached[slot]) return cached[slot];
+  int dev = 0, cus = 0, per_cu = 0;
+  hipGetDevice(&dev);
+  hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  switch (group) {
+    case 1: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<1>, 64, 0); break;
+    case 2: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<2>, 64, 0); break;
+    case 4: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<4>, 64, 0); break;
+    default: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<8>, 64, 0); break;
   }
+#if XV_DECODE_WAVES_PER_CU > 0
+  per_cu = min(per_cu, XV_DECODE_WAVES_PER_CU);
+#endif
+  cached[slot] = max(1, cus) * max(1, per_cu);
+  return cached[slot];
 }
 
 }  // namespace
 
+// Workspace layout: [256 B reserved][partial outputs fp32][partial log2-sum-exp fp32]
+size_t counter_bytes(int, int) { return 256; }
+
 extern "C" size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int max_blocks_per_seq, int block_size, int head_dim) {
-  (void)num_kv_heads; (void)block_size;
-  if (batch <= 0 || max_blocks_per_seq <= 0) return 0;
-  const int ms = (max_blocks_per_seq + pages_per_split() - 1) / pages_per_split();
-  return (size_t)batch * num_q_heads * ms * ((size_t)head_dim + 1) * sizeof(float);
+  (void)block_size;
+  if (batch <= 0 || max_blocks_per_seq <= 0 || num_kv_heads <= 0) return 256;
+  const int parts = (max_blocks_per_seq + min_range_pages(max_blocks_per_seq) - 1) / min_range_pages(max_blocks_per_seq) + 1;
+  return counter_bytes(batch, num_kv_heads) + (size_t)batch * num_q_heads * parts * ((size_t)head_dim + 1) * sizeof(float);
 }
 
 extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -299,33 +404,33 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   const int group = num_q_heads / num_kv_heads;
   if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
-  const int pps = pages_per_split();
-  const int max_splits = (max_blocks_per_seq + pps - 1) / pps;
+  if (batch > kMaxBatch) return (int)hipErrorInvalidValue;
   const size_t need = xv_paged_decode_workspace_size(batch, num_q_heads, num_kv_heads, max_blocks_per_seq,
                                                      block_size, head_dim);
-  if (max_splits > 1 && (workspace == nullptr || workspace_bytes < need)) return (int)hipErrorInvalidValue;
+  if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
   DecodeArgs a;
   a.q = (const bf16_t*)q; a.q_st = q_stride_tok; a.q_sh = q_stride_head;
   a.kc = (const bf16_t*)k_cache; a.vc = (const bf16_t*)v_cache;
   a.page_stride = page_stride; a.tok_stride = tok_stride; a.head_stride = head_stride;
   a.bt = block_tables; a.bt_stride = bt_stride; a.seqlens = cache_seqlens;
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
-  a.ws_o = (float*)workspace;
-  a.ws_lse = a.ws_o ? a.ws_o + (size_t)batch * num_q_heads * max_splits * kD : nullptr;
-  a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.pps = pps; a.max_splits = max_splits;
+  const int lmin = min_range_pages(max_blocks_per_seq);
+  a.max_parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
+  a.ws_o = (float*)((char*)workspace + counter_bytes(batch, num_kv_heads));
+  a.ws_lse = a.ws_o + (size_t)batch * num_q_heads * a.max_parts * kD;
+  a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin;
+  // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
+  const int64_t max_total = (int64_t)batch * num_kv_heads * max_blocks_per_seq;
+  a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
-  const int units = batch * num_kv_heads * max_splits;
-  const int variant = decode_variant();
   switch (group) {
-    case 1: launch_group<1>(a, units, variant, stream); break;
-    case 2: launch_group<2>(a, units, variant, stream); break;
-    case 4: launch_group<4>(a, units, variant, stream); break;
-    default: launch_group<8>(a, units, variant, stream); break;
+    case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;
+    case 2: paged_decode_kernel<2><<<a.nwaves, 64, 0, stream>>>(a); break;
+    case 4: paged_decode_kernel<4><<<a.nwaves, 64, 0, stream>>>(a); break;
+    default: paged_decode_kernel<8><<<a.nwaves, 64, 0, stream>>>(a); break;
   }
   XV_CHECK_LAUNCH();
-  if (max_splits > 1) {
-    merge_splits_kernel<<<dim3((unsigned)(batch * num_q_heads)), 64, 0, stream>>>(a);
-    XV_CHECK_LAUNCH();
-  }
+  merge_parts_kernel<<<dim3((unsigned)(batch * num_q_heads)), 64, 0, stream>>>(a);
+  XV_CHECK_LAUNCH();
   return 0;
 }

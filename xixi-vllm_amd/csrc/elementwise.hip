@@ -4,7 +4,7 @@
 // accumulate in fp32 and reduce across lanes with DPP, so each element is
 // read once from HBM and written once.
 #include "xv_common.h"
-#include "../../include/xv_kernels.h"
+#include "xv_kernels.h"
 
 // --------------------------------------------------------------------------
 // KV store: one thread moves one 16-byte chunk of K and the matching chunk of V.

@@ -15,7 +15,7 @@
 // (query i of q_len sees keys j <= k_len - q_len + i); fully masked tiles are
 // skipped.  Keys come from dense rows or through the paged block table.
 #include "xv_common.h"
-#include "../../include/xv_kernels.h"
+#include "xv_kernels.h"
 #include <math.h>
 
 namespace {

@@ -15,7 +15,7 @@
 // exp2 is a fixed Taylor polynomial with explicit FMAs so that the masses,
 // hence the token ids, are bit-identical to the C restatement of the oracle.
 #include "xv_common.h"
-#include "../../include/xv_kernels.h"
+#include "xv_kernels.h"
 #include <math.h>
 
 #pragma clang fp contract(off)
