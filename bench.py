@@ -84,6 +84,133 @@ def time_decode(torch, cases, steps: int, warmup: int):
     return e0.elapsed_time(e1) / steps, wall
 
 
+def _time(torch, fn, iters=50, warmup=5):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters * 1e3  # us
+
+
+def kernel_suite(torch, dev) -> dict:
+    """Config 3 (fused elementwise/reduction set at Qwen3-8B width over 8192
+    tokens) and the sampler, each against its algorithmic HBM bytes."""
+    import xvllm.layers.ops  # noqa: F401
+    from xvllm.kv_ops import store_kvcache
+    from xvllm.layers.rotary import build_cos_sin_cache
+    from xvllm.sampler import sample
+
+    g = torch.Generator(device=dev).manual_seed(3)
+    T, H, HQ_, HKV_, D_, I = 8192, 4096, 32, 8, 128, 12288
+    rnd = lambda *shape: torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+    out = {}
+
+    def rec(name, us, nbytes):
+        out[name] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+
+    x, r = rnd(T, H), rnd(T, H)
+    w = (torch.randn(H, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    rec("fused_add_rmsnorm_T8192_H4096", _time(torch, lambda: torch.ops.vllm.fused_add_rmsnorm(x, r, w, 1e-6)),
+        T * H * 2 * 4 + H * 2)
+    del x, r
+    qkv = rnd(T, (HQ_ + 2 * HKV_) * D_)
+    q = qkv[:, : HQ_ * D_].view(T, HQ_, D_)
+    k = qkv[:, HQ_ * D_ : (HQ_ + HKV_) * D_].view(T, HKV_, D_)
+    qw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    kw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
+    pos = torch.randint(0, 32768, (T,), generator=g, device=dev)
+    cs = build_cos_sin_cache(D_, 32768, 1e6).to(dev)
+    rec("qk_norm_rope_T8192_32q8kv", _time(torch, lambda: torch.ops.xv.qk_norm_rope(q, k, qw, kw, 1e-6, pos, cs)),
+        T * (HQ_ + HKV_) * D_ * 2 * 2 + 8 * T + T * D_ * 4)
+    x = rnd(T, 2 * I)
+    rec("silu_and_mul_T8192_I12288", _time(torch, lambda: torch.ops.vllm.silu_and_mul(x)), T * 3 * I * 2)
+    del x
+    kk, vv = rnd(T, HKV_, D_), rnd(T, HKV_, D_)
+    nb = 1024
+    kc = torch.zeros((nb, PAGE, HKV_, D_), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(nb * PAGE, generator=g, device=dev)[:T].to(torch.int32)
+    rec("store_kvcache_T8192", _time(torch, lambda: store_kvcache(kk, vv, kc.view(-1, HKV_, D_), vc.view(-1, HKV_, D_), slots)),
+        2 * T * HKV_ * D_ * 2 * 2 + 4 * T)
+    del kc, vc
+    V = 151936
+    for bsz in (64, 256):
+        logits = rnd(bsz, V)
+        temps = torch.full((bsz,), 0.7, device=dev)
+        tps = torch.full((bsz,), 0.9, device=dev)
+        tks = torch.full((bsz,), 50, dtype=torch.int32, device=dev)
+        u = torch.rand(bsz, generator=g, device=dev)
+        rec(f"sampler_greedy_B{bsz}", _time(torch, lambda: sample(logits, temps, all_greedy=True), 20), bsz * V * 2)
+        rec(f"sampler_k50_p0.9_B{bsz}", _time(torch, lambda: sample(logits, temps, tps, tks, None, u, use_top_k=True,
+                                                                    use_top_p=True), 20), bsz * V * 2)
+    return out
+
+
+def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = False) -> dict:
+    """Qwen3-8B (36 layers, random bf16 weights ~N(0,0.02)) decode step at the
+    given per-sequence contexts: hipGraph replay of the decode body + LM head +
+    sampler, steady state (metadata staged once)."""
+    from xvllm.batch import SeqSchedule
+    from xvllm.config import QWEN3_8B
+    from xvllm.kv_pool import KVPool
+    from xvllm.model_runner import ModelRunner
+    from xvllm.models import Qwen3ForCausalLM
+
+    cfg = QWEN3_8B
+    bsz = len(ctx)
+    need = [(c + PAGE - 1) // PAGE for c in ctx]
+    pool = math.ceil(1.25 * sum(need))
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+            kv = KVPool(cfg, num_blocks=pool, block_size=PAGE, device=dev, dtype=torch.bfloat16)
+    finally:
+        torch.set_default_dtype(torch.float32)
+    kv.kv_cache.normal_()
+    max_ctx = max(ctx) + 1
+    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=max_ctx, device=dev)
+    g = torch.Generator().manual_seed(11)
+    perm = torch.randperm(pool, generator=g).tolist()
+    seqs, o = [], 0
+    for i, c in enumerate(ctx):
+        seqs.append(SeqSchedule(seq_id=i, token_ids=[int(torch.randint(0, cfg.vocab_size, (1,), generator=g))],
+                                num_cached_tokens=c - 1, block_table=perm[o : o + need[i]],
+                                temperature=0.7 if sampled else 0.0, top_p=0.9 if sampled else None,
+                                top_k=50 if sampled else None))
+        o += need[i]
+    runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
+
+    def step():
+        return runner._sample_logits(runner.decode_hidden(bsz), bsz)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ids = step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
+    kvbytes = sum(ctx) * cfg.num_hidden_layers * cfg.num_key_value_heads * 128 * 2 * 2
+    roof_ms = (wbytes + kvbytes) / (HBM_PEAK_GBS * 1e9) * 1e3
+    runner.destroy()
+    assert ids.shape[0] == bsz
+    return {"batch": bsz, "mean_ctx": round(sum(ctx) / bsz, 1), "sampling": "T0.7/k50/p0.9" if sampled else "greedy",
+            "ms_per_step": round(ms, 4), "tok_per_s": round(bsz / (ms * 1e-3), 1),
+            "roofline_ms": round(roof_ms, 4), "roofline_tok_per_s": round(bsz / (roof_ms * 1e-3), 1),
+            "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}
+
+
 def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
     """numpy oracle on host cores, one BLAS thread, over a prefix of the
     config-2 batch until the time budget is used (at least one sequence)."""
@@ -125,6 +252,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-suite", action="store_true", help="skip the config-3 kernel set and the sampler")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B decode tok/s measurement")
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -187,6 +316,13 @@ def main() -> int:
         "sweep": sweep,
         "wall_s_timed_region": round(wall, 4),
     }
+    if not args.no_suite:
+        line["kernels"] = kernel_suite(torch, dev)
+    if not args.no_e2e:
+        del cases
+        torch.cuda.empty_cache()
+        line["decode_e2e"] = decode_e2e(torch, dev, ctx)
+        line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctx)
     print(json.dumps(line))

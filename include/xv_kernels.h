@@ -34,15 +34,17 @@ int xv_abi_version(void);
  *   k_cache[slot[i], h, :] = key[i, h, :];  v_cache[slot[i], h, :] = value[i, h, :]
  *   for every i in [0, num_tokens) with slot[i] >= 0 (slot -1 is skipped, kv_ops.py:22-23).
  * key/value rows: element (i, h, d) at i*key_stride_tok + h*key_stride_head + d.
- * cache element (slot, h, d) at slot*cache_stride_slot + h*cache_stride_head + d
- * (for the pool layout [NB, BS, Hkv, D]: slot = page*BS + offset).
- * head_dim must be a multiple of 8 and all row starts 16-byte aligned.
+ * cache element of slot s = page*block_size + t, head h, dim d at
+ * page*cache_page_stride + t*cache_tok_stride + h*cache_head_stride + d
+ * (the reference pool [NB, BS, Hkv, D]; block_size 1 describes a flat
+ * [num_slots, Hkv, D] view).  head_dim must be a multiple of 8 and all row
+ * starts 16-byte aligned.
  */
 int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
                      const void* value, int64_t value_stride_tok, int64_t value_stride_head,
                      void* k_cache, void* v_cache,
-                     int64_t cache_stride_slot, int64_t cache_stride_head,
-                     const int32_t* slot_mapping, int64_t num_tokens,
+                     int64_t cache_page_stride, int64_t cache_tok_stride, int64_t cache_head_stride,
+                     int block_size, const int32_t* slot_mapping, int64_t num_tokens,
                      int num_kv_heads, int head_dim, hipStream_t stream);
 
 /*

@@ -13,7 +13,7 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
     const bf16_t* __restrict__ key, int64_t ks_tok, int64_t ks_head,
     const bf16_t* __restrict__ value, int64_t vs_tok, int64_t vs_head,
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
-    int64_t cs_slot, int64_t cs_head, const int32_t* __restrict__ slots,
+    int64_t cs_page, int64_t cs_tok, int64_t cs_head, int block_size, const int32_t* __restrict__ slots,
     int64_t total_chunks, int chunks_per_tok, int chunks_per_head) {
   int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total_chunks) return;
@@ -25,7 +25,9 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
   int d = (c - h * chunks_per_head) * 8;
   Vec8 kv = load_vec8_nt(key + tok * ks_tok + h * ks_head + d);
   Vec8 vv = load_vec8_nt(value + tok * vs_tok + h * vs_head + d);
-  int64_t dst = (int64_t)slot * cs_slot + h * cs_head + d;
+  const int page = slot / block_size;
+  const int t = slot - page * block_size;
+  int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
   store_vec8(k_cache + dst, kv);
   store_vec8(v_cache + dst, vv);
 }
@@ -33,10 +35,11 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
 extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
                                 const void* value, int64_t value_stride_tok, int64_t value_stride_head,
                                 void* k_cache, void* v_cache,
-                                int64_t cache_stride_slot, int64_t cache_stride_head,
-                                const int32_t* slot_mapping, int64_t num_tokens,
+                                int64_t cache_page_stride, int64_t cache_tok_stride, int64_t cache_head_stride,
+                                int block_size, const int32_t* slot_mapping, int64_t num_tokens,
                                 int num_kv_heads, int head_dim, hipStream_t stream) {
-  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8) return (int)hipErrorInvalidValue;
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || block_size <= 0)
+    return (int)hipErrorInvalidValue;
   if (num_tokens == 0) return 0;
   int cph = head_dim / 8;
   int cpt = cph * num_kv_heads;
@@ -44,8 +47,8 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
   int64_t blocks = (total + 255) / 256;
   store_kvcache_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(
       (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok,
-      value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_stride_slot, cache_stride_head,
-      slot_mapping, total, cpt, cph);
+      value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_page_stride, cache_tok_stride,
+      cache_head_stride, block_size, slot_mapping, total, cpt, cph);
   XV_CHECK_LAUNCH();
   return 0;
 }

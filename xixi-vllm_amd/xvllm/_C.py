@@ -16,7 +16,7 @@ i32, i64, f32, vp, sz = C.c_int, C.c_int64, C.c_float, C.c_void_p, C.c_size_t
 SIGNATURES: dict[str, tuple] = {
     "xv_error_string": (C.c_char_p, [i32]),
     "xv_abi_version": (i32, []),
-    "xv_store_kvcache": (i32, [vp, i64, i64, vp, i64, i64, vp, vp, i64, i64, vp, i64, i32, i32, vp]),
+    "xv_store_kvcache": (i32, [vp, i64, i64, vp, i64, i64, vp, vp, i64, i64, i64, i32, vp, i64, i32, i32, vp]),
     "xv_paged_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "xv_paged_decode_attention": (
         i32,

@@ -1,0 +1,178 @@
+"""Static device buffers and their pinned host mirrors for one engine step
+(reference src/compute/batch.py:37-251): decode / prefill metadata, block
+tables and sampling parameters, staged on the host with numpy and copied
+H2D without blocking, so that graph replays read them in place.
+
+Decode metadata per sequence (batch.py:119-124): input id = last token,
+position = num_cached_tokens, slot = bt[pos // BS] * BS + pos % BS,
+cache_seqlens = pos + 1.  Rows padded up to a graph bucket get slot -1,
+seqlen 0 and block table -1 (batch.py:133-136).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+
+@dataclass
+class SeqSchedule:
+    """What the model runner needs of one scheduled sequence (the fields of the
+    reference's wire record, src/data/batch.py:81-98)."""
+    seq_id: int
+    token_ids: list[int]            # decode: [last token]; prefill: this chunk's tokens
+    num_cached_tokens: int
+    block_table: list[int]
+    temperature: float = 0.0
+    top_p: float | None = None
+    top_k: int | None = None
+    min_p: float | None = None
+    need_sample: bool = True
+
+
+def slots_for_range(block_table, start: int, end: int, block_size: int) -> np.ndarray:
+    """Physical slot of every token position in [start, end) (sequence.py:26-51)."""
+    p = np.arange(start, end, dtype=np.int64)
+    bt = np.asarray(block_table, dtype=np.int64)
+    return (bt[p // block_size] * block_size + p % block_size).astype(np.int32)
+
+
+def _pinned(shape, dtype, fill=None):
+    t = torch.empty(shape, dtype=dtype, pin_memory=True)
+    if fill is not None:
+        t.fill_(fill)
+    return t
+
+
+class Batch:
+    def __init__(self, *, max_bs: int, max_tokens: int, max_blocks: int, vocab_size: int,
+                 device: torch.device, block_size: int) -> None:
+        self.max_bs, self.max_tokens, self.max_blocks = max_bs, max_tokens, max_blocks
+        self.vocab_size, self.device, self.block_size = vocab_size, device, block_size
+        gpu = lambda shape, dt, fill=0: torch.full(shape, fill, dtype=dt, device=device)
+        self.input_ids = gpu((max_tokens,), torch.int64)
+        self.positions = gpu((max_tokens,), torch.int64)
+        self.slot_mapping = gpu((max_tokens,), torch.int32, -1)
+        self.cache_seqlens = gpu((max_bs,), torch.int32)
+        self.cu_seqlens_q = gpu((max_bs + 1,), torch.int32)
+        self.cu_seqlens_k = gpu((max_bs + 1,), torch.int32)
+        self.block_tables = gpu((max_bs, max_blocks), torch.int32, -1)
+        self.temperatures = gpu((max_bs,), torch.float32)
+        self.top_ps = gpu((max_bs,), torch.float32)
+        self.top_ks = gpu((max_bs,), torch.int32)
+        self.min_ps = gpu((max_bs,), torch.float32)
+        self.all_greedy, self.any_greedy = True, False
+        self.use_top_k = self.use_top_p = self.use_min_p = False
+        self.max_top_k = 0
+        # pinned host staging
+        self._h_ids = _pinned((max_tokens,), torch.int64)
+        self._h_pos = _pinned((max_tokens,), torch.int64)
+        self._h_slot = _pinned((max_tokens,), torch.int32, -1)
+        self._h_csl = _pinned((max_bs,), torch.int32)
+        self._h_cuq = _pinned((max_bs + 1,), torch.int32)
+        self._h_cuk = _pinned((max_bs + 1,), torch.int32)
+        self._h_bt = _pinned((max_bs, max_blocks), torch.int32, -1)
+        self._h_samp = _pinned((4, max_bs), torch.float32)
+        self._h_topk = _pinned((max_bs,), torch.int32)
+        self._bt_np = self._h_bt.numpy()
+        self._row_len = np.full(max_bs, -1, dtype=np.int64)   # entries of each host row in sync
+        self._row_sid = np.full(max_bs, -1, dtype=np.int64)   # sequence that owns the row
+        self._samp_key = None
+
+    # ------------------------------------------------------------ block tables
+    def _sync_block_tables(self, seqs: list[SeqSchedule]) -> None:
+        """Bring host rows up to date (append-only growth writes one entry) and
+        copy the used rows H2D in one transfer (batch.py:181-215)."""
+        bt = self._bt_np
+        dirty = False
+        for i, s in enumerate(seqs):
+            k = len(s.block_table)
+            if self._row_sid[i] == s.seq_id and self._row_len[i] == k:
+                continue
+            if self._row_sid[i] == s.seq_id and self._row_len[i] == k - 1 and k > 0:
+                bt[i, k - 1] = s.block_table[-1]
+            else:
+                bt[i, :k] = s.block_table
+                bt[i, k:] = -1
+            self._row_sid[i], self._row_len[i] = s.seq_id, k
+            dirty = True
+        if dirty:
+            n = len(seqs)
+            self.block_tables[:n].copy_(self._h_bt[:n], non_blocking=True)
+
+    def _sync_sampling(self, seqs: list[SeqSchedule]) -> None:
+        key = tuple((s.seq_id, s.temperature, s.top_p, s.top_k, s.min_p) for s in seqs)
+        if key == self._samp_key:
+            return
+        self._samp_key = key
+        n = len(seqs)
+        v = self.vocab_size
+        t = np.array([s.temperature for s in seqs], np.float32)
+        p = np.array([1.0 if s.top_p is None else s.top_p for s in seqs], np.float32)
+        k = np.array([v if (s.top_k is None or s.top_k <= 0) else min(s.top_k, v) for s in seqs], np.int32)
+        m = np.array([0.0 if s.min_p is None else s.min_p for s in seqs], np.float32)
+        h = self._h_samp.numpy()
+        h[0, :n], h[1, :n], h[2, :n] = t, p, m
+        self._h_topk.numpy()[:n] = k
+        self.temperatures[:n].copy_(self._h_samp[0, :n], non_blocking=True)
+        self.top_ps[:n].copy_(self._h_samp[1, :n], non_blocking=True)
+        self.min_ps[:n].copy_(self._h_samp[2, :n], non_blocking=True)
+        self.top_ks[:n].copy_(self._h_topk[:n], non_blocking=True)
+        self.all_greedy = bool(np.all(t <= 1e-5))
+        self.any_greedy = bool(np.any(t <= 1e-5))
+        self.use_top_k = bool(np.any(k < v))
+        self.use_top_p = bool(np.any(p < 1.0))
+        self.use_min_p = bool(np.any(m > 0.0))
+        self.max_top_k = int(k.max()) if self.use_top_k else 0
+
+    # ------------------------------------------------------------ decode
+    def build_decode(self, seqs: list[SeqSchedule], *, pad_to: int | None = None) -> None:
+        n = len(seqs)
+        self._sync_block_tables(seqs)
+        pos = np.fromiter((s.num_cached_tokens for s in seqs), np.int64, n)
+        ids = np.fromiter((s.token_ids[-1] for s in seqs), np.int64, n)
+        rows = np.arange(n)
+        slot = self._bt_np[rows, pos // self.block_size].astype(np.int64) * self.block_size + pos % self.block_size
+        self._h_ids.numpy()[:n] = ids
+        self._h_pos.numpy()[:n] = pos
+        self._h_slot.numpy()[:n] = slot
+        self._h_csl.numpy()[:n] = pos + 1
+        self.input_ids[:n].copy_(self._h_ids[:n], non_blocking=True)
+        self.positions[:n].copy_(self._h_pos[:n], non_blocking=True)
+        self.slot_mapping[:n].copy_(self._h_slot[:n], non_blocking=True)
+        self.cache_seqlens[:n].copy_(self._h_csl[:n], non_blocking=True)
+        self._sync_sampling(seqs)
+        if pad_to is not None and pad_to > n:
+            self.slot_mapping[n:pad_to].fill_(-1)
+            self.cache_seqlens[n:pad_to].zero_()
+            self.block_tables[n:pad_to].fill_(-1)
+            self._row_sid[n:pad_to] = -1
+            self._row_len[n:pad_to] = -1
+
+    # ------------------------------------------------------------ prefill
+    def build_prefill(self, seqs: list[SeqSchedule]) -> tuple[int, int, int, bool]:
+        ids, pos, slot = self._h_ids.numpy(), self._h_pos.numpy(), self._h_slot.numpy()
+        cuq, cuk = self._h_cuq.numpy(), self._h_cuk.numpy()
+        cuq[0] = cuk[0] = 0
+        nt = max_q = max_k = 0
+        for i, s in enumerate(seqs):
+            start, n = s.num_cached_tokens, len(s.token_ids)
+            end = start + n
+            ids[nt : nt + n] = s.token_ids
+            pos[nt : nt + n] = np.arange(start, end)
+            slot[nt : nt + n] = slots_for_range(s.block_table, start, end, self.block_size)
+            cuq[i + 1], cuk[i + 1] = cuq[i] + n, cuk[i] + end
+            max_q, max_k = max(max_q, n), max(max_k, end)
+            nt += n
+        bs = len(seqs)
+        self.input_ids[:nt].copy_(self._h_ids[:nt], non_blocking=True)
+        self.positions[:nt].copy_(self._h_pos[:nt], non_blocking=True)
+        self.slot_mapping[:nt].copy_(self._h_slot[:nt], non_blocking=True)
+        self.cu_seqlens_q[: bs + 1].copy_(self._h_cuq[: bs + 1], non_blocking=True)
+        self.cu_seqlens_k[: bs + 1].copy_(self._h_cuk[: bs + 1], non_blocking=True)
+        has_cache = int(cuk[bs]) > int(cuq[bs])
+        if has_cache:
+            self._sync_block_tables(seqs)
+        self._sync_sampling(seqs)
+        return nt, max_q, max_k, has_cache

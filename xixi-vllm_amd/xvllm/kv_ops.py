@@ -18,8 +18,8 @@ def store_kvcache(
 
     key/value: [N, Hkv, D] (any row strides with a unit last stride; the
     reference makes them contiguous first, kv_ops.py:42-45 -- here the kernel
-    reads the strided view directly).  k_cache/v_cache: [num_slots, Hkv, D]
-    views of the pool (or [NB, BS, Hkv, D]).
+    reads the strided view directly).  k_cache/v_cache: paged [NB, BS, Hkv, D]
+    views of the pool (any strides, written in place) or flat [num_slots, Hkv, D].
     """
     require_cuda(key, value, k_cache, v_cache, slot_mapping)
     require_bf16(key, value, k_cache, v_cache)
@@ -28,16 +28,22 @@ def store_kvcache(
     for t in (key, value):
         if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or not aligned16(t):
             raise ValueError("key/value need a unit last stride and 16-byte aligned head rows")
-    kc = k_cache.reshape(-1, num_heads, head_dim)
-    vc = v_cache.reshape(-1, num_heads, head_dim)
-    if kc.stride() != vc.stride():
+    kc, vc = k_cache, v_cache
+    if kc.stride() != vc.stride() or kc.shape != vc.shape:
         raise ValueError("k_cache and v_cache must share one layout")
+    if kc.dim() == 4:  # [NB, BS, Hkv, D]
+        assert kc.shape[2] == num_heads and kc.shape[3] == head_dim
+        ps, ts, hs, bs = kc.stride(0), kc.stride(1), kc.stride(2), kc.shape[1]
+    else:  # [num_slots, Hkv, D]
+        kc = kc.view(-1, num_heads, head_dim)
+        vc = vc.view(-1, num_heads, head_dim)
+        ps, ts, hs, bs = kc.stride(0), 0, kc.stride(1), 1
     slots = slot_mapping if slot_mapping.dtype == torch.int32 else slot_mapping.to(torch.int32)
     slots = slots.contiguous()
     _C.check(
         _C.lib().xv_store_kvcache(
             ptr(key), key.stride(0), key.stride(1), ptr(value), value.stride(0), value.stride(1),
-            ptr(kc), ptr(vc), kc.stride(0), kc.stride(1), ptr(slots), n, num_heads, head_dim,
+            ptr(kc), ptr(vc), ps, ts, hs, bs, ptr(slots), n, num_heads, head_dim,
             stream_of(key),
         ),
         "xv_store_kvcache",

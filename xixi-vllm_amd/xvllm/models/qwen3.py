@@ -1,0 +1,126 @@
+"""Qwen3 dense decoder wired onto the xvllm operator API, one GPU (the
+reference's tp=1, pp=1 case of src/compute/models/qwen3.py:44-238).
+
+Per layer: input RMSNorm (fused with the residual add after layer 0), fused
+qkv GEMM, per-head q/k RMSNorm + NeoX RoPE (one kernel, `xv::qk_norm_rope`),
+`vllm::attention` (KV store + paged decode / prefill), o GEMM, fused add +
+RMSNorm, gate_up GEMM, SiLU-and-mul, down GEMM.  GEMMs stay on PyTorch
+(hipBLASLt).  Weights are plain tensors (random init for the benchmarks; the
+reference's checkpoint loader is out of scope).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ..config import head_dim as _head_dim
+from ..config import rope_theta as _rope_theta
+from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
+from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
+from ..sampler import sample
+
+
+class Qwen3MLP(nn.Module):
+    def __init__(self, hidden: int, inter: int):
+        super().__init__()
+        self.gate_up_proj = nn.Parameter(torch.empty(2 * inter, hidden))  # [gate; up] (linear.py:297-304)
+        self.down_proj = nn.Parameter(torch.empty(hidden, inter))
+
+    def forward(self, x):
+        return F.linear(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj)
+
+
+class Qwen3Attention(nn.Module):
+    def __init__(self, cfg, layer_id: int):
+        super().__init__()
+        self.num_heads = cfg.num_attention_heads
+        self.num_kv_heads = cfg.num_key_value_heads
+        self.head_dim = _head_dim(cfg)
+        self.q_size = self.num_heads * self.head_dim
+        self.kv_size = self.num_kv_heads * self.head_dim
+        self.qkv_proj = nn.Parameter(torch.empty(self.q_size + 2 * self.kv_size, cfg.hidden_size))
+        self.o_proj = nn.Parameter(torch.empty(cfg.hidden_size, self.q_size))
+        self.q_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
+        self.k_norm = RMSNorm(self.head_dim, cfg.rms_norm_eps)
+        self.rotary_emb = RotaryEmbedding(self.head_dim, self.head_dim, cfg.max_position_embeddings, _rope_theta(cfg))
+        self.attn = Attention(self.num_heads, self.head_dim, self.num_kv_heads, layer_id=layer_id)
+        self.eps = cfg.rms_norm_eps
+
+    def forward(self, positions, hidden, attn: AttnInputs):
+        qkv = F.linear(hidden, self.qkv_proj)
+        q, k, v = self._split_norm_rope(positions, qkv)
+        o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
+        return F.linear(o, self.o_proj)
+
+    def _split_norm_rope(self, positions, qkv):
+        """split -> per-head q/k RMSNorm -> RoPE (reference qwen3.py:117-128),
+        the two norms and the rotation as one kernel reading the qkv views."""
+        t = qkv.shape[0]
+        q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
+        k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
+        v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
+        q, k = torch.ops.xv.qk_norm_rope(
+            q, k, self.q_norm.weight, self.k_norm.weight, self.eps, positions, self.rotary_emb.cos_sin_cache
+        )
+        return q, k, v
+
+
+class Qwen3DecoderLayer(nn.Module):
+    def __init__(self, cfg, layer_id: int):
+        super().__init__()
+        self.self_attn = Qwen3Attention(cfg, layer_id)
+        self.mlp = Qwen3MLP(cfg.hidden_size, cfg.intermediate_size)
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+    def forward(self, positions, hidden, residual, attn: AttnInputs):
+        hidden, residual = self.input_layernorm(hidden, residual)
+        hidden = self.self_attn(positions, hidden, attn)
+        hidden, residual = self.post_attention_layernorm(hidden, residual)
+        return self.mlp(hidden), residual
+
+
+class Qwen3Model(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.embed_tokens = nn.Parameter(torch.empty(cfg.vocab_size, cfg.hidden_size))
+        self.layers = nn.ModuleList([Qwen3DecoderLayer(cfg, i) for i in range(cfg.num_hidden_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+    def forward(self, input_ids, positions, attn: AttnInputs):
+        h, residual = F.embedding(input_ids, self.embed_tokens), None
+        for layer in self.layers:
+            h, residual = layer(positions, h, residual, attn)
+        return self.norm(h, residual)[0]
+
+
+class Qwen3ForCausalLM(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.config = cfg
+        self.model = Qwen3Model(cfg)
+        self.lm_head = nn.Parameter(torch.empty(cfg.vocab_size, cfg.hidden_size))
+
+    def forward(self, input_ids, positions, attn: AttnInputs):
+        return self.model(input_ids, positions, attn)
+
+    def compute_logits(self, hidden):
+        return F.linear(hidden, self.lm_head)
+
+    def argmax(self, hidden):
+        """Greedy ids (reference vocab_parallel.py:180-216): argmax of the bf16
+        logits, lowest id on ties, by the sampler kernel."""
+        logits = self.compute_logits(hidden)
+        return sample(logits, None, all_greedy=True)
+
+    @torch.no_grad()
+    def random_init_(self, std: float = 0.02, seed: int = 0):
+        """Weights ~ N(0, std) (norm weights 1), drawn on the parameters' device."""
+        g = torch.Generator(device=self.lm_head.device).manual_seed(seed)
+        for name, p in self.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=g)
+        return self
