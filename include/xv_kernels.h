@@ -157,6 +157,24 @@ int xv_qk_norm_rope(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                     int num_q_heads, int num_kv_heads, int head_dim, hipStream_t stream);
 
 /*
+ * Decode-step fusion of xv_qk_norm_rope with the KV store: q is normed and
+ * rotated into q_out; k is normed, rotated and written, and v copied, straight
+ * into the paged cache at slot_mapping[t] (slot -1 stores nothing), with the
+ * cache addressing of xv_store_kvcache.  Replaces the pair
+ * Qwen3Attention._split_norm_rope (src/compute/models/qwen3.py:117-128) +
+ * store_kvcache (src/compute/kv_ops.py:35-62, called at attention.py:66-72).
+ */
+int xv_qk_norm_rope_store(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                          const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                          const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                          const void* q_weight, const void* k_weight, float eps,
+                          const int64_t* positions, const float* cos_sin_cache, void* q_out,
+                          void* k_cache, void* v_cache, int64_t cache_page_stride,
+                          int64_t cache_tok_stride, int64_t cache_head_stride, int block_size,
+                          const int32_t* slot_mapping, int64_t num_tokens, int num_q_heads,
+                          int num_kv_heads, int head_dim, hipStream_t stream);
+
+/*
  * SiLU-and-mul.
  * Replaces vllm::silu_and_mul, src/compute/layers/ops.py:20-23 (gate first, up second).
  *   out[t, i] = silu(x[t, i]) * x[t, I + i]

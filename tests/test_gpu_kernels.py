@@ -8,6 +8,7 @@ import pytest
 import torch
 
 import oracle.ops as O
+import xvllm.layers.ops  # noqa: F401  (registers the vllm:: and xv:: ops)
 from helpers import f32, gen, make_paged, randn_bf16
 
 pytestmark = pytest.mark.gpu
@@ -261,3 +262,36 @@ def test_sampler_many_draws_bitexact(dev):
     got = sample(logits.to(dev), args["temps"].to(dev), args["tps"].to(dev), args["tks"].to(dev), None, u.to(dev),
                  use_top_k=True, use_top_p=True)
     assert np.array_equal(got.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("hnd", [False, True])
+def test_qk_norm_rope_store_matches_separate_ops(dev, hnd):
+    """Fused decode kernel == qk_norm_rope followed by store_kvcache, bit for bit,
+    into a reference-layout pool and into a head-major (strided) pool view."""
+    from xvllm.kv_ops import store_kvcache
+
+    g = gen(77)
+    t, hq, hkv, d, nb = 13, 32, 8, 128, 12
+    qkv, pos, cs = _rope_inputs(g, t, hq, hkv)
+    qw = randn_bf16((d,), g, std=0.1, mean=1.0).to(dev)
+    kw = randn_bf16((d,), g, std=0.1, mean=1.0).to(dev)
+    qg = qkv.to(dev)
+    q = qg[:, : hq * d].view(t, hq, d)
+    k = qg[:, hq * d : (hq + hkv) * d].view(t, hkv, d)
+    v = qg[:, (hq + hkv) * d :].view(t, hkv, d)
+    slots = torch.randperm(nb * 16, generator=g)[:t].to(torch.int32)
+    slots[3] = -1
+
+    def pool():
+        if hnd:  # physical [NB, Hkv, BS, D] seen as [NB, BS, Hkv, D]
+            return randn_bf16((nb, hkv, 16, d), g).to(dev).permute(0, 2, 1, 3)
+        return randn_bf16((nb, 16, hkv, d), g).to(dev)
+
+    kc1, vc1 = pool(), pool()
+    kc2, vc2 = kc1.clone(), vc1.clone()
+    qo, ko = torch.ops.xv.qk_norm_rope(q, k, qw, kw, 1e-6, pos.to(dev), cs.to(dev))
+    store_kvcache(ko, v, kc1, vc1, slots.to(dev))
+    qf = torch.ops.xv.qk_norm_rope_store(q, k, v, qw, kw, 1e-6, pos.to(dev), cs.to(dev), kc2, vc2, slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(qf, qo)
+    assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)

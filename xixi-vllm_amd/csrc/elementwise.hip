@@ -57,10 +57,20 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
 // RMSNorm family.  TPR lanes own one row (16 = a DPP row, 64 = a wave); each
 // lane keeps up to VPT 8-element vectors of the row in registers.
 // --------------------------------------------------------------------------
+// Sum over the TPR lanes owning a row (TPR = 256: the whole workgroup, through LDS).
 template <int TPR>
 XV_INLINE float row_sum(float x) {
-  if constexpr (TPR == 16) return row16_sum(x);
-  else return wave_sum(x);
+  if constexpr (TPR == 16) {
+    return row16_sum(x);
+  } else if constexpr (TPR == 64) {
+    return wave_sum(x);
+  } else {
+    __shared__ float part[4];
+    x = wave_sum(x);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+    __syncthreads();
+    return (part[0] + part[1]) + (part[2] + part[3]);
+  }
 }
 
 template <int TPR, int VPT>
@@ -77,12 +87,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   const bf16_t* xr = x + o * s_outer + i * s_inner;
   int nvec = hidden >> 3;
   float v[VPT][8];
+  Vec8 wv[VPT];
   float ss = 0.f;
 #pragma unroll
   for (int k = 0; k < VPT; ++k) {
     int vi = lane + k * TPR;
     if (active && vi < nvec) {
       unpack8(load_vec8(xr + vi * 8), v[k]);
+      wv[k] = load_vec8(w + vi * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += v[k][e] * v[k][e];
     }
@@ -96,7 +108,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
     int vi = lane + k * TPR;
     if (vi < nvec) {
       float wf[8], r[8];
-      unpack8(load_vec8(w + vi * 8), wf);
+      unpack8(wv[k], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
       store_vec8(orow + vi * 8, pack8(r));
@@ -115,6 +127,17 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
   bf16_t* xr = x + (active ? row : 0) * xs;
   bf16_t* rr = res + (active ? row : 0) * rs;
   int nvec = hidden >> 3;
+  // all loads (x, residual, weight) issued up front: one memory round trip
+  Vec8 xv[VPT], rv[VPT], wv[VPT];
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (active && vi < nvec) {
+      xv[k] = load_vec8(xr + vi * 8);
+      rv[k] = load_vec8(rr + vi * 8);
+      wv[k] = load_vec8(w + vi * 8);
+    }
+  }
   float v[VPT][8];
   float ss = 0.f;
 #pragma unroll
@@ -122,8 +145,8 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
     int vi = lane + k * TPR;
     if (active && vi < nvec) {
       float a[8], b[8];
-      unpack8(load_vec8_nt(xr + vi * 8), a);
-      unpack8(load_vec8_nt(rr + vi * 8), b);
+      unpack8(xv[k], a);
+      unpack8(rv[k], b);
 #pragma unroll
       for (int e = 0; e < 8; ++e) { v[k][e] = a[e] + b[e]; ss += v[k][e] * v[k][e]; }
       store_vec8(rr + vi * 8, pack8(v[k]));
@@ -137,7 +160,7 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
     int vi = lane + k * TPR;
     if (vi < nvec) {
       float wf[8], r[8];
-      unpack8(load_vec8(w + vi * 8), wf);
+      unpack8(wv[k], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
       store_vec8(xr + vi * 8, pack8(r));
@@ -150,6 +173,13 @@ static int dispatch_norm(int64_t rows, int hidden, hipStream_t stream, Args... a
   if (hidden <= 0 || hidden % 8 || hidden > 16384) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   int nvec = hidden / 8;
+  // few long rows (decode batches): a whole workgroup per row keeps each
+  // lane's memory chain short; many rows: a wave (or a DPP row) per row
+  if (rows <= 1024 && nvec >= 256) {
+    if (nvec <= 512) return Launcher<256, 2>::run(rows, stream, args...);
+    if (nvec <= 1024) return Launcher<256, 4>::run(rows, stream, args...);
+    return Launcher<256, 8>::run(rows, stream, args...);
+  }
   if (nvec <= 16) return Launcher<16, 1>::run(rows, stream, args...);
   if (nvec <= 32) return Launcher<16, 2>::run(rows, stream, args...);
   if (nvec <= 64) return Launcher<16, 4>::run(rows, stream, args...);
@@ -203,21 +233,42 @@ extern "C" int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, i
 // 16 lanes own one head of D = 128: lane j holds elements [8j, 8j+8); the
 // rotation partner of lane j is lane j^8 (same DPP row, fetched by row_ror:8).
 // --------------------------------------------------------------------------
-template <bool NORM>
+// STORE: k heads go (roped) and v heads go (copied) straight into the paged
+// cache at slot_mapping[t] (slot -1: nothing stored), instead of into k_out.
+struct CacheDst {
+  bf16_t* kc; bf16_t* vc;
+  int64_t ps, ts, hs;
+  int block_size;
+  const int32_t* slots;
+  const bf16_t* v; int64_t vs_tok, vs_head;
+};
+
+template <bool NORM, bool STORE>
 __global__ __launch_bounds__(256) void rope_kernel(
     const bf16_t* __restrict__ q, int64_t qs_tok, int64_t qs_head,
     const bf16_t* __restrict__ k, int64_t ks_tok, int64_t ks_head,
     const bf16_t* __restrict__ qw, const bf16_t* __restrict__ kw, float eps,
     const int64_t* __restrict__ positions, const float* __restrict__ cos_sin,
     bf16_t* __restrict__ q_out, bf16_t* __restrict__ k_out,
-    int64_t num_tokens, int hq, int hkv) {
+    int64_t num_tokens, int hq, int hkv, CacheDst cd) {
   constexpr int D = 128;
-  const int heads = hq + hkv;
+  const int heads = hq + hkv + (STORE ? hkv : 0);  // STORE: v heads follow the k heads
   int64_t gh = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
   int lane = threadIdx.x & 15;
   bool active = gh < num_tokens * heads;
   int64_t tok = active ? gh / heads : 0;
   int h = active ? (int)(gh - tok * heads) : 0;
+  if constexpr (STORE) {
+    if (h >= hq + hkv) {  // v head: plain copy into the cache (no cross-lane work in this group)
+      const int32_t slot = active ? cd.slots[tok] : -1;
+      if (slot < 0) return;
+      const int vh = h - hq - hkv;
+      const int page = slot / cd.block_size, t = slot - page * cd.block_size;
+      const Vec8 vv = load_vec8(cd.v + tok * cd.vs_tok + (int64_t)vh * cd.vs_head + lane * 8);
+      store_vec8(cd.vc + (int64_t)page * cd.ps + (int64_t)t * cd.ts + (int64_t)vh * cd.hs + lane * 8, vv);
+      return;
+    }
+  }
   const bool is_q = h < hq;
   const bf16_t* src = is_q ? q + tok * qs_tok + (int64_t)h * qs_head
                            : k + tok * ks_tok + (int64_t)(h - hq) * ks_head;
@@ -255,8 +306,30 @@ __global__ __launch_bounds__(256) void rope_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) r[e] = x[e] * c[e] + partner[e] * s[e];
   }
-  bf16_t* dst = is_q ? q_out + (tok * hq + h) * D : k_out + (tok * hkv + (h - hq)) * D;
-  store_vec8(dst + lane * 8, pack8(r));
+  if (is_q) {
+    store_vec8(q_out + (tok * hq + h) * D + lane * 8, pack8(r));
+  } else if constexpr (STORE) {
+    const int32_t slot = cd.slots[tok];
+    if (slot < 0) return;
+    const int page = slot / cd.block_size, t = slot - page * cd.block_size;
+    store_vec8(cd.kc + (int64_t)page * cd.ps + (int64_t)t * cd.ts + (int64_t)(h - hq) * cd.hs + lane * 8, pack8(r));
+  } else {
+    store_vec8(k_out + (tok * hkv + (h - hq)) * D + lane * 8, pack8(r));
+  }
+}
+
+template <bool NORM, bool STORE>
+static int launch_rope_t(const void* q, int64_t qst, int64_t qsh, const void* k, int64_t kst, int64_t ksh,
+                         const void* qw, const void* kw, float eps, const int64_t* positions, const float* cs,
+                         void* q_out, void* k_out, int64_t T, int hq, int hkv, const CacheDst& cd,
+                         hipStream_t stream) {
+  const int64_t heads = T * (hq + hkv + (STORE ? hkv : 0));
+  const unsigned blocks = (unsigned)((heads + 15) / 16);
+  rope_kernel<NORM, STORE><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
+                                                       (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
+                                                       (bf16_t*)q_out, (bf16_t*)k_out, T, hq, hkv, cd);
+  XV_CHECK_LAUNCH();
+  return 0;
 }
 
 static int launch_rope(bool norm, const void* q, int64_t qst, int64_t qsh, const void* k, int64_t kst,
@@ -265,18 +338,32 @@ static int launch_rope(bool norm, const void* q, int64_t qst, int64_t qsh, const
                        hipStream_t stream) {
   if (D != 128 || hq <= 0 || hkv < 0 || T < 0) return (int)hipErrorInvalidValue;
   if (T == 0) return 0;
-  int64_t heads = T * (hq + hkv);
-  unsigned blocks = (unsigned)((heads + 15) / 16);
-  if (norm)
-    rope_kernel<true><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
-                                                  (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
-                                                  (bf16_t*)q_out, (bf16_t*)k_out, T, hq, hkv);
-  else
-    rope_kernel<false><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
-                                                   nullptr, nullptr, 0.f, positions, cs, (bf16_t*)q_out,
-                                                   (bf16_t*)k_out, T, hq, hkv);
-  XV_CHECK_LAUNCH();
-  return 0;
+  CacheDst cd = {};
+  return norm ? launch_rope_t<true, false>(q, qst, qsh, k, kst, ksh, qw, kw, eps, positions, cs, q_out, k_out, T, hq,
+                                           hkv, cd, stream)
+              : launch_rope_t<false, false>(q, qst, qsh, k, kst, ksh, qw, kw, eps, positions, cs, q_out, k_out, T,
+                                            hq, hkv, cd, stream);
+}
+
+extern "C" int xv_qk_norm_rope_store(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                     const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                     const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                     const void* q_weight, const void* k_weight, float eps,
+                                     const int64_t* positions, const float* cos_sin_cache, void* q_out,
+                                     void* k_cache, void* v_cache, int64_t cache_page_stride,
+                                     int64_t cache_tok_stride, int64_t cache_head_stride, int block_size,
+                                     const int32_t* slot_mapping, int64_t num_tokens, int num_q_heads,
+                                     int num_kv_heads, int head_dim, hipStream_t stream) {
+  if (head_dim != 128 || num_q_heads <= 0 || num_kv_heads <= 0 || num_tokens < 0 || block_size <= 0)
+    return (int)hipErrorInvalidValue;
+  if (num_tokens == 0) return 0;
+  CacheDst cd;
+  cd.kc = (bf16_t*)k_cache; cd.vc = (bf16_t*)v_cache;
+  cd.ps = cache_page_stride; cd.ts = cache_tok_stride; cd.hs = cache_head_stride; cd.block_size = block_size;
+  cd.slots = slot_mapping; cd.v = (const bf16_t*)v; cd.vs_tok = v_stride_tok; cd.vs_head = v_stride_head;
+  return launch_rope_t<true, true>(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, q_weight, k_weight,
+                                   eps, positions, cos_sin_cache, q_out, nullptr, num_tokens, num_q_heads,
+                                   num_kv_heads, cd, stream);
 }
 
 extern "C" int xv_rotary_embedding(const void* q, int64_t q_stride_tok, int64_t q_stride_head,

@@ -34,6 +34,10 @@ SIGNATURES: dict[str, tuple] = {
     "xv_qk_norm_rope": (
         i32, [vp, i64, i64, vp, i64, i64, vp, vp, f32, vp, vp, vp, vp, i64, i32, i32, i32, vp]
     ),
+    "xv_qk_norm_rope_store": (
+        i32, [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp, f32, vp, vp, vp, vp, vp, i64, i64, i64, i32, vp,
+              i64, i32, i32, i32, vp]
+    ),
     "xv_silu_and_mul": (i32, [vp, i64, vp, i64, i64, i32, vp]),
     "xv_sampler_workspace_size": (sz, [i32, i32]),
     "xv_sample": (i32, [vp, i64, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz, vp]),

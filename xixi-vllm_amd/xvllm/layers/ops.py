@@ -170,3 +170,54 @@ def qk_norm_rope(
 @qk_norm_rope.register_fake
 def _qk_norm_rope_fake(q, k, q_weight, k_weight, eps, positions, cos_sin_cache):
     return torch.empty(q.shape, dtype=q.dtype, device=q.device), torch.empty(k.shape, dtype=k.dtype, device=k.device)
+
+
+def _cache_strides(cache: torch.Tensor) -> tuple[int, int, int, int]:
+    """(page, token, head strides, block size) of a paged [NB, BS, Hkv, D] cache view."""
+    assert cache.dim() == 4 and cache.stride(-1) == 1
+    return cache.stride(0), cache.stride(1), cache.stride(2), cache.shape[1]
+
+
+@torch.library.custom_op("xv::qk_norm_rope_store", mutates_args=("k_cache", "v_cache"))
+def qk_norm_rope_store(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    q_weight: torch.Tensor,
+    k_weight: torch.Tensor,
+    eps: float,
+    positions: torch.Tensor,
+    cos_sin_cache: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+) -> torch.Tensor:
+    """Decode-step fusion: q/k head RMSNorm + RoPE; q returned [T, Hq, D], k (roped)
+    and v written into the paged caches at slot_mapping (reference
+    qwen3.py:117-128 followed by kv_ops.store_kvcache)."""
+    require_cuda(q, k, v, k_cache, v_cache, slot_mapping)
+    require_bf16(q, k, v, k_cache, v_cache)
+    q3, qs0, qs1 = _head_view(q)
+    k3, ks0, ks1 = _head_view(k)
+    v3, vs0, vs1 = _head_view(v)
+    n, hq, d = q3.shape
+    ps, ts, hs, bs = _cache_strides(k_cache)
+    assert v_cache.stride() == k_cache.stride()
+    slots = slot_mapping.to(torch.int32).contiguous()
+    pos = positions.to(torch.int64).contiguous()
+    qo = torch.empty((n, hq, d), dtype=q.dtype, device=q.device)
+    _C.check(
+        _C.lib().xv_qk_norm_rope_store(
+            ptr(q3), qs0, qs1, ptr(k3), ks0, ks1, ptr(v3), vs0, vs1, ptr(q_weight.contiguous()),
+            ptr(k_weight.contiguous()), float(eps), ptr(pos), ptr(cos_sin_cache.contiguous()), ptr(qo),
+            ptr(k_cache), ptr(v_cache), ps, ts, hs, bs, ptr(slots), n, hq, k3.shape[1], d, stream_of(q),
+        ),
+        "xv_qk_norm_rope_store",
+    )
+    return qo
+
+
+@qk_norm_rope_store.register_fake
+def _qk_norm_rope_store_fake(q, k, v, q_weight, k_weight, eps, positions, cos_sin_cache, k_cache, v_cache,
+                             slot_mapping):
+    return torch.empty(q.shape, dtype=q.dtype, device=q.device)

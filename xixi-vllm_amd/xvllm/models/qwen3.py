@@ -17,6 +17,7 @@ from torch import nn
 from ..config import head_dim as _head_dim
 from ..config import rope_theta as _rope_theta
 from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
+from ..layers.attention import kv_cache_of
 from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
 
@@ -49,17 +50,35 @@ class Qwen3Attention(nn.Module):
 
     def forward(self, positions, hidden, attn: AttnInputs):
         qkv = F.linear(hidden, self.qkv_proj)
-        q, k, v = self._split_norm_rope(positions, qkv)
-        o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
+        if not attn.is_prefill:
+            # decode: norm + RoPE + KV store in one kernel, attention reads the cache
+            q, k, v = self._split_norm_rope_store(positions, qkv, attn.slot_mapping)
+            o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn._replace(slot_mapping=None))
+        else:
+            q, k, v = self._split_norm_rope(positions, qkv)
+            o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
         return F.linear(o, self.o_proj)
 
-    def _split_norm_rope(self, positions, qkv):
-        """split -> per-head q/k RMSNorm -> RoPE (reference qwen3.py:117-128),
-        the two norms and the rotation as one kernel reading the qkv views."""
+    def _views(self, qkv):
         t = qkv.shape[0]
         q = qkv[:, : self.q_size].view(t, self.num_heads, self.head_dim)
         k = qkv[:, self.q_size : self.q_size + self.kv_size].view(t, self.num_kv_heads, self.head_dim)
         v = qkv[:, self.q_size + self.kv_size :].view(t, self.num_kv_heads, self.head_dim)
+        return q, k, v
+
+    def _split_norm_rope_store(self, positions, qkv, slot_mapping):
+        q, k, v = self._views(qkv)
+        k_cache, v_cache = kv_cache_of(self.attn.layer_id)
+        q = torch.ops.xv.qk_norm_rope_store(
+            q, k, v, self.q_norm.weight, self.k_norm.weight, self.eps, positions, self.rotary_emb.cos_sin_cache,
+            k_cache, v_cache, slot_mapping,
+        )
+        return q, k, v
+
+    def _split_norm_rope(self, positions, qkv):
+        """split -> per-head q/k RMSNorm -> RoPE (reference qwen3.py:117-128),
+        the two norms and the rotation as one kernel reading the qkv views."""
+        q, k, v = self._views(qkv)
         q, k = torch.ops.xv.qk_norm_rope(
             q, k, self.q_norm.weight, self.k_norm.weight, self.eps, positions, self.rotary_emb.cos_sin_cache
         )
