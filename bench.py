@@ -28,6 +28,10 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
+# FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
+# 2 x 313494.2 KiB read (FETCH_SIZE counts half on this part) + 3210.9 KiB written.
+MEASURED_TRAFFIC_BYTES = int((2 * 313494.2 + 3210.9) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
@@ -254,6 +258,9 @@ def main() -> int:
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-suite", action="store_true", help="skip the config-3 kernel set and the sampler")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B decode tok/s measurement")
+    ap.add_argument("--e2e-only", action="store_true", help="only the Qwen3-8B decode step (for profiling)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -266,8 +273,19 @@ def main() -> int:
         print(json.dumps({"error": "no GPU visible"}))
         return 1
     dev = torch.device("cuda:0")
+    if args.calibrate_copy:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibration": "copy", "bytes_read": 1 << 30, "bytes_written": 1 << 30, "launches": 5}))
+        return 0
     g = torch.Generator().manual_seed(args.seed)
     ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
+    if args.e2e_only:
+        print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
+        return 0
     cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1)
     ms, wall = time_decode(torch, cases, args.steps, args.warmup)
     nbytes = algo_bytes(ctx)
@@ -309,7 +327,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": MEASURED_TRAFFIC_BYTES,
             "algorithmic_bytes_per_call": nbytes,
             "kernel": "paged_decode_kernel<4> + merge_splits_kernel (one call)",
         },
