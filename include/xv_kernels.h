@@ -188,7 +188,7 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  * Replaces Sampler.forward, src/compute/sampler.py:27-119, and the greedy
  * ParallelLMHead.argmax, src/compute/layers/vocab_parallel.py:180-216.
  * Per row: temperature <= 1e-5 (or flag XV_SAMPLE_ALL_GREEDY) -> argmax of the
- * logits, lowest index on ties.  Otherwise x = logit / temperature; candidates
+ *  logits, lowest index on ties.  Otherwise x = logit * (1/temperature); candidates
  * are ordered by descending x, ties by ascending id; the kept set is the
  * shortest prefix satisfying top-k (top_ks[b] < V), top-p (a candidate is
  * dropped when the mass strictly before it exceeds top_p of the top-k mass)

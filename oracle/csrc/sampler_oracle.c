@@ -5,6 +5,7 @@
  * _sample_ordered) and src/compute/layers/vocab_parallel.py:180-216 (greedy
  * argmax), with the draw made explicit: one uniform u per row, inverse CDF
  * over the kept candidates in ascending id order, masses in 2^-40 fixed point.
+ * The logits are scaled by 1/T (one fp32 reciprocal per row), not divided.
  *
  * Written as the direct, sort-based formulation (the reference sorts the
  * scaled logits and takes a cumulative sum); the GPU kernel reaches the same
@@ -80,11 +81,12 @@ int64_t oracle_sample_row(const uint16_t *logits, int V, float temperature, floa
   }
   /* the max logit: inverse of order_key */
   uint16_t maxbits = (kmax & 0x8000u) ? (uint16_t)(kmax & 0x7fffu) : (uint16_t)~kmax;
-  const float zmax = bf16f(maxbits) / temperature;
+  const float inv_t = 1.0f / temperature;
+  const float zmax = bf16f(maxbits) * inv_t;
   float *e = malloc(sizeof(float) * V);
   for (int i = 0; i < V; ++i) {
     if (key[i] == 0u) { e[i] = 0.f; q[i] = 0; continue; }
-    float z = bf16f(logits[i]) / temperature;
+    float z = bf16f(logits[i]) * inv_t;
     float d = z - zmax;
     d = d * 1.44269502162933349609375f; /* log2(e) in fp32 */
     e[i] = oracle_exp2(d);
@@ -162,10 +164,11 @@ void oracle_probs_row(const uint16_t *logits, int V, float temperature, float to
     if (key[i] > kmax) kmax = key[i];
   }
   uint16_t maxbits = (kmax & 0x8000u) ? (uint16_t)(kmax & 0x7fffu) : (uint16_t)~kmax;
-  const float zmax = bf16f(maxbits) / temperature;
+  const float inv_t = 1.0f / temperature;
+  const float zmax = bf16f(maxbits) * inv_t;
   for (int i = 0; i < V; ++i) {
     if (key[i] == 0u) { e[i] = 0.f; q[i] = 0; continue; }
-    float d = bf16f(logits[i]) / temperature - zmax;
+    float d = bf16f(logits[i]) * inv_t - zmax;
     d = d * 1.44269502162933349609375f;
     e[i] = oracle_exp2(d);
     q[i] = (int64_t)(e[i] * 1099511627776.0f);

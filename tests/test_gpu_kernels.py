@@ -205,8 +205,10 @@ def test_prefill_attention(dev, hq, hkv, qlens, klens, paged):
 
 # ------------------------------------------------------------------ sampler
 def _sampler_case(g, b, v, std=2.0, ties=False):
+    if ties == "flat":
+        std = 0.004
     x = torch.randn((b, v), generator=g) * std
-    if ties:
+    if ties is True:
         x = torch.round(x * 4) / 4  # few distinct values: ties everywhere
     return x.to(torch.bfloat16)
 
@@ -222,6 +224,9 @@ def _sampler_case(g, b, v, std=2.0, ties=False):
         ("minp", 8, 151936, 8, 1.0, 1.0, 0, 0.1, False),
         ("all_filters_ties", 8, 32000, 2 | 4 | 8, 0.8, 0.8, 300, 0.02, True),
         ("odd_vocab", 5, 1003, 2 | 4, 1.1, 0.6, 7, 0.0, False),
+        # near-flat rows: the boundary bucket overflows LDS -> the row-wide radix-select path
+        ("flat_fallback_topp", 4, 151936, 4, 1.0, 0.5, 0, 0.0, "flat"),
+        ("flat_fallback_topk", 4, 151936, 2 | 4, 1.0, 0.9, 20000, 0.0, "flat"),
     ],
 )
 def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, ties):

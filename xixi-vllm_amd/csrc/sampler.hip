@@ -1,19 +1,27 @@
 // Vocab-wide sampler for gfx950: greedy argmax, temperature / top-k / top-p /
 // min-p with an explicit uniform per row, one 1024-thread workgroup per row.
 //
-// The candidates are ordered by descending logit, ties by ascending id.  Since
-// x = logit / T is monotone in the bf16 logit, the order key is the 16-bit
-// order-preserving image of the bf16 bits, so every cut-off is found by a
-// two-level (high byte, low byte) radix select over key histograms of counts
-// and fixed-point masses held in LDS, instead of a sort:
-//   q(key) = trunc(2^40 * 2^((x - x_max) * log2 e)), an exact int64 per candidate
-//   top-k : rank k-1 found by count;   top-p : first rank whose inclusive mass
-//   exceeds floor(top_p * mass(top-k));  min-p : smallest key with p >= min_p.
-// The kept set is the shortest of the three prefixes (boundary = key + tie
-// index); the token is the first kept id (ascending) whose inclusive mass
-// exceeds floor(u * M_kept), found by a block-wide int64 prefix scan.
-// exp2 is a fixed Taylor polynomial with explicit FMAs so that the masses,
-// hence the token ids, are bit-identical to the C restatement of the oracle.
+// Candidates are ordered by descending logit, ties by ascending id.  Every
+// candidate's probability mass is an exact int64
+//   q = trunc(2^40 * 2^d),  d = (l * (1/T) - x_max) * log2 e  (<= 0)
+// with a fixed Taylor exp2 (explicit FMAs) shared with the C restatement of the
+// oracle, so kept sets, masses and token ids are bit-identical to it.
+//
+// Fast path (every row whose boundary fits in LDS):
+//   1. one pass: max key;
+//   2. one pass: q of every candidate, binned by distance below the max,
+//      bucket = min(255, floor(-16 d)) (1/16 of a binary order per bucket;
+//      per-wave LDS histograms of counts and masses, the far bucket in registers);
+//   3. the buckets give the bucket holding each cut-off: top-k (by count),
+//      top-p (first bucket whose inclusive mass exceeds floor(top_p * mass of
+//      the top-k set)), min-p (bucket of the smallest key whose probability
+//      reaches min_p of the largest); only the earliest such bucket's
+//      candidates are gathered to LDS and bitonic-sorted, which gives the exact
+//      boundary candidate (key, id) and the kept mass M;
+//   4. one pass: inverse CDF in ascending id order, exp only for kept ids:
+//      the first kept id whose inclusive mass exceeds floor(u * M).
+// A boundary bucket larger than LDS falls back to an exact row-wide two-level
+// (high byte, low byte) radix select over LDS histograms.
 #include "xv_common.h"
 #include "xv_kernels.h"
 #include <math.h>
@@ -26,6 +34,8 @@ constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
 constexpr int kTile = kThreads * 8;
 constexpr int64_t kTieAll = 0x7fffffffffffffffll;
+constexpr int kBuckets = 256;
+constexpr int kMaxCand = 8192;  // candidates of one bucket sorted in LDS
 
 XV_INLINE float sampler_exp2(float x) {
   if (!(x > -125.0f)) return 0.0f;
@@ -48,13 +58,18 @@ XV_INLINE uint32_t order_key(uint32_t b) {  // 0 is reserved for NaN / padding
 }
 XV_INLINE uint32_t key_to_bits(uint32_t k) { return (k & 0x8000u) ? (k & 0x7fffu) : (~k & 0xffffu); }
 
-XV_INLINE float exp_of(uint32_t bits, float temp, float zmax) {
-  float z = bf16_to_f32(bits) / temp;
+// d = (l / T - x_max) * log2 e, evaluated as the oracle does
+XV_INLINE float log2_ratio(uint32_t bits, float inv_t, float zmax) {
+  float z = bf16_to_f32(bits) * inv_t;
   float d = z - zmax;
-  d = d * 1.44269502162933349609375f;
-  return sampler_exp2(d);
+  return d * 1.44269502162933349609375f;
 }
+XV_INLINE float exp_of(uint32_t bits, float inv_t, float zmax) { return sampler_exp2(log2_ratio(bits, inv_t, zmax)); }
 XV_INLINE int64_t mass_of(float e) { return (int64_t)(e * 1099511627776.0f); }
+XV_INLINE int bucket_of(float d) {
+  const float u = -d * 16.0f;
+  return u < 255.0f ? (int)u : 255;
+}
 
 // Load the 8 logits of thread t in tile j (bits, 0xffff = NaN for padding).
 XV_INLINE void load8(const bf16_t* row, int V, int base, bool vec_ok, uint32_t (&bits)[8]) {
@@ -65,6 +80,54 @@ XV_INLINE void load8(const bf16_t* row, int V, int base, bool vec_ok, uint32_t (
   } else {
 #pragma unroll
     for (int k = 0; k < 8; ++k) bits[k] = (base + k < V) ? (uint32_t)row[base + k] : 0xffffu;
+  }
+}
+
+// Apply f(bits, id) to every id of this thread's contiguous range
+// [t*C, t*C + C), C a multiple of 8: chunks of kChunk 16-byte loads are issued
+// together, so a pass over the row costs a few memory round trips, not one
+// per vector.  Thread order is id order.
+constexpr int kChunk = 8;
+XV_INLINE int range_len(int V) { return ((V + kThreads - 1) / kThreads + 7) / 8 * 8; }
+// Apply f(bits, id) to the ids of a coalesced, lane-interleaved layout: in
+// step c, vector v of thread t is id 8*((c*kChunk + v)*kThreads + t).  Ids
+// ascend within a thread.  Order across threads is not id order.
+template <typename F>
+XV_INLINE void for_each_strided(const bf16_t* row, int V, bool vec_ok, F&& f) {
+  const int nvec = (V + 7) / 8;
+  for (int c = 0; c * kChunk * kThreads < nvec; ++c) {
+    uint32_t bits[kChunk][8];
+#pragma unroll
+    for (int v = 0; v < kChunk; ++v) {
+      const int vi = (c * kChunk + v) * kThreads + threadIdx.x;
+      if (vi < nvec) load8(row, V, vi * 8, vec_ok, bits[v]);
+    }
+#pragma unroll
+    for (int v = 0; v < kChunk; ++v) {
+      const int vi = (c * kChunk + v) * kThreads + threadIdx.x;
+      if (vi < nvec)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) f(bits[v][k], vi * 8 + k);
+    }
+  }
+}
+
+template <typename F>
+XV_INLINE void for_each_elem(const bf16_t* row, int V, bool vec_ok, F&& f) {
+  const int C = range_len(V);
+  const int i0 = threadIdx.x * C, i1 = min(V, i0 + C);
+  for (int c = i0; c < i1; c += 8 * kChunk) {
+    uint32_t bits[kChunk][8];
+#pragma unroll
+    for (int v = 0; v < kChunk; ++v)
+      if (c + 8 * v < i1) load8(row, V, c + 8 * v, vec_ok, bits[v]);
+#pragma unroll
+    for (int v = 0; v < kChunk; ++v)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int id = c + 8 * v + k;
+        if (id < i1) f(bits[v][k], id);
+      }
   }
 }
 
@@ -80,6 +143,16 @@ struct Shared {
   int64_t b_id;
   int64_t b_total;
   int b_hb;
+  int b_int[8];
+  int64_t b_long[8];
+};
+
+// LDS of the fast path: per-wave bucket histograms, then the candidate list
+struct FastShared {
+  uint32_t wcnt[kWaves][kBuckets];
+  unsigned long long wmass[kWaves][kBuckets];
+  unsigned long long cand[kMaxCand];  // (key << 32) | (0xffffffff - id), sorted descending
+  int ncand;
 };
 
 XV_INLINE uint32_t wave_max_u(uint32_t x) {
@@ -167,66 +240,14 @@ XV_INLINE bool earlier(const Boundary& a, const Boundary& b) {
   return a.key > b.key || (a.key == b.key && a.tie < b.tie);
 }
 
-__global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restrict__ logits, int64_t stride, int V,
-                                                          const float* __restrict__ temps,
-                                                          const float* __restrict__ top_ps,
-                                                          const int32_t* __restrict__ top_ks,
-                                                          const float* __restrict__ min_ps,
-                                                          const float* __restrict__ uniforms, int flags,
-                                                          int64_t* __restrict__ out_ids) {
-  __shared__ Shared s;
-  const int b = blockIdx.x;
+// Exact cut-offs by a two-level (high byte, low byte) radix select over LDS
+// histograms of the whole row: the fallback when the boundary bucket of the
+// fast path holds more candidates than LDS does (very flat distributions).
+XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t,
+                                float zmax, int top_k, float top_p, float min_p, bool use_k, bool use_p,
+                                bool use_m, Boundary& bd_out, int64_t& id_cut_out, int64_t& M_out) {
   const int t = threadIdx.x;
-  const bf16_t* row = logits + (int64_t)b * stride;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
-  const int ntiles = (V + kTile - 1) / kTile;
-  const float temp = temps ? temps[b] : 1.0f;
-  const bool greedy = (flags & XV_SAMPLE_ALL_GREEDY) || temp <= 1e-5f;
-
-  // ---- pass 1: max (greedy: max value then lowest index holding it) ----
-  if (greedy) {
-    float fm = -INFINITY;
-    for (int j = 0; j < ntiles; ++j) {
-      uint32_t bits[8];
-      load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (order_key(bits[k])) fm = fmaxf(fm, bf16_to_f32(bits[k]));
-    }
-    fm = block_maxf(s, fm);
-    uint32_t best = 0xffffffffu;
-    for (int j = 0; j < ntiles; ++j) {
-      uint32_t bits[8];
-      const int base = j * kTile + t * 8;
-      load8(row, V, base, vec_ok, bits);
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (order_key(bits[k]) && bf16_to_f32(bits[k]) == fm) best = min(best, (uint32_t)(base + k));
-    }
-    best = block_min_u(s, best);
-    if (t == 0) out_ids[b] = best == 0xffffffffu ? 0 : (int64_t)best;
-    return;
-  }
-
-  uint32_t kmax = 0;
-  for (int j = 0; j < ntiles; ++j) {
-    uint32_t bits[8];
-    load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) kmax = max(kmax, order_key(bits[k]));
-  }
-  kmax = block_max_u(s, kmax);
-  const float zmax = bf16_to_f32(key_to_bits(kmax)) / temp;
-
-  const int top_k = ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
-  const float top_p = ((flags & XV_SAMPLE_USE_TOP_P) && top_ps) ? top_ps[b] : 1.0f;
-  const float min_p = ((flags & XV_SAMPLE_USE_MIN_P) && min_ps) ? min_ps[b] : 0.0f;
-  const bool use_k = top_k > 0 && top_k < V;
-  const bool use_p = top_p < 1.0f;
-  const bool use_m = min_p > 0.0f;
-
-  Boundary bd = {1u, kTieAll};  // everything kept
-
+  Boundary bd = {1u, kTieAll};
   if (use_k || use_p || use_m) {
     // ---- pass 2: high-byte histogram of counts and masses; min-p key ----
     for (int i = t; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
@@ -239,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
       for (int k = 0; k < 8; ++k) {
         const uint32_t key = order_key(bits[k]);
         if (!key) continue;
-        const float e = exp_of(bits[k], temp, zmax);
+        const float e = exp_of(bits[k], inv_t, zmax);
         if (use_m && e >= min_p) kmin_p = min(kmin_p, key);
         atomicAdd(&s.cnt[key >> 8], 1u);
         atomicAdd(&s.mass[key >> 8], (unsigned long long)mass_of(e));
@@ -306,11 +327,11 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
           const uint32_t key = order_key(bits[k]);
-          if (key > bk.key) above += mass_of(exp_of(bits[k], temp, zmax));
+          if (key > bk.key) above += mass_of(exp_of(bits[k], inv_t, zmax));
         }
       }
       above = block_sum_l(s, above);
-      total_k = above + (bk.tie + 1) * mass_of(exp_of(key_to_bits(bk.key), temp, zmax));
+      total_k = above + (bk.tie + 1) * mass_of(exp_of(key_to_bits(bk.key), inv_t, zmax));
     } else {
       total_k = s.b_total;
     }
@@ -330,7 +351,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
         for (int k = 0; k < 8; ++k) {
           const uint32_t key = order_key(bits[k]);
           if (!key) continue;
-          atomicAdd(&s.mass[key >> 8], (unsigned long long)mass_of(exp_of(bits[k], temp, zmax)));
+          atomicAdd(&s.mass[key >> 8], (unsigned long long)mass_of(exp_of(bits[k], inv_t, zmax)));
         }
       }
       __syncthreads();
@@ -359,7 +380,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
           for (int k = 0; k < 8; ++k) {
             const uint32_t key = order_key(bits[k]);
             if (!key || (int)(key >> 8) != hb) continue;
-            atomicAdd(&s.mass[key & 255], (unsigned long long)mass_of(exp_of(bits[k], temp, zmax)));
+            atomicAdd(&s.mass[key & 255], (unsigned long long)mass_of(exp_of(bits[k], inv_t, zmax)));
           }
         }
         __syncthreads();
@@ -371,7 +392,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
             m += (int64_t)s.mass[lb];
           }
           const uint32_t key = ((uint32_t)hb << 8) | (uint32_t)lb;
-          const int64_t q = mass_of(exp_of(key_to_bits(key), temp, zmax));
+          const int64_t q = mass_of(exp_of(key_to_bits(key), inv_t, zmax));
           s.b_key = key;
           s.b_tie = q > 0 ? (thr - m) / q : kTieAll;
         }
@@ -413,7 +434,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
           if (r == bd.tie) s.b_id = base + k;
           ++r;
         }
-        if (kept) M += mass_of(exp_of(bits[k], temp, zmax));
+        if (kept) M += mass_of(exp_of(bits[k], inv_t, zmax));
       }
       carry += tile_ties;
     }
@@ -422,39 +443,411 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
     __syncthreads();  // every thread has read b_id before it is reset below
   }
 
-  // ---- pass 6: inverse-CDF draw in ascending id order ----
+  bd_out = bd;
+  id_cut_out = id_cut;
+  M_out = M;
+}
+
+XV_INLINE int64_t block_min_l(Shared& s, int64_t x) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const int64_t y = __shfl_xor(x, o);
+    x = y < x ? y : x;
+  }
+  const int w = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) s.red_l[w] = x;
+  __syncthreads();
+  int64_t r = s.red_l[0];
+  for (int i = 1; i < kWaves; ++i) r = s.red_l[i] < r ? s.red_l[i] : r;
+  return r;
+}
+
+XV_INLINE uint32_t cand_key(unsigned long long c) { return (uint32_t)(c >> 32); }
+XV_INLINE int64_t cand_id(unsigned long long c) { return (int64_t)(0xffffffffu - (uint32_t)(c & 0xffffffffu)); }
+XV_INLINE int64_t cand_mass(unsigned long long c, float inv_t, float zmax) {
+  return mass_of(exp_of(key_to_bits(cand_key(c)), inv_t, zmax));
+}
+
+// Bitonic sort of fs.cand[0, n) descending (n <= kMaxCand), padding with
+// zeros up to the next power of two; the padding sorts last.
+XV_INLINE void sort_cand_desc(FastShared& fs, int n) {
+  const int t = threadIdx.x;
+  int np2 = 1;
+  while (np2 < n) np2 <<= 1;
+  for (int i = n + t; i < np2; i += kThreads) fs.cand[i] = 0ull;  // padding sorts last
+  __syncthreads();
+  for (int size = 2; size <= np2; size <<= 1) {
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      for (int i = t; i < np2 / 2; i += kThreads) {
+        const int lo = 2 * i - (i & (stride - 1));
+        const int hi = lo + stride;
+        const unsigned long long a = fs.cand[lo], b = fs.cand[hi];
+        const bool desc = (lo & size) == 0;
+        if (desc ? (a < b) : (a > b)) { fs.cand[lo] = b; fs.cand[hi] = a; }
+      }
+      __syncthreads();
+    }
+  }
+}
+
+// Gather the candidates of bucket `target` into fs.cand and bitonic-sort them
+// descending (key descending, id ascending).  Returns the count; a count above
+// kMaxCand means the bucket did not fit (nothing sorted).
+XV_INLINE int gather_bucket(FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t,
+                            float zmax, int target, int target_lo = -1) {
+  if (target_lo < 0) target_lo = target;  // gather buckets target_lo .. target
+  const int t = threadIdx.x;
+  __syncthreads();
+  if (t == 0) fs.ncand = 0;
+  __syncthreads();
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int id) {
+    const uint32_t key = order_key(bits);
+    if (!key) return;
+    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax));
+    if (bkt < target_lo || bkt > target) return;
+    const int slot = atomicAdd(&fs.ncand, 1);
+    if (slot < kMaxCand)
+      fs.cand[slot] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
+  });
+  __syncthreads();
+  const int n = fs.ncand;
+  if (n > kMaxCand) return n;
+  sort_cand_desc(fs, n);
+  return n;
+}
+
+// Sum of the masses of the first m sorted candidates.
+XV_INLINE int64_t list_mass_prefix(Shared& s, const FastShared& fs, int n, int64_t m, float inv_t, float zmax) {
+  const int per = (n + kThreads - 1) / kThreads;
+  const int i0 = threadIdx.x * per, i1 = min(n, i0 + per);
+  int64_t sum = 0;
+  for (int i = i0; i < i1; ++i)
+    if (i < m) sum += cand_mass(fs.cand[i], inv_t, zmax);
+  return block_sum_l(s, sum);
+}
+
+// First sorted index whose inclusive mass (plus base) exceeds thr, n if none.
+XV_INLINE int64_t list_first_exceed(Shared& s, const FastShared& fs, int n, int64_t base, int64_t thr, float inv_t,
+                                    float zmax) {
+  const int per = (n + kThreads - 1) / kThreads;
+  const int i0 = threadIdx.x * per, i1 = min(n, i0 + per);
+  int64_t local = 0;
+  for (int i = i0; i < i1; ++i) local += cand_mass(fs.cand[i], inv_t, zmax);
+  int64_t tot;
+  int64_t cum = base + block_excl_scan(s, local, &tot);
+  int64_t found = n;
+  for (int i = i0; i < i1; ++i) {
+    cum += cand_mass(fs.cand[i], inv_t, zmax);
+    if (cum > thr) { found = i; break; }
+  }
+  return block_min_l(s, found);
+}
+
+// Number of sorted candidates with key >= kmin (a prefix of the list).
+XV_INLINE int64_t list_count_ge(Shared& s, const FastShared& fs, int n, uint32_t kmin) {
+  int64_t c = 0;
+  for (int i = threadIdx.x; i < n; i += kThreads) c += cand_key(fs.cand[i]) >= kmin;
+  return block_sum_l(s, c);
+}
+
+// Smallest key whose probability reaches min_p of the largest (0xffffffff:
+// none).  Only candidates within half a binary order of the threshold need an
+// exp: below that their probability is certainly under min_p.
+XV_INLINE uint32_t minp_key(Shared& s, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t, float zmax,
+                            float min_p) {
+  const float d_lo = __log2f(min_p) - 0.5f;
+  uint32_t kminp = 0xffffffffu;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
+    const uint32_t key = order_key(bits);
+    if (!key) return;
+    const float d = log2_ratio(bits, inv_t, zmax);
+    if (d >= d_lo && sampler_exp2(d) >= min_p) kminp = min(kminp, key);
+  });
+  return block_min_u(s, kminp);
+}
+
+// Fast path with top-k: bucket counts only (no exp), then every candidate of
+// the buckets up to the one holding rank k-1 is gathered and sorted; the
+// top-k set, its mass, the top-p and min-p cuts all come from that list.
+XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
+                             float inv_t, float zmax, int top_k, float top_p, float min_p, bool use_p, bool use_m,
+                             uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
+  const int t = threadIdx.x, w = t >> 6;
+  for (int i = t; i < kWaves * kBuckets; i += kThreads) (&fs.wcnt[0][0])[i] = 0u;
+  __syncthreads();
+  int64_t far_c = 0;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
+    if (!order_key(bits)) return;
+    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax));
+    if (bkt < kBuckets - 1) atomicAdd(&fs.wcnt[w][bkt], 1u);
+    else far_c += 1;
+  });
+  far_c = block_sum_l(s, far_c);
+  __syncthreads();
+  if (t < kBuckets) {
+    uint32_t c = 0;
+    for (int ww = 0; ww < kWaves; ++ww) c += fs.wcnt[ww][t];
+    if (t == kBuckets - 1) c += (uint32_t)far_c;
+    s.cnt[t] = c;
+  }
+  __syncthreads();
+  int bk = kBuckets;
+  int64_t upto = 0;  // candidates in buckets 0..bk
+  {
+    int64_t c = 0;
+    for (int bkt = 0; bkt < kBuckets; ++bkt) {
+      c += s.cnt[bkt];
+      if (c >= top_k) { bk = bkt; upto = c; break; }
+    }
+  }
+  if (bk >= kBuckets - 1 || upto > kMaxCand) return false;  // rank k-1 far out or too many: exact row-wide path
+  const uint32_t kminp = use_m ? minp_key(s, row, V, vec_ok, ntiles, inv_t, zmax, min_p) : 0xffffffffu;
+  const int n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bk, 0);
+  if (n > kMaxCand) return false;
+  const int64_t total_k = list_mass_prefix(s, fs, n, top_k, inv_t, zmax);
+  int64_t jcut = (int64_t)top_k - 1;
+  if (use_p) {
+    const int64_t thr = (int64_t)floor((double)top_p * (double)total_k);
+    jcut = min(jcut, list_first_exceed(s, fs, n, 0, thr, inv_t, zmax));
+  }
+  if (use_m && kminp != 0xffffffffu && kminp >= cand_key(fs.cand[n - 1]))
+    jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
+  if (jcut >= n) jcut = n - 1;
+  if (jcut < 0) jcut = 0;
+  const unsigned long long edge = fs.cand[jcut];
+  key_cut = cand_key(edge);
+  id_cut = cand_id(edge);
+  M = list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+  list_kept = (int)jcut + 1;  // the kept set is exactly fs.cand[0, jcut]
+  return true;
+}
+
+// Fast path: kept set = key > key_cut, or key == key_cut and id <= id_cut;
+// M = its mass.  Returns false when a boundary bucket overflowed the list.
+XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
+                             float inv_t, float zmax, int top_k, float top_p, float min_p, bool use_k, bool use_p,
+                             bool use_m, uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
+  const int t = threadIdx.x, w = t >> 6;
+  if (use_k) return topk_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_p, use_m,
+                                  key_cut, id_cut, M, list_kept);
+  // ---- pass 2: every candidate's mass, binned by distance below the max ----
+  for (int i = t; i < kWaves * kBuckets; i += kThreads) {
+    (&fs.wcnt[0][0])[i] = 0u;
+    (&fs.wmass[0][0])[i] = 0ull;
+  }
+  __syncthreads();
+  int64_t far_c = 0, far_m = 0;
+  uint32_t kminp = 0xffffffffu;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
+    const uint32_t key = order_key(bits);
+    if (!key) return;
+    const float d = log2_ratio(bits, inv_t, zmax);
+    const float e = sampler_exp2(d);
+    const int64_t q = mass_of(e);
+    const int bkt = bucket_of(d);
+    if (bkt < kBuckets - 1) {
+      atomicAdd(&fs.wcnt[w][bkt], 1u);
+      atomicAdd(&fs.wmass[w][bkt], (unsigned long long)q);
+    } else {
+      far_c += 1;
+      far_m += q;
+    }
+    if (use_m && e >= min_p) kminp = min(kminp, key);
+  });
+  far_c = block_sum_l(s, far_c);
+  far_m = block_sum_l(s, far_m);
+  if (use_m) kminp = block_min_u(s, kminp);
+  __syncthreads();
+  if (t < kBuckets) {
+    uint32_t c = 0;
+    unsigned long long m = 0;
+    for (int ww = 0; ww < kWaves; ++ww) { c += fs.wcnt[ww][t]; m += fs.wmass[ww][t]; }
+    if (t == kBuckets - 1) { c += (uint32_t)far_c; m += (unsigned long long)far_m; }
+    s.cnt[t] = c;
+    s.mass[t] = m;
+  }
+  __syncthreads();
+  int64_t total = 0;
+  for (int bkt = 0; bkt < kBuckets; ++bkt) total += (int64_t)s.mass[bkt];
+  key_cut = 1u;
+  id_cut = kTieAll;
+  M = total;
+  if (!(use_k || use_p || use_m)) return true;
+
+  // ---- bucket of each cut-off ----
+  int bk = kBuckets;
+  int64_t ck_before = 0, mk_before = 0;
+  if (use_k) {
+    int64_t c = 0, m = 0;
+    for (int bkt = 0; bkt < kBuckets; ++bkt) {
+      if (c + s.cnt[bkt] >= (uint32_t)top_k) { bk = bkt; ck_before = c; mk_before = m; break; }
+      c += s.cnt[bkt];
+      m += (int64_t)s.mass[bkt];
+    }
+  }
+  int64_t total_k = total;
+  int nk = 0;
+  if (bk < kBuckets) {
+    nk = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bk);
+    if (nk > kMaxCand) return false;
+    total_k = mk_before + list_mass_prefix(s, fs, nk, top_k - ck_before, inv_t, zmax);
+  }
+  int bp = kBuckets;
+  int64_t thr = 0, mp_before = 0;
+  if (use_p) {
+    thr = (int64_t)floor((double)top_p * (double)total_k);
+    int64_t m = 0;
+    for (int bkt = 0; bkt < kBuckets; ++bkt) {
+      if (m + (int64_t)s.mass[bkt] > thr) { bp = bkt; mp_before = m; break; }
+      m += (int64_t)s.mass[bkt];
+    }
+  }
+  int bm = kBuckets;
+  if (use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), inv_t, zmax));
+  const int bf = min(bk, min(bp, bm));
+  if (bf >= kBuckets) return true;  // no cut-off limits the row: everything kept
+  int n = nk;
+  if (bf != bk) {
+    n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bf);
+    if (n > kMaxCand) return false;
+  }
+  // ---- exact cut inside the boundary bucket ----
+  int64_t jcut = kTieAll;
+  if (bk == bf) jcut = min(jcut, (int64_t)top_k - ck_before - 1);
+  if (bp == bf) jcut = min(jcut, list_first_exceed(s, fs, n, mp_before, thr, inv_t, zmax));
+  if (bm == bf) jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
+  if (jcut >= n) jcut = n - 1;
+  if (jcut < 0) jcut = 0;
+  int64_t m_before = 0;
+  for (int bkt = 0; bkt < bf; ++bkt) m_before += (int64_t)s.mass[bkt];
+  const unsigned long long edge = fs.cand[jcut];
+  key_cut = cand_key(edge);
+  id_cut = cand_id(edge);
+  M = m_before + list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+  return true;
+}
+
+__global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restrict__ logits, int64_t stride, int V,
+                                                          const float* __restrict__ temps,
+                                                          const float* __restrict__ top_ps,
+                                                          const int32_t* __restrict__ top_ks,
+                                                          const float* __restrict__ min_ps,
+                                                          const float* __restrict__ uniforms, int flags,
+                                                          int64_t* __restrict__ out_ids) {
+  __shared__ Shared s;
+  __shared__ FastShared fs;
+  const int b = blockIdx.x;
+  const int t = threadIdx.x;
+  const bf16_t* row = logits + (int64_t)b * stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int ntiles = (V + kTile - 1) / kTile;
+  const float temp = temps ? temps[b] : 1.0f;
+  const bool greedy = (flags & XV_SAMPLE_ALL_GREEDY) || temp <= 1e-5f;
+
+  // ---- greedy: max value, then the lowest index holding it ----
+  if (greedy) {
+    // one pass: the lane's max and its lowest id, then the block's
+    float fm = -INFINITY;
+    uint32_t best = 0xffffffffu;
+    for_each_strided(row, V, vec_ok, [&](uint32_t bits, int id) {
+      if (!order_key(bits)) return;
+      const float v = bf16_to_f32(bits);
+      if (v > fm) { fm = v; best = (uint32_t)id; }  // ids ascend within a lane: keeps the lowest
+    });
+    const float gm = block_maxf(s, fm);
+    best = block_min_u(s, fm == gm ? best : 0xffffffffu);
+    if (t == 0) out_ids[b] = best == 0xffffffffu ? 0 : (int64_t)best;
+    return;
+  }
+
+  // ---- pass 1: the largest key ----
+  uint32_t kmax = 0;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) { kmax = max(kmax, order_key(bits)); });
+  kmax = block_max_u(s, kmax);
+  const float inv_t = 1.0f / temp;
+  const float zmax = bf16_to_f32(key_to_bits(kmax)) * inv_t;
+
+  const int top_k = ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
+  const float top_p = ((flags & XV_SAMPLE_USE_TOP_P) && top_ps) ? top_ps[b] : 1.0f;
+  const float min_p = ((flags & XV_SAMPLE_USE_MIN_P) && min_ps) ? min_ps[b] : 0.0f;
+  const bool use_k = top_k > 0 && top_k < V;
+  const bool use_p = top_p < 1.0f;
+  const bool use_m = min_p > 0.0f;
+
+  uint32_t key_cut;
+  int64_t id_cut, M;
+  int list_kept = 0;  // > 0: the kept set is the sorted list prefix fs.cand[0, list_kept)
+  if (!fast_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m,
+                     key_cut, id_cut, M, list_kept)) {
+    list_kept = 0;
+    Boundary bd;
+    general_boundary(s, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m, bd, id_cut,
+                     M);
+    key_cut = bd.key;
+  }
+
+  // ---- last pass: inverse-CDF draw in ascending id order (exp for kept ids only) ----
+  // Thread t owns the contiguous ids [t*C, t*C + C), C a multiple of 8, so one
+  // block scan orders the whole row.
   const float u = uniforms ? uniforms[b] : 0.5f;
   int64_t rdraw = (int64_t)((double)u * (double)M);
   if (rdraw >= M) rdraw = M - 1;
   if (rdraw < 0) rdraw = 0;
-  if (t == 0) s.b_id = -1;
-  int64_t carry = 0;
-  for (int j = 0; j < ntiles; ++j) {
-    uint32_t bits[8];
-    const int base = j * kTile + t * 8;
-    load8(row, V, base, vec_ok, bits);
-    int64_t qk[8];
-    int64_t sum = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t key = order_key(bits[k]);
-      const bool kept = key && (key > bd.key || (key == bd.key && (int64_t)(base + k) <= id_cut));
-      qk[k] = kept ? mass_of(exp_of(bits[k], temp, zmax)) : 0;
-      sum += qk[k];
+  if (list_kept > 0) {
+    // The kept set is in LDS: re-key it as (~id << 32 | key), so the
+    // descending sort puts ids in ascending order, then scan its masses.
+    const int n = list_kept;
+    __syncthreads();
+    for (int i = t; i < n; i += kThreads) {
+      const unsigned long long c = fs.cand[i];
+      fs.cand[i] = ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c);
     }
-    int64_t tile_sum;
-    int64_t cum = carry + block_excl_scan(s, sum, &tile_sum);
-    if (cum <= rdraw && rdraw < cum + sum) {
+    __syncthreads();
+    sort_cand_desc(fs, n);
+    auto entry_mass = [&](unsigned long long c) {
+      return mass_of(exp_of(key_to_bits((uint32_t)(c & 0xffffffffu)), inv_t, zmax));
+    };
+    const int per = (n + kThreads - 1) / kThreads;
+    const int j0 = t * per, j1 = min(n, j0 + per);
+    int64_t local = 0;
+    for (int j = j0; j < j1; ++j) local += entry_mass(fs.cand[j]);
+    int64_t tot;
+    int64_t cum = block_excl_scan(s, local, &tot);
+    int64_t found = kTieAll;
+    for (int j = j0; j < j1; ++j) {
+      cum += entry_mass(fs.cand[j]);
+      if (cum > rdraw) { found = 0xffffffffu - (uint32_t)(fs.cand[j] >> 32); break; }
+    }
+    found = block_min_l(s, found);
+    if (t == 0) out_ids[b] = found == kTieAll ? 0 : found;
+    return;
+  }
+  const int C = ((V + kThreads - 1) / kThreads + 7) / 8 * 8;
+  const int i0 = t * C, i1 = min(V, i0 + C);
+  auto kept_mass = [&](uint32_t bits, int id) -> int64_t {
+    const uint32_t key = order_key(bits);
+    const bool kept = key && (key > key_cut || (key == key_cut && (int64_t)id <= id_cut));
+    return kept ? mass_of(exp_of(bits, inv_t, zmax)) : 0;
+  };
+  int64_t mine = 0;
+  for_each_elem(row, V, vec_ok, [&](uint32_t bits, int id) { mine += kept_mass(bits, id); });
+  __syncthreads();
+  if (t == 0) s.b_id = -1;
+  int64_t tot;
+  int64_t cum = block_excl_scan(s, mine, &tot);
+  if (cum <= rdraw && rdraw < cum + mine) {
+    for (int i = i0; i < i1 && s.b_id < 0; i += 8) {
+      uint32_t bits[8];
+      load8(row, V, i, vec_ok, bits);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        cum += qk[k];
-        if (cum > rdraw) { s.b_id = base + k; break; }
+        if (i + k >= i1) break;
+        cum += kept_mass(bits[k], i + k);
+        if (cum > rdraw) { s.b_id = i + k; break; }
       }
     }
-    carry += tile_sum;
-    __syncthreads();
-    if (s.b_id >= 0) break;
   }
+  __syncthreads();
   if (t == 0) out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
 }
 

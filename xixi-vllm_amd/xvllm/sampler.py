@@ -4,7 +4,7 @@ radix-select sampling kernel (one workgroup per row).
 
 Semantics follow the reference: temperature <= 1e-5 rows (or ``all_greedy``)
 take the argmax of the logits (lowest id on ties, as ``argmax``); otherwise
-the logits are divided by the temperature and filtered by top-k, then top-p
+the logits are scaled by 1/temperature and filtered by top-k, then top-p
 and min-p over the renormalised top-k set, keeping at least the best token.
 The reference draws with ``torch.multinomial`` / exponential noise; here the
 draw is an explicit uniform per row (``uniforms``, or ``torch.rand`` from
