@@ -43,7 +43,10 @@ def algo_bytes(ctx: list[int], hq=HQ, hkv=HKV, d=D) -> int:
     return kv + qo + bt + 4 * len(ctx)
 
 
-def make_case(torch, ctx: list[int], layers: int, dev, seed: int):
+def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = "nhd"):
+    """Per layer: q, K pool, V pool, block tables, seqlens.  layout "nhd" is
+    the reference's [NB, BS, Hkv, D] page; "hnd" stores [NB, Hkv, BS, D] and
+    passes the transposed view (same logical shape)."""
     g = torch.Generator().manual_seed(seed)
     need = [(c + PAGE - 1) // PAGE for c in ctx]
     pool = math.ceil(1.25 * sum(need))
@@ -57,8 +60,11 @@ def make_case(torch, ctx: list[int], layers: int, dev, seed: int):
             bt[b, :n] = perm[o : o + n].to(torch.int32)
             o += n
         gd = torch.Generator(device=dev).manual_seed(seed * 100 + layer)
-        kc = torch.randn((pool, PAGE, HKV, D), generator=gd, device=dev).to(torch.bfloat16)
-        vc = torch.randn((pool, PAGE, HKV, D), generator=gd, device=dev).to(torch.bfloat16)
+        shape = (pool, PAGE, HKV, D) if layout == "nhd" else (pool, HKV, PAGE, D)
+        kc = torch.randn(shape, generator=gd, device=dev).to(torch.bfloat16)
+        vc = torch.randn(shape, generator=gd, device=dev).to(torch.bfloat16)
+        if layout == "hnd":
+            kc, vc = kc.transpose(1, 2), vc.transpose(1, 2)
         q = torch.randn((len(ctx), HQ * D), generator=gd, device=dev).to(torch.bfloat16)
         cases.append((q, kc, vc, bt.to(dev), torch.tensor(ctx, dtype=torch.int32, device=dev)))
     return cases

@@ -9,16 +9,17 @@
 // merged by a second kernel through an fp32 workspace (normalised partial
 // output + log2-sum-exp).  A segment inside one range is written directly.
 // All G = Hq/Hkv query heads of a kv head are served by one pass.  Per page:
-//   K (HBM -> VGPR) is the A operand of S^T = K Q^T on v_mfma_f32_16x16x32_bf16:
-//     lane = 16*g + i: row i = token i, MFMA step s contracts d-chunk 4s+g, so
-//     the four lanes of a token read 64 contiguous bytes per load instruction.
+//   K and V go HBM -> LDS by LDS-DMA, whole 256-byte rows per instruction,
+//   into a swizzled image (conflict-free reads below).
+//   K (LDS -> VGPR) is the A operand of S^T = K Q^T on v_mfma_f32_16x16x32_bf16:
+//     lane = 16*g + i: row i = token i, MFMA step s contracts d-chunk 4s+g.
 //   Q^T is the B operand: column c = lane%16 holds query head c % G.
 //   S^T lands as acc[r] = S[head c%G][token 4g+r]; the online softmax reduces
 //   the 4 tokens in-lane and the 4 lane rows with two cross-row shuffles.
 //   P (bf16) is then already the A operand of O = P V on
 //   v_mfma_f32_16x16x16_bf16 (row = head, k = token 4g+j): no shuffle.
-//   V (HBM -> VGPR -> LDS, rows padded to 288 B) is read back transposed with
-//   ds_read_b64_tr_b16 as the B operand (k = token, column = d), 8 d-tiles.
+//   V is read from LDS transposed with ds_read_b64_tr_b16 as the B operand
+//   (k = token, column = d), 8 d-tiles.
 //   O accumulates in the MFMA output layout: 8 tiles x 4 fp32 per lane.
 #include "xv_common.h"
 #include "xv_kernels.h"
@@ -31,7 +32,7 @@ constexpr int kD = 128;
 constexpr int kPage = 16;
 constexpr int kVPageBytes = 4096;  // one page's V rows of one kv head in LDS
 #ifndef XV_DECODE_NBUF
-#define XV_DECODE_NBUF 6
+#define XV_DECODE_NBUF 4
 #endif
 constexpr int kNbuf = XV_DECODE_NBUF;
 #ifndef XV_DECODE_WAVES_PER_CU
@@ -56,20 +57,27 @@ struct DecodeArgs {
   float scale_log2;
 };
 
-struct PageRegs {
-  Vec8 k[4];  // K rows of the page in MFMA A-operand layout (V goes straight to LDS)
-};
-
-// A page's K rows are read with buffer loads into VGPRs and its V rows with
-// buffer loads straight into LDS (LDS-DMA: lane l's 16 bytes land at
-// base + 16*l), so V never occupies VGPRs.  The page base is wave uniform (a
-// scalar resource per page) and the per-lane offset
-// t*tok_stride + 8*g (+32*s) is the same for every page (any page layout with
-// 256-byte head rows works: [BS][Hkv][D] as the reference pool, or [Hkv][BS][D]).
-// The resource covers only the page's valid rows: rows past the sequence end
-// read as zeros, so garbage (even NaN) in unused cache slots never reaches P.V.
+// Both K and V of a page travel HBM -> LDS by LDS-DMA (buffer_load ... lds:
+// lane l's 16 bytes land at base + 16*l), so no page data passes through
+// VGPRs before it is needed and the compiler never has to wait for a page
+// load: the only wait on page data is the explicit vmcnt in process_page.
+//
+// LDS image of one page of one kv head (4 KB for K, 4 KB for V): token t's
+// 256-byte row at t*256, its 16-byte chunk c in slot c ^ swz(t).  The swizzle
+// makes the 16 tokens of a K read (same chunk) and the 8 tokens of each half
+// of a transposed V read land in distinct banks.
+// Load instruction s (0..3) moves tokens 4s..4s+3 as four whole 256-byte rows
+// (lane l: token 4s + l/16, slot l%16, i.e. chunk (l%16) ^ swz(t)), so every
+// instruction reads full rows whatever the page layout ([BS][Hkv][D] as the
+// reference pool, or [Hkv][BS][D]).  The page base is wave uniform (a scalar
+// buffer resource per page) covering only the page's valid rows: rows past
+// the sequence end read as zeros, so garbage (even NaN) in unused cache slots
+// never reaches P.V.
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kPageLds = 2 * kVPageBytes;  // K then V
+
+XV_INLINE int swz(int t) { return ((t & 7) << 1) | (t >> 3); }
 
 // base and bytes are wave uniform: readfirstlane lets the compiler keep the
 // resource in SGPRs (otherwise it emits a per-lane "waterfall" loop).
@@ -81,21 +89,43 @@ XV_INLINE __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(q, (short)0, (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
-// V LDS layout of one page (4 KB): chunk c = 4s+g of token t at s*1024 + g*256 + t*16.
-XV_INLINE void issue_page(PageRegs& r, char* vbuf, const DecodeArgs& a, int page, int kvh, int valid_rows,
-                          int lane_off) {
+// Per-lane offsets, fixed for the whole kernel.
+struct LaneOffsets {
+  int g[4];  // global byte offset of load instruction s within a page
+  uint32_t k[4];  // LDS byte offset of this lane's K A-operand chunk for MFMA step s
+  uint32_t v[8];  // LDS byte offset (V half) of this lane's transposed read for O tile n
+};
+
+XV_INLINE LaneOffsets lane_offsets(int64_t tok_stride, int lane) {
+  LaneOffsets o;
+  const int i = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int t = 4 * s + g;
+    o.g[s] = (int)(t * tok_stride * 2) + ((i ^ swz(t)) << 4);
+    // K A operand of step s: row = token i, d-chunk 4s + g
+    o.k[s] = (uint32_t)(i * 256 + (((4 * s + g) ^ swz(i)) << 4));
+  }
+  // V B operand of tile n: lane (g, i) supplies token 4g + i/4, columns
+  // 16n + 4(i%4) .. +3 = chunk 2n + (i%4)/2, bytes 8*(i%2) of it
+  const int t = 4 * g + (i >> 2);
+#pragma unroll
+  for (int n = 0; n < 8; ++n)
+    o.v[n] = (uint32_t)(kVPageBytes + t * 256 + (((2 * n + ((i & 3) >> 1)) ^ swz(t)) << 4) + 8 * (i & 1));
+  return o;
+}
+
+XV_INLINE void issue_page(char* buf, const DecodeArgs& a, int page, int kvh, int valid_rows,
+                          const LaneOffsets& lo) {
   const int64_t base = (int64_t)page * a.page_stride + (int64_t)kvh * a.head_stride;
   const uint32_t bytes = (uint32_t)(((int64_t)(valid_rows - 1) * a.tok_stride + kD) * 2);
   const __amdgpu_buffer_rsrc_t rk = page_rsrc(a.kc + base, bytes);
   const __amdgpu_buffer_rsrc_t rv = page_rsrc(a.vc + base, bytes);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    u32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off + 64 * s, 0, 0);
-    r.k[s].w[0] = v[0]; r.k[s].w[1] = v[1]; r.k[s].w[2] = v[2]; r.k[s].w[3] = v[3];
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + 1024 * s), 16, lo.g[s], 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kVPageBytes + 1024 * s), 16, lo.g[s], 0, 0, 0);
   }
-#pragma unroll
-  for (int s = 0; s < 4; ++s)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(vbuf + 1024 * s), 16, lane_off + 64 * s, 0, 0, 0);
 }
 
 XV_INLINE bf16x8_t as_bf16x8(const Vec8& v) {
@@ -110,77 +140,99 @@ struct SplitState {
   floatx4_t o[8];  // O tile n: rows 4g+r (head (4g+r)%G), column d = 16n + lane%16
 };
 
+constexpr float kLazy = 8.0f;
+
+// O row 4g+RR *= alpha of its head (4g+RR)%G, read from that lane of the row.
+template <int G, int RR>
+XV_INLINE void rescale_row(SplitState& st, float alpha, int g) {
+  float ar;
+  if constexpr (G == 8) ar = (g & 1) ? row_bcast<(4 + RR) % 8>(alpha) : row_bcast<RR % 8>(alpha);
+  else ar = row_bcast<RR % G>(alpha);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.o[n][RR] *= ar;
+}
+
 template <int G>
-XV_INLINE void process_page(SplitState& st, const PageRegs& r, const char* vbuf, const bf16x8_t (&qb)[4],
+XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
                             int page_tok0, int ctx, float scale_log2, int lane) {
-  const int i = lane & 15, g = lane >> 4;
+  const int g = lane >> 4;
+  // The page arrived by LDS-DMA; the 8 VMEM operations of each of the
+  // kNbuf-1 pages issued after it may still be in flight: vmcnt(8*(kNbuf-1))
+  // waits exactly for this page.  Waits and reads are one asm block so that
+  // the compiler, which cannot tell the LDS buffers apart, adds no wait of
+  // its own on the loads in flight.
+  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+  bf16x8_t kr[4];
+  short4_t vt[8];
+  __asm__ __volatile__(
+      "s_waitcnt vmcnt(%24)\n\t"
+      "ds_read_b128 %0, %12\n\t"
+      "ds_read_b128 %1, %13\n\t"
+      "ds_read_b128 %2, %14\n\t"
+      "ds_read_b128 %3, %15\n\t"
+      "ds_read_b64_tr_b16 %4, %16\n\t"
+      "ds_read_b64_tr_b16 %5, %17\n\t"
+      "ds_read_b64_tr_b16 %6, %18\n\t"
+      "ds_read_b64_tr_b16 %7, %19\n\t"
+      "ds_read_b64_tr_b16 %8, %20\n\t"
+      "ds_read_b64_tr_b16 %9, %21\n\t"
+      "ds_read_b64_tr_b16 %10, %22\n\t"
+      "ds_read_b64_tr_b16 %11, %23\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(kr[0]), "=&v"(kr[1]), "=&v"(kr[2]), "=&v"(kr[3]), "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]),
+        "=&v"(vt[3]), "=&v"(vt[4]), "=&v"(vt[5]), "=&v"(vt[6]), "=&v"(vt[7])
+      : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),
+        "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),
+        "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7]), "n"(8 * (kNbuf - 1))
+      : "memory");
   // ---- S^T = K Q^T ----
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(r.k[s]), qb[s], acc, 0, 0, 0);
+  for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kr[s], qb[s], acc, 0, 0, 0);
   // ---- online softmax for head c%G over tokens 4g..4g+3 ----
   float sc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) sc[j] = (page_tok0 + 4 * g + j < ctx) ? acc[j] * scale_log2 : -INFINITY;
   float mx = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-  mx = fmaxf(mx, __shfl_xor(mx, 16));
-  mx = fmaxf(mx, __shfl_xor(mx, 32));
+  mx = xor32_max(xor16_max(mx));
+  // Lazy rescaling: the running max used for exp2 only moves when some head's
+  // max grew by more than kLazy (p <= 2^kLazy meanwhile, exact after the
+  // final 1/l).  Random or trained logits settle within a few pages, after
+  // which the O rescale (32 accumulator reads/writes) is skipped.
   const float m_new = fmaxf(st.m, mx);
-  const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
-  st.m = m_new;
+  if (__any(m_new > st.m + kLazy)) {
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.m = m_new;
+    st.l *= alpha;
+    rescale_row<G, 0>(st, alpha, g);
+    rescale_row<G, 1>(st, alpha, g);
+    rescale_row<G, 2>(st, alpha, g);
+    rescale_row<G, 3>(st, alpha, g);
+  }
   float p[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - m_new);
-  st.l = st.l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+  for (int j = 0; j < 4; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - st.m);
+  st.l += (p[0] + p[1]) + (p[2] + p[3]);
   short4_t pa;
 #pragma unroll
   for (int j = 0; j < 4; ++j) pa[j] = (short)f32_to_bf16(p[j]);
-  // rescale O rows: row 4g+rr holds head (4g+rr)%G, whose alpha sits in lane (row base)|head
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int hsrc = (4 * g + rr) % G;
-    const float ar = __shfl(alpha, (lane & 48) | hsrc);
-#pragma unroll
-    for (int n = 0; n < 8; ++n) st.o[n][rr] *= ar;
-  }
-  // ---- O += P V, V^T tiles read transposed from the page's LDS copy ----
-  // tile n = d 16n..16n+15 = chunks 2n, 2n+1; lane (g, i) supplies token
-  // 4g + i/4, columns 16n + 4(i%4) .. +3
-  const char* vb = vbuf + ((i & 3) >> 1) * 256 + (4 * g + (i >> 2)) * 16 + 8 * (i & 1);
-  // The page's V arrived by LDS-DMA; the 8 VMEM operations of each of the
-  // kNbuf-1 pages issued after it may still be in flight: vmcnt(8*(kNbuf-1))
-  // waits exactly for this page.  The reads are one asm block so that the compiler, which
-  // cannot tell the two LDS buffers apart, does not wait for everything.
-  short4_t vt[8];
-  const uint32_t va = (uint32_t)reinterpret_cast<uintptr_t>(vb);
-  __asm__ __volatile__(
-      "s_waitcnt vmcnt(%9)\n\t"
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %8 offset:512\n\t"
-      "ds_read_b64_tr_b16 %2, %8 offset:1024\n\t"
-      "ds_read_b64_tr_b16 %3, %8 offset:1536\n\t"
-      "ds_read_b64_tr_b16 %4, %8 offset:2048\n\t"
-      "ds_read_b64_tr_b16 %5, %8 offset:2560\n\t"
-      "ds_read_b64_tr_b16 %6, %8 offset:3072\n\t"
-      "ds_read_b64_tr_b16 %7, %8 offset:3584\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]), "=&v"(vt[3]), "=&v"(vt[4]), "=&v"(vt[5]), "=&v"(vt[6]), "=&v"(vt[7])
-      : "v"(va), "n"(8 * (kNbuf - 1))
-      : "memory");
+  // ---- O += P V ----
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
 }
+
+// Pages of one segment whose ids are held in lanes at a time (kIdWindow/64 per lane).
+constexpr int kIdWindow = 256;
 
 // Attention of one (sequence b, kv head) over pages [pb, pe) of the sequence.
 // full: the range holds the whole sequence -> final bf16 output; otherwise the
 // normalised partial and its log2-sum-exp go to partial slot `part`.
 template <int G>
-XV_INLINE void decode_segment(const DecodeArgs& a, int b, int kvh, int pb, int pe, bool full, int part, char* lds,
-                              int lane) {
+XV_INLINE void decode_segment(const DecodeArgs& a, const LaneOffsets& lo, int b, int kvh, int pb, int pe, bool full,
+                              int part, char* lds, int lane) {
   const int i = lane & 15, g = lane >> 4;
   const int head0 = kvh * G;
   const int ctx = a.seqlens[b];
-  const int npages = (ctx + kPage - 1) / kPage;
 
   bf16x8_t qb[4];
   {
@@ -194,31 +246,41 @@ XV_INLINE void decode_segment(const DecodeArgs& a, int b, int kvh, int pb, int p
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int lane_off = (int)((int64_t)i * a.tok_stride * 2 + 16 * g);
-  for (int c0 = pb; c0 < pe; c0 += 64) {
-    const int np = min(64, pe - c0);
-    // page ids of this chunk, one per lane, broadcast with readlane
-    int pid = 0;
-    if (lane < np) pid = a.bt[(int64_t)b * a.bt_stride + c0 + lane];
-    // kNbuf page buffers (K in VGPRs, V in LDS): kNbuf-1 pages are always in
-    // flight ahead of the one being processed.  Prefetches are issued
-    // unconditionally (clamped to the chunk's last page) so the number of VMEM
-    // operations after any page is fixed, which the LDS wait in process_page
-    // relies on.
-    PageRegs r[kNbuf];
+  for (int c0 = pb; c0 < pe; c0 += kIdWindow) {
+    const int np = min(kIdWindow, pe - c0);
+    // page ids of this window: page c0 + 64w + lane in pid<w> (four scalars,
+    // not an array, so they stay in VGPRs)
+    static_assert(kIdWindow == 256, "four id registers per lane");
+    const int32_t* btb = a.bt + (int64_t)b * a.bt_stride + c0 + lane;
+    const int pid0 = lane < np ? btb[0] : 0;
+    const int pid1 = 64 + lane < np ? btb[64] : 0;
+    const int pid2 = 128 + lane < np ? btb[128] : 0;
+    const int pid3 = 192 + lane < np ? btb[192] : 0;
+    auto page_of = [pid0, pid1, pid2, pid3](int x) {  // x wave uniform
+      // read all four, select among scalars: an indexed select would be
+      // turned into an LDS array
+      const int l = x & 63;
+      const int r0 = __builtin_amdgcn_readlane(pid0, l), r1 = __builtin_amdgcn_readlane(pid1, l);
+      const int r2 = __builtin_amdgcn_readlane(pid2, l), r3 = __builtin_amdgcn_readlane(pid3, l);
+      return x < 128 ? (x < 64 ? r0 : r1) : (x < 192 ? r2 : r3);
+    };
     auto rows = [&](int pg) { return min(kPage, ctx - pg * kPage); };
+    // kNbuf page buffers: kNbuf-1 pages are always in flight ahead of the one
+    // being processed.  Prefetches are issued unconditionally (clamped to the
+    // window's last page) so the number of VMEM operations after any page is
+    // fixed, which the wait in process_page relies on.
 #pragma unroll
     for (int k = 0; k < kNbuf - 1; ++k) {
       const int nk = min(k, np - 1);
-      issue_page(r[k], lds + k * kVPageBytes, a, __builtin_amdgcn_readlane(pid, nk), kvh, rows(c0 + nk), lane_off);
+      issue_page(lds + k * kPageLds, a, page_of(nk), kvh, rows(c0 + nk), lo);
     }
     for (int it = 0; it < np; it += kNbuf) {
 #pragma unroll
       for (int u = 0; u < kNbuf; ++u) {
         const int ahead = (u + kNbuf - 1) % kNbuf;
         const int na = min(it + u + kNbuf - 1, np - 1);
-        issue_page(r[ahead], lds + ahead * kVPageBytes, a, __builtin_amdgcn_readlane(pid, na), kvh, rows(c0 + na), lane_off);
-        if (it + u < np) process_page<G>(st, r[u], lds + u * kVPageBytes, qb, (c0 + it + u) * kPage, ctx, a.scale_log2, lane);
+        issue_page(lds + ahead * kPageLds, a, page_of(na), kvh, rows(c0 + na), lo);
+        if (it + u < np) process_page<G>(st, lds + u * kPageLds, lo, qb, (c0 + it + u) * kPage, ctx, a.scale_log2, lane);
       }
     }
   }
@@ -253,6 +315,10 @@ XV_INLINE void decode_segment(const DecodeArgs& a, int b, int kvh, int pb, int p
 
 constexpr int kMaxBatch = 256;  // sequences per launch (larger batches are launched in chunks)
 
+#ifndef XV_DECODE_OVERSUB
+#define XV_DECODE_OVERSUB 1  // ranges per resident wave slot
+#endif
+
 #ifndef XV_DECODE_WPE
 #define XV_DECODE_WPE 1  // waves per SIMD the register budget is fitted to
 #endif
@@ -263,9 +329,15 @@ XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
   return (int)max((int64_t)a.lmin, per);
 }
 
+// Timing hook for out-of-tree instrumentation builds; empty in the library.
+#ifndef XV_DECODE_TIMESTAMP
+#define XV_DECODE_TIMESTAMP(slot)
+#endif
+
 template <int G>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WPE, XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[kNbuf * kVPageBytes];
+  XV_DECODE_TIMESTAMP(0);
+  __shared__ __attribute__((aligned(16))) char lds[kNbuf * kPageLds];
   __shared__ int pref[kMaxBatch + 1];  // pages of sequences 0..b-1
   const int lane = threadIdx.x;
   // prefix sums of the page counts (every wave computes them; B <= 1024)
@@ -286,8 +358,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   __syncthreads();  // single wave: orders the LDS prefix writes before the reads
   const int64_t total = (int64_t)a.hkv * carry;
   const int L = range_pages(a, total);
+  const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
   int64_t f = (int64_t)blockIdx.x * L;
   const int64_t f1 = min(f + L, total);
+  XV_DECODE_TIMESTAMP(1);
   while (f < f1) {
     // sequence b holding flat page f: largest b with hkv*pref[b] <= f
     int lo = 0, hi = a.batch - 1;
@@ -304,9 +378,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
     const int64_t e = min(f1, seg1);
     const bool full = (f == seg0) && (e == seg1);
     const int part = (int)(blockIdx.x - seg0 / L);
-    decode_segment<G>(a, b, kvh, (int)(f - seg0), (int)(e - seg0), full, part, lds, lane);
+    decode_segment<G>(a, offs, b, kvh, (int)(f - seg0), (int)(e - seg0), full, part, lds, lane);
     f = e;
   }
+  XV_DECODE_TIMESTAMP(2);
 }
 
 // Merge the partials of one (sequence, query head): 64 lanes x 2 dims.  Also
@@ -421,7 +496,7 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin;
   // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_blocks_per_seq;
-  a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
+  a.nwaves = (int)min((int64_t)waves_for(group) * XV_DECODE_OVERSUB, (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
   switch (group) {
     case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;

@@ -75,6 +75,24 @@ XV_INLINE float row16_max(float x) {
   x = fmaxf(x, dpp_f<0xB1>(x));
   return x;
 }
+// max(x[l], x[l ^ 16]) and max(x[l], x[l ^ 32]) with the gfx950 row-swap
+// permutes (VALU, no LDS round trip).  permlane16_swap exchanges the odd
+// 16-lane rows of its first operand with the even rows of its second, so with
+// both operands = x each lane ends up holding x[l] in one result and
+// x[l ^ 16] in the other; permlane32_swap does the same across halves.
+XV_INLINE float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+XV_INLINE float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Lane n of each 16-lane row, broadcast to the row (DPP row_newbcast).
+template <int N>
+XV_INLINE float row_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + N, 0xf, 0xf, false));
+}
 // Full wave64 reductions (result valid in every lane).
 XV_INLINE float wave_sum(float x) {
   x = row16_sum(x);
