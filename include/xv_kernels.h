@@ -57,15 +57,17 @@ int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
  *   block_tables : int32 [B, bt_stride]; only the first ceil(seqlen/block_size) entries are read
  *   cache_seqlens: int32 [B]; 0 marks a padding row whose output is written as zeros
  *   out    : element (b, h, d) at b*out_stride_tok + h*D + d
- *   workspace: at least xv_paged_decode_workspace_size(...) bytes: fp32 partial
- *              outputs (and their log2-sum-exp) of sequences split across waves,
- *              merged by a second kernel.  Calls sharing a workspace must be
- *              ordered on one stream.
+ *   workspace: at least xv_paged_decode_workspace_size(...) bytes: per-segment
+ *              partial counts, then fp32 partial outputs (and their
+ *              log2-sum-exp) of sequences split across waves, merged by a
+ *              second kernel.  No initial contents are required.  Calls
+ *              sharing a workspace must be ordered on one stream.
  * Query head h reads kv head h / (Hq / Hkv).  scale multiplies q.k (1/sqrt(D) in the reference).
  * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16, batch <= 256,
  * head rows of 256 contiguous bytes with head_stride*(Hkv-1) + D <= tok_stride
  * or tok_stride == D (the reference's [page][token][head][d] pool, or a
- * [page][head][token][d] pool).
+ * [page][head][token][d] pool).  q, k_cache, v_cache 16-byte aligned and every
+ * stride a multiple of 8 elements (rows move by 16-byte LDS-DMA).
  */
 size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                       int max_blocks_per_seq, int block_size, int head_dim);

@@ -90,6 +90,52 @@ def test_paged_decode_config2_full_size(dev):
     assert np.isfinite(got).all()
 
 
+def test_paged_decode_many_short_sequences(dev):
+    """256 sequences of 0..40 tokens: wave ranges cross many segments shorter
+    than the page pipeline, with empty (padding) rows among them."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = gen(77)
+    ctx = torch.randint(0, 41, (256,), generator=g).tolist()
+    ctx[5] = ctx[200] = 0
+    need = sum((c + 15) // 16 for c in ctx)
+    kc, vc, bt, sl = make_paged(ctx, int(need * 1.25) + 4, 8, 128, g)
+    q = randn_bf16((256, 32, 128), g)
+    want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
+    out = paged_decode_attention(q.view(256, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), 32, 8, 128)
+    torch.cuda.synchronize()
+    _close(f32(out).reshape(256, 32, 128), want)
+
+
+def test_paged_decode_long_ranges(dev):
+    """B 64 x ctx 8192: each wave streams ~256 pages, crossing page-id table
+    windows.  K/V are drawn on the device; the oracle gets only the pages of
+    the checked rows."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    bsz, ctxlen, hq, hkv, d = 64, 8192, 32, 8, 128
+    npg = ctxlen // 16
+    pool = bsz * npg + 7
+    kc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=gen(6))[: bsz * npg].to(torch.int32)
+    bt = perm.view(bsz, npg).to(dev)
+    sl = torch.full((bsz,), ctxlen, dtype=torch.int32, device=dev)
+    sl[3] = ctxlen - 5
+    q = torch.randn((bsz, hq * d), generator=g, device=dev).to(torch.bfloat16)
+    out = paged_decode_attention(q, kc, vc, bt, sl, hq, hkv, d)
+    torch.cuda.synchronize()
+    rows = [0, 3, 40, 63]
+    for r in rows:
+        pages = bt[r].long()
+        kr, vr = f32(kc[pages].cpu()), f32(vc[pages].cpu())
+        want = O.paged_decode_attention(f32(q[r : r + 1].cpu()).reshape(1, hq, d), kr, vr,
+                                        np.arange(npg, dtype=np.int32)[None, :], np.array([int(sl[r])]))
+        _close(f32(out[r : r + 1].cpu()).reshape(1, hq, d), want)
+    assert torch.isfinite(out.float()).all()
+
+
 @pytest.mark.parametrize("rows,hidden", [(7, 4096), (64, 1024), (33, 128), (3, 5120), (2, 4104)])
 def test_rmsnorm(dev, rows, hidden):
     g = gen(rows)

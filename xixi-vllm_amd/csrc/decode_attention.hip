@@ -31,13 +31,9 @@ namespace {
 constexpr int kD = 128;
 constexpr int kPage = 16;
 constexpr int kVPageBytes = 4096;  // one page's V rows of one kv head in LDS
-#ifndef XV_DECODE_NBUF
-#define XV_DECODE_NBUF 4
-#endif
-constexpr int kNbuf = XV_DECODE_NBUF;
 #ifndef XV_DECODE_WAVES_PER_CU
 #define XV_DECODE_WAVES_PER_CU 4  // one wave per SIMD: no oldest-first starvation between waves
-#endif  // pages in registers/LDS per wave (kNbuf-1 in flight ahead)
+#endif
 
 typedef short short4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4_t lds_short4;
@@ -50,6 +46,7 @@ struct DecodeArgs {
   const int32_t* seqlens;
   bf16_t* out; int64_t out_st;
   float* ws_o; float* ws_lse;
+  int* ws_nparts;  // partials per (sequence, kv head), written by the wave holding the segment's last page
   int batch, hq, hkv, group;
   int lmin;       // minimum pages per wave range
   int max_parts;  // partial slots per (sequence, head) in the workspace
@@ -142,22 +139,28 @@ struct SplitState {
 
 constexpr float kLazy = 8.0f;
 
-// O row 4g+RR *= alpha of its head (4g+RR)%G, read from that lane of the row.
+// Value of head (4g+RR)%G -- the head of O row 4g+RR -- for a per-head value
+// that is equal across the four 16-lane rows: lane (4g+RR)%G of this row.
+template <int G, int RR>
+XV_INLINE float head_of_row(float x, int g) {
+  if constexpr (G == 8) return (g & 1) ? row_bcast<(4 + RR) % 8>(x) : row_bcast<RR % 8>(x);
+  else return row_bcast<RR % G>(x);
+}
+
+// O row 4g+RR *= alpha of its head.
 template <int G, int RR>
 XV_INLINE void rescale_row(SplitState& st, float alpha, int g) {
-  float ar;
-  if constexpr (G == 8) ar = (g & 1) ? row_bcast<(4 + RR) % 8>(alpha) : row_bcast<RR % 8>(alpha);
-  else ar = row_bcast<RR % G>(alpha);
+  const float ar = head_of_row<G, RR>(alpha, g);
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n][RR] *= ar;
 }
 
-template <int G>
+template <int G, int NB>
 XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
                             int page_tok0, int ctx, float scale_log2, int lane) {
   const int g = lane >> 4;
   // The page arrived by LDS-DMA; the 8 VMEM operations of each of the
-  // kNbuf-1 pages issued after it may still be in flight: vmcnt(8*(kNbuf-1))
+  // NB-1 pages issued after it may still be in flight: vmcnt(8*(NB-1))
   // waits exactly for this page.  Waits and reads are one asm block so that
   // the compiler, which cannot tell the LDS buffers apart, adds no wait of
   // its own on the loads in flight.
@@ -183,7 +186,7 @@ XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& 
         "=&v"(vt[3]), "=&v"(vt[4]), "=&v"(vt[5]), "=&v"(vt[6]), "=&v"(vt[7])
       : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),
         "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),
-        "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7]), "n"(8 * (kNbuf - 1))
+        "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7]), "n"(8 * (NB - 1))
       : "memory");
   // ---- S^T = K Q^T ----
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -221,103 +224,177 @@ XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& 
   for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
 }
 
-// Pages of one segment whose ids are held in lanes at a time (kIdWindow/64 per lane).
-constexpr int kIdWindow = 256;
+// Stream positions per half of the page-id table.
+constexpr int kIdWindow = 128;
 
-// Attention of one (sequence b, kv head) over pages [pb, pe) of the sequence.
-// full: the range holds the whole sequence -> final bf16 output; otherwise the
-// normalised partial and its log2-sum-exp go to partial slot `part`.
-template <int G>
-XV_INLINE void decode_segment(const DecodeArgs& a, const LaneOffsets& lo, int b, int kvh, int pb, int pe, bool full,
-                              int part, char* lds, int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const int head0 = kvh * G;
-  const int ctx = a.seqlens[b];
+// Uniform position of a page in the flat (sequence, kv head, page) space.
+struct Cursor {
+  int b, kvh, pg;  // sequence, kv head, page within the sequence
+  int npb, ctx;    // pages and tokens of sequence b
+};
 
-  bf16x8_t qb[4];
-  {
-    const bf16_t* qp = a.q + (int64_t)b * a.q_st + (int64_t)(head0 + (i % G)) * a.q_sh + 8 * g;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qb[s] = as_bf16x8(load_vec8(qp + 32 * s));
+// The next page of the flat space.  Sequences without pages (cache_seqlens
+// 0) hold no flat positions and are stepped over; the caller only advances
+// while a next page exists, and the loop is bounded by the batch regardless.
+XV_INLINE void advance(Cursor& c, const int* pref, const int* sl, int hkv, int batch) {
+  if (++c.pg < c.npb) return;
+  c.pg = 0;
+  if (++c.kvh < hkv) return;
+  c.kvh = 0;
+  do {
+    ++c.b;
+    c.npb = __builtin_amdgcn_readfirstlane(pref[c.b + 1] - pref[c.b]);
+  } while (c.npb == 0 && c.b < batch - 1);
+  c.ctx = __builtin_amdgcn_readfirstlane(sl[c.b]);
+}
+
+// Sequence holding flat page f: the largest b with hkv*pref[b] <= f.
+XV_INLINE int seq_of(const int* pref, int batch, int hkv, int64_t f) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)hkv * pref[mid] <= f) lo = mid; else hi = mid - 1;
   }
-  SplitState st;
+  return lo;
+}
+
+// q rows of one (sequence, kv head): G rows of 256 B in LDS, row h at h*256.
+// One LDS-DMA instruction moves 4 rows (1 KB); rows past G read as zeros.
+template <int G> constexpr int kQSlot = G <= 4 ? 1024 : G * 256;
+template <int G> constexpr int kBufBytes = kPageLds + kQSlot<G>;
+// Page buffers per wave: 4 (3 at G = 8) keeps four waves' LDS within a CU.
+template <int G> constexpr int kNbufG = G <= 4 ? 4 : 3;
+
+template <int G>
+XV_INLINE void issue_q(char* slot, const DecodeArgs& a, int b, int kvh, int lane) {
+  const bf16_t* base = a.q + (int64_t)b * a.q_st + (int64_t)kvh * G * a.q_sh;
+  const uint32_t bytes = (uint32_t)(((int64_t)(G - 1) * a.q_sh + kD) * 2);
+  const __amdgpu_buffer_rsrc_t rq = page_rsrc(base, bytes);
+#pragma unroll
+  for (int j = 0; j < (G + 3) / 4; ++j) {
+    const int row = 4 * j + (lane >> 4);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)(slot + 1024 * j), 16,
+                                             (int)(row * a.q_sh * 2) + ((lane & 15) << 4), 0, 0, 0);
+  }
+}
+
+// Q^T B operand of MFMA step s from the q slot: column i holds head i % G,
+// k = d-chunk 4s + g.  The slot arrived with the page it was issued with:
+// the same vmcnt as that page's wait covers it.
+template <int G, int NB>
+XV_INLINE void read_q(bf16x8_t (&qb)[4], const char* slot, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const uint32_t a0 = (uint32_t)reinterpret_cast<uintptr_t>(slot) + (i % G) * 256 + g * 16;
+  __asm__ __volatile__(
+      "s_waitcnt vmcnt(%5)\n\t"
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %4 offset:64\n\t"
+      "ds_read_b128 %2, %4 offset:128\n\t"
+      "ds_read_b128 %3, %4 offset:192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(qb[0]), "=&v"(qb[1]), "=&v"(qb[2]), "=&v"(qb[3])
+      : "v"(a0), "n"(8 * (NB - 1))
+      : "memory");
+}
+
+// Write the finished segment (b, kvh): bf16 output if this wave covered the
+// whole segment, else the normalised partial and its log2-sum-exp in slot part.
+template <int G, int RR>
+XV_INLINE void finish_row(const DecodeArgs& a, const SplitState& st, float lsum, int b, int head0, bool full,
+                          int part, int lane) {
+  const int i = lane & 15, g = lane >> 4;
+  const float lh = head_of_row<G, RR>(lsum, g);
+  const float mh = head_of_row<G, RR>(st.m, g);
+  const int row = 4 * g + RR;
+  if (row >= G) return;  // rows past G are replicas
+  const float inv = 1.0f / lh;
+  const int head = head0 + row;
+  if (full) {
+    bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[16 * n] = (bf16_t)f32_to_bf16(st.o[n][RR] * inv);
+  } else {
+    const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_parts + part;
+    float* o = a.ws_o + wrow * kD + i;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) o[16 * n] = st.o[n][RR] * inv;
+    if (i == 0) a.ws_lse[wrow] = mh + __log2f(lh);
+  }
+}
+
+template <int G>
+XV_INLINE void finish_segment(const DecodeArgs& a, const SplitState& st, int b, int kvh, bool full, int part,
+                              int lane) {
+  // total p-sum of head c%G over the four rows
+  float lsum = xor16_sum(st.l);
+  lsum = xor32_sum(lsum);
+  finish_row<G, 0>(a, st, lsum, b, kvh * G, full, part, lane);
+  finish_row<G, 1>(a, st, lsum, b, kvh * G, full, part, lane);
+  finish_row<G, 2>(a, st, lsum, b, kvh * G, full, part, lane);
+  finish_row<G, 3>(a, st, lsum, b, kvh * G, full, part, lane);
+}
+
+XV_INLINE void reset(SplitState& st) {
   st.m = -INFINITY;
   st.l = 0.f;
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+}
 
-  for (int c0 = pb; c0 < pe; c0 += kIdWindow) {
-    const int np = min(kIdWindow, pe - c0);
-    // page ids of this window: page c0 + 64w + lane in pid<w> (four scalars,
-    // not an array, so they stay in VGPRs)
-    static_assert(kIdWindow == 256, "four id registers per lane");
-    const int32_t* btb = a.bt + (int64_t)b * a.bt_stride + c0 + lane;
-    const int pid0 = lane < np ? btb[0] : 0;
-    const int pid1 = 64 + lane < np ? btb[64] : 0;
-    const int pid2 = 128 + lane < np ? btb[128] : 0;
-    const int pid3 = 192 + lane < np ? btb[192] : 0;
-    auto page_of = [pid0, pid1, pid2, pid3](int x) {  // x wave uniform
-      // read all four, select among scalars: an indexed select would be
-      // turned into an LDS array
-      const int l = x & 63;
-      const int r0 = __builtin_amdgcn_readlane(pid0, l), r1 = __builtin_amdgcn_readlane(pid1, l);
-      const int r2 = __builtin_amdgcn_readlane(pid2, l), r3 = __builtin_amdgcn_readlane(pid3, l);
-      return x < 128 ? (x < 64 ? r0 : r1) : (x < 192 ? r2 : r3);
-    };
-    auto rows = [&](int pg) { return min(kPage, ctx - pg * kPage); };
-    // kNbuf page buffers: kNbuf-1 pages are always in flight ahead of the one
-    // being processed.  Prefetches are issued unconditionally (clamped to the
-    // window's last page) so the number of VMEM operations after any page is
-    // fixed, which the wait in process_page relies on.
+// Page ids of the wave's stream live in a double-buffered LDS table of
+// kIdWindow positions per half, filled by LDS-DMA from the block table (lane l
+// fetches position base + l, base + 64 + l).  The half for window k+1 is
+// requested when the issue side enters window k, kIdWindow pages before its
+// first use: every page wait in between (vmcnt in process_page) orders it.
+// Positions past the range fetch entry 0 (never used).
+XV_INLINE void load_window(char* half, const DecodeArgs& a, __amdgpu_buffer_rsrc_t rbt, const int* pref, int64_t f0,
+                           int base, int n, int lane) {
 #pragma unroll
-    for (int k = 0; k < kNbuf - 1; ++k) {
-      const int nk = min(k, np - 1);
-      issue_page(lds + k * kPageLds, a, page_of(nk), kvh, rows(c0 + nk), lo);
+  for (int j = 0; j < kIdWindow / 64; ++j) {
+    const int y = base + 64 * j + lane;
+    int off = 0;
+    if (y < n) {
+      const int64_t f = f0 + y;
+      const int b = seq_of(pref, a.batch, a.hkv, f);
+      const int npb = pref[b + 1] - pref[b];
+      const int r = (int)(f - (int64_t)a.hkv * pref[b]);
+      const int kvh = r / npb;
+      off = (int)(((int64_t)b * a.bt_stride + (r - kvh * npb)) * 4);
     }
-    for (int it = 0; it < np; it += kNbuf) {
-#pragma unroll
-      for (int u = 0; u < kNbuf; ++u) {
-        const int ahead = (u + kNbuf - 1) % kNbuf;
-        const int na = min(it + u + kNbuf - 1, np - 1);
-        issue_page(lds + ahead * kPageLds, a, page_of(na), kvh, rows(c0 + na), lo);
-        if (it + u < np) process_page<G>(st, lds + u * kPageLds, lo, qb, (c0 + it + u) * kPage, ctx, a.scale_log2, lane);
-      }
-    }
-  }
-
-  // total p-sum of head c%G, then fetch it for the heads of this lane's O rows
-  float lsum = st.l;
-  lsum += __shfl_xor(lsum, 16);
-  lsum += __shfl_xor(lsum, 32);
-  // rows 4g+rr with 4g+rr < G hold distinct heads; the others are replicas
-#pragma unroll
-  for (int rr = 0; rr < 4; ++rr) {
-    const int row = 4 * g + rr;
-    const int hsrc = row % G;
-    const float lh = __shfl(lsum, hsrc);
-    const float mh = __shfl(st.m, hsrc);
-    if (row >= G) continue;
-    const float inv = 1.0f / lh;
-    const int head = head0 + row;
-    if (full) {
-      bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) o[16 * n] = (bf16_t)f32_to_bf16(st.o[n][rr] * inv);
-    } else {
-      const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_parts + part;
-      float* o = a.ws_o + wrow * kD + i;
-#pragma unroll
-      for (int n = 0; n < 8; ++n) o[16 * n] = st.o[n][rr] * inv;
-      if (i == 0) a.ws_lse[wrow] = mh + __log2f(lh);
-    }
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rbt, (lds_void*)(half + 256 * j), 4, off, 0, 0, 0);
   }
 }
 
-constexpr int kMaxBatch = 256;  // sequences per launch (larger batches are launched in chunks)
+// Page ids of stream positions y0 .. y0+3 (clamped to n-1) from the table,
+// with one LDS wait for the four (an asm read: the compiler does not order
+// LDS-DMA writes against plain LDS reads).
+struct Ids4 {
+  int v[4];
+};
+XV_INLINE uint32_t id_addr(const char* tab, int y) {
+  return (uint32_t)reinterpret_cast<uintptr_t>(tab) + ((y / kIdWindow) & 1) * (kIdWindow * 4) + (y % kIdWindow) * 4;
+}
+XV_INLINE Ids4 lookup4(const char* tab, int y0, int n) {
+  int r0, r1, r2, r3;
+  __asm__ __volatile__(
+      "ds_read_b32 %0, %4\n\t"
+      "ds_read_b32 %1, %5\n\t"
+      "ds_read_b32 %2, %6\n\t"
+      "ds_read_b32 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(r0), "=&v"(r1), "=&v"(r2), "=&v"(r3)
+      : "v"(id_addr(tab, min(y0, n - 1))), "v"(id_addr(tab, min(y0 + 1, n - 1))),
+        "v"(id_addr(tab, min(y0 + 2, n - 1))), "v"(id_addr(tab, min(y0 + 3, n - 1)))
+      : "memory");
+  Ids4 r;
+  r.v[0] = __builtin_amdgcn_readfirstlane(r0);
+  r.v[1] = __builtin_amdgcn_readfirstlane(r1);
+  r.v[2] = __builtin_amdgcn_readfirstlane(r2);
+  r.v[3] = __builtin_amdgcn_readfirstlane(r3);
+  return r;
+}
 
-#ifndef XV_DECODE_OVERSUB
-#define XV_DECODE_OVERSUB 1  // ranges per resident wave slot
-#endif
+constexpr int kMaxBatch = 256;  // sequences per launch (larger batches are launched in chunks)
 
 #ifndef XV_DECODE_WPE
 #define XV_DECODE_WPE 1  // waves per SIMD the register budget is fitted to
@@ -337,79 +414,138 @@ XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
 template <int G>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WPE, XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
   XV_DECODE_TIMESTAMP(0);
-  __shared__ __attribute__((aligned(16))) char lds[kNbuf * kPageLds];
+  constexpr int NB = kNbufG<G>;
+  constexpr int BUF = kBufBytes<G>;
+  __shared__ __attribute__((aligned(16))) char lds[NB * BUF];
   __shared__ int pref[kMaxBatch + 1];  // pages of sequences 0..b-1
+  __shared__ int sl[kMaxBatch];        // cache_seqlens
+  __shared__ __attribute__((aligned(16))) char idtab[2 * kIdWindow * 4];
   const int lane = threadIdx.x;
-  // prefix sums of the page counts (every wave computes them; B <= 1024)
+  // prefix sums of the page counts (every wave computes them)
   int carry = 0;
   for (int c = 0; c < a.batch; c += 64) {
     const int b = c + lane;
-    const int np = b < a.batch ? (max(a.seqlens[b], 0) + kPage - 1) / kPage : 0;
+    const int ctx = b < a.batch ? max(a.seqlens[b], 0) : 0;
+    const int np = (ctx + kPage - 1) / kPage;
     int inc = np;
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) {
       const int y = __shfl_up(inc, o);
       if (lane >= o) inc += y;
     }
-    if (b < a.batch) pref[b + 1] = carry + inc;
+    if (b < a.batch) {
+      pref[b + 1] = carry + inc;
+      sl[b] = ctx;
+    }
     carry += __shfl(inc, 63);
   }
   if (lane == 0) pref[0] = 0;
-  __syncthreads();  // single wave: orders the LDS prefix writes before the reads
+  __syncthreads();  // single wave: orders the LDS writes before the reads
   const int64_t total = (int64_t)a.hkv * carry;
   const int L = range_pages(a, total);
+  const int64_t f0 = (int64_t)blockIdx.x * L;
+  const int n = (int)max((int64_t)0, min(f0 + L, total) - f0);  // pages of this wave's range
+  if (n == 0) return;
   const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
-  int64_t f = (int64_t)blockIdx.x * L;
-  const int64_t f1 = min(f + L, total);
   XV_DECODE_TIMESTAMP(1);
-  while (f < f1) {
-    // sequence b holding flat page f: largest b with hkv*pref[b] <= f
-    int lo = 0, hi = a.batch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if ((int64_t)a.hkv * pref[mid] <= f) lo = mid; else hi = mid - 1;
-    }
-    const int b = lo;
-    const int npb = pref[b + 1] - pref[b];
-    const int64_t base = (int64_t)a.hkv * pref[b];
-    const int kvh = (int)((f - base) / npb);
-    const int64_t seg0 = base + (int64_t)kvh * npb;
-    const int64_t seg1 = seg0 + npb;
-    const int64_t e = min(f1, seg1);
-    const bool full = (f == seg0) && (e == seg1);
-    const int part = (int)(blockIdx.x - seg0 / L);
-    decode_segment<G>(a, offs, b, kvh, (int)(f - seg0), (int)(e - seg0), full, part, lds, lane);
-    f = e;
+
+  // cursor at the range's first page
+  Cursor c0;
+  c0.b = __builtin_amdgcn_readfirstlane(seq_of(pref, a.batch, a.hkv, f0));
+  c0.npb = __builtin_amdgcn_readfirstlane(pref[c0.b + 1] - pref[c0.b]);
+  c0.ctx = __builtin_amdgcn_readfirstlane(sl[c0.b]);
+  {
+    const int r = (int)(f0 - (int64_t)a.hkv * pref[c0.b]);
+    c0.kvh = __builtin_amdgcn_readfirstlane(r / c0.npb);
+    c0.pg = __builtin_amdgcn_readfirstlane(r - c0.kvh * c0.npb);
   }
+  Cursor ic = c0, pc = c0;  // issue and process cursors
+  const __amdgpu_buffer_rsrc_t rbt =
+      page_rsrc(reinterpret_cast<const bf16_t*>(a.bt), (uint32_t)((int64_t)a.batch * a.bt_stride * 4));
+  load_window(idtab, a, rbt, pref, f0, 0, n, lane);
+  load_window(idtab + kIdWindow * 4, a, rbt, pref, f0, kIdWindow, n, lane);
+  __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");  // nothing else in flight yet
+  int issued = -1;  // last stream position issued
+
+  // One page (and, at a segment start, its q rows) into buffer `slot`.
+  // Positions past the range are clamped to its last page (a harmless
+  // re-read), so every call issues the same 8 page loads; the wait in
+  // process_page relies on that count.
+  auto issue = [&](int y, int slot, int page_id) {
+    char* buf = lds + slot * BUF;
+    if (y > issued) {
+      const bool newseg = issued < 0 || (advance(ic, pref, sl, a.hkv, a.batch), ic.pg == 0);
+      issued = y;
+      if (y % kIdWindow == 0 && y > 0)  // entering window k: request window k+1
+        load_window(idtab + ((y / kIdWindow + 1) & 1) * (kIdWindow * 4), a, rbt, pref, f0, y + kIdWindow, n, lane);
+      if (newseg) issue_q<G>(buf + kPageLds, a, ic.b, ic.kvh, lane);
+    }
+    issue_page(buf, a, page_id, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
+  };
+
+  SplitState st;
+  reset(st);
+  bf16x8_t qb[4];
+  auto finish = [&](const Cursor& c) {
+    const int64_t seg0 = (int64_t)a.hkv * pref[c.b] + (int64_t)c.kvh * c.npb;
+    const bool full = seg0 >= f0 && seg0 + c.npb <= f0 + n;
+    const int part = (int)(blockIdx.x - seg0 / L);
+    finish_segment<G>(a, st, c.b, c.kvh, full, part, lane);
+    if (lane == 0 && seg0 + c.npb <= f0 + n) a.ws_nparts[c.b * a.hkv + c.kvh] = full ? 1 : part + 1;
+  };
+  auto process = [&](int x, int slot) {
+    const char* buf = lds + slot * BUF;
+    if (x > 0) {
+      const Cursor prev = pc;
+      advance(pc, pref, sl, a.hkv, a.batch);
+      if (pc.pg == 0) {
+        finish(prev);
+        reset(st);
+        read_q<G, NB>(qb, buf + kPageLds, lane);
+      }
+    } else {
+      read_q<G, NB>(qb, buf + kPageLds, lane);
+    }
+    process_page<G, NB>(st, buf, offs, qb, pc.pg * kPage, pc.ctx, a.scale_log2, lane);
+  };
+
+  static_assert(NB <= 4, "four ids per lookup");
+  {
+    const Ids4 ids = lookup4(idtab, 0, n);
+#pragma unroll
+    for (int k = 0; k < NB - 1; ++k) issue(min(k, n - 1), k, ids.v[k]);
+  }
+  for (int x0 = 0; x0 < n; x0 += NB) {
+    // ids of the NB positions issued in this round; window k+1 of the table
+    // was requested when the issue side entered window k, at least
+    // kIdWindow - 2*NB positions before any of them
+    const Ids4 ids = lookup4(idtab, x0 + NB - 1, n);
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      issue(min(x0 + u + NB - 1, n - 1), (u + NB - 1) % NB, ids.v[u]);
+      if (x0 + u < n) process(x0 + u, u);
+    }
+  }
+  finish(pc);
   XV_DECODE_TIMESTAMP(2);
 }
 
 // Merge the partials of one (sequence, query head): 64 lanes x 2 dims.  Also
-// writes the zero output of padding rows (cache_seqlens 0).
+// writes the zero output of padding rows (cache_seqlens 0).  The partial
+// count comes from the main kernel; the loads of every partial's lse and
+// output are independent, so the merge costs two memory round trips.
 __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int b = blockIdx.x / a.hq;
   const int h = blockIdx.x - b * a.hq;
   const int lane = threadIdx.x;
-  int before = 0, total = 0;
-  for (int c = lane; c < a.batch; c += 64) {
-    const int np = (max(a.seqlens[c], 0) + kPage - 1) / kPage;
-    total += np;
-    if (c < b) before += np;
-  }
-  for (int o = 32; o > 0; o >>= 1) {
-    before += __shfl_xor(before, o);
-    total += __shfl_xor(total, o);
-  }
-  const int npb = (max(a.seqlens[b], 0) + kPage - 1) / kPage;
+  const int ctx = a.seqlens[b];
+  const int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
   const int d = lane * 2;
   uint32_t* dst = reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)h * kD + d);
-  if (npb == 0) {
+  if (ctx <= 0) {
     *dst = 0u;
     return;
   }
-  const int L = range_pages(a, (int64_t)a.hkv * total);
-  const int64_t seg0 = (int64_t)a.hkv * before + (int64_t)(h / a.group) * npb;
-  const int n = (int)((seg0 + npb - 1) / L - seg0 / L) + 1;
   if (n <= 1) return;
   const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
   float mx = -INFINITY;
@@ -452,8 +588,8 @@ int waves_for(int group) {
 
 }  // namespace
 
-// Workspace layout: [256 B reserved][partial outputs fp32][partial log2-sum-exp fp32]
-size_t counter_bytes(int, int) { return 256; }
+// Workspace layout: [partial counts int32, B*Hkv, padded to 256 B][partial outputs fp32][partial log2-sum-exp fp32]
+size_t counter_bytes(int batch, int num_kv_heads) { return ((size_t)batch * num_kv_heads * 4 + 255) / 256 * 256; }
 
 extern "C" size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int max_blocks_per_seq, int block_size, int head_dim) {
@@ -480,6 +616,10 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
   if (batch > kMaxBatch) return (int)hipErrorInvalidValue;
+  // rows move by 16-byte LDS-DMA: aligned bases, strides in whole 16-byte units
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
+      (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
+    return (int)hipErrorInvalidValue;
   const size_t need = xv_paged_decode_workspace_size(batch, num_q_heads, num_kv_heads, max_blocks_per_seq,
                                                      block_size, head_dim);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
@@ -491,12 +631,13 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
   const int lmin = min_range_pages(max_blocks_per_seq);
   a.max_parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
+  a.ws_nparts = (int*)workspace;
   a.ws_o = (float*)((char*)workspace + counter_bytes(batch, num_kv_heads));
   a.ws_lse = a.ws_o + (size_t)batch * num_q_heads * a.max_parts * kD;
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin;
   // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_blocks_per_seq;
-  a.nwaves = (int)min((int64_t)waves_for(group) * XV_DECODE_OVERSUB, (max_total + lmin - 1) / lmin);
+  a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
   switch (group) {
     case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;
