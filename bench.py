@@ -95,13 +95,21 @@ def time_decode(torch, cases, steps: int, warmup: int):
 
 
 def _time(torch, fn, iters=50, warmup=5):
+    """Device time per call of fn (us): `iters` calls captured in one HIP
+    graph and replayed, so host-side launch cost (Python op wrappers) never
+    leaves the GPU idle between kernels."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(iters):
-        fn()
+    graph.replay()
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / iters * 1e3  # us
@@ -124,31 +132,49 @@ def kernel_suite(torch, dev) -> dict:
         out[name] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
 
-    x, r = rnd(T, H), rnd(T, H)
+    # Each op cycles through enough input sets that one set plus the others
+    # exceed the 256 MB MALL: every call streams its operands from HBM.
+    def cycle(fns):
+        it = [0]
+
+        def step():
+            fns[it[0] % len(fns)]()
+            it[0] += 1
+        return step
+
     w = (torch.randn(H, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
-    rec("fused_add_rmsnorm_T8192_H4096", _time(torch, lambda: torch.ops.vllm.fused_add_rmsnorm(x, r, w, 1e-6)),
+    sets = [(rnd(T, H), rnd(T, H)) for _ in range(2)]
+    rec("fused_add_rmsnorm_T8192_H4096",
+        _time(torch, cycle([lambda x=x, r=r: torch.ops.vllm.fused_add_rmsnorm(x, r, w, 1e-6) for x, r in sets])),
         T * H * 2 * 4 + H * 2)
-    del x, r
-    qkv = rnd(T, (HQ_ + 2 * HKV_) * D_)
-    q = qkv[:, : HQ_ * D_].view(T, HQ_, D_)
-    k = qkv[:, HQ_ * D_ : (HQ_ + HKV_) * D_].view(T, HKV_, D_)
+    del sets
     qw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
     kw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
-    pos = torch.randint(0, 32768, (T,), generator=g, device=dev)
     cs = build_cos_sin_cache(D_, 32768, 1e6).to(dev)
-    rec("qk_norm_rope_T8192_32q8kv", _time(torch, lambda: torch.ops.xv.qk_norm_rope(q, k, qw, kw, 1e-6, pos, cs)),
-        T * (HQ_ + HKV_) * D_ * 2 * 2 + 8 * T + T * D_ * 4)
-    x = rnd(T, 2 * I)
-    rec("silu_and_mul_T8192_I12288", _time(torch, lambda: torch.ops.vllm.silu_and_mul(x)), T * 3 * I * 2)
-    del x
-    kk, vv = rnd(T, HKV_, D_), rnd(T, HKV_, D_)
+    fns = []
+    for _ in range(3):
+        qkv = rnd(T, (HQ_ + 2 * HKV_) * D_)
+        q = qkv[:, : HQ_ * D_].view(T, HQ_, D_)
+        k = qkv[:, HQ_ * D_ : (HQ_ + HKV_) * D_].view(T, HKV_, D_)
+        pos = torch.randint(0, 32768, (T,), generator=g, device=dev)
+        fns.append(lambda q=q, k=k, pos=pos: torch.ops.xv.qk_norm_rope(q, k, qw, kw, 1e-6, pos, cs))
+    rec("qk_norm_rope_T8192_32q8kv", _time(torch, cycle(fns)), T * (HQ_ + HKV_) * D_ * 2 * 2 + 8 * T + T * D_ * 4)
+    del fns, qkv, q, k
+    xs = [rnd(T, 2 * I) for _ in range(2)]
+    rec("silu_and_mul_T8192_I12288", _time(torch, cycle([lambda x=x: torch.ops.vllm.silu_and_mul(x) for x in xs])),
+        T * 3 * I * 2)
+    del xs
     nb = 1024
-    kc = torch.zeros((nb, PAGE, HKV_, D_), dtype=torch.bfloat16, device=dev)
-    vc = torch.zeros_like(kc)
-    slots = torch.randperm(nb * PAGE, generator=g, device=dev)[:T].to(torch.int32)
-    rec("store_kvcache_T8192", _time(torch, lambda: store_kvcache(kk, vv, kc.view(-1, HKV_, D_), vc.view(-1, HKV_, D_), slots)),
-        2 * T * HKV_ * D_ * 2 * 2 + 4 * T)
-    del kc, vc
+    fns = []
+    for _ in range(5):
+        kk, vv = rnd(T, HKV_, D_), rnd(T, HKV_, D_)
+        kc = torch.zeros((nb, PAGE, HKV_, D_), dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        slots = torch.randperm(nb * PAGE, generator=g, device=dev)[:T].to(torch.int32)
+        fns.append(lambda kk=kk, vv=vv, kc=kc, vc=vc, slots=slots:
+                   store_kvcache(kk, vv, kc.view(-1, HKV_, D_), vc.view(-1, HKV_, D_), slots))
+    rec("store_kvcache_T8192", _time(torch, cycle(fns)), 2 * T * HKV_ * D_ * 2 * 2 + 4 * T)
+    del fns, kc, vc, kk, vv
     V = 151936
     for bsz in (64, 256):
         logits = rnd(bsz, V)

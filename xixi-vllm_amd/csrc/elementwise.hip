@@ -28,8 +28,8 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
   const int page = slot / block_size;
   const int t = slot - page * block_size;
   int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
-  store_vec8(k_cache + dst, kv);
-  store_vec8(v_cache + dst, vv);
+  store_vec8_nt(k_cache + dst, kv);
+  store_vec8_nt(v_cache + dst, vv);
 }
 
 extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
@@ -93,7 +93,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
   for (int k = 0; k < VPT; ++k) {
     int vi = lane + k * TPR;
     if (active && vi < nvec) {
-      unpack8(load_vec8(xr + vi * 8), v[k]);
+      unpack8(load_vec8_nt(xr + vi * 8), v[k]);
       wv[k] = load_vec8(w + vi * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss += v[k][e] * v[k][e];
@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
       unpack8(wv[k], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
-      store_vec8(orow + vi * 8, pack8(r));
+      store_vec8_nt(orow + vi * 8, pack8(r));
     }
   }
 }
@@ -133,8 +133,8 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
   for (int k = 0; k < VPT; ++k) {
     int vi = lane + k * TPR;
     if (active && vi < nvec) {
-      xv[k] = load_vec8(xr + vi * 8);
-      rv[k] = load_vec8(rr + vi * 8);
+      xv[k] = load_vec8_nt(xr + vi * 8);
+      rv[k] = load_vec8_nt(rr + vi * 8);
       wv[k] = load_vec8(w + vi * 8);
     }
   }
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
       unpack8(rv[k], b);
 #pragma unroll
       for (int e = 0; e < 8; ++e) { v[k][e] = a[e] + b[e]; ss += v[k][e] * v[k][e]; }
-      store_vec8(rr + vi * 8, pack8(v[k]));
+      store_vec8_nt(rr + vi * 8, pack8(v[k]));
     }
   }
   ss = row_sum<TPR>(ss);
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
       unpack8(wv[k], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
-      store_vec8(xr + vi * 8, pack8(r));
+      store_vec8_nt(xr + vi * 8, pack8(r));
     }
   }
 }
@@ -173,9 +173,11 @@ static int dispatch_norm(int64_t rows, int hidden, hipStream_t stream, Args... a
   if (hidden <= 0 || hidden % 8 || hidden > 16384) return (int)hipErrorInvalidValue;
   if (rows == 0) return 0;
   int nvec = hidden / 8;
-  // few long rows (decode batches): a whole workgroup per row keeps each
-  // lane's memory chain short; many rows: a wave (or a DPP row) per row
-  if (rows <= 1024 && nvec >= 256) {
+  // long rows: a whole workgroup per row keeps each lane's memory chain short
+  // and gives many small workgroups (several residency rounds, so loads of
+  // one round overlap the reductions of another); short rows: a wave (or a
+  // DPP row) per row
+  if (nvec >= 256) {
     if (nvec <= 512) return Launcher<256, 2>::run(rows, stream, args...);
     if (nvec <= 1024) return Launcher<256, 4>::run(rows, stream, args...);
     return Launcher<256, 8>::run(rows, stream, args...);
@@ -230,8 +232,8 @@ extern "C" int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, i
 
 // --------------------------------------------------------------------------
 // NeoX RoPE (optionally preceded by the per-head RMSNorm of Qwen3).
-// 16 lanes own one head of D = 128: lane j holds elements [8j, 8j+8); the
-// rotation partner of lane j is lane j^8 (same DPP row, fetched by row_ror:8).
+// 16 lanes (one DPP row) own one head of D = 128: lane j holds elements
+// [8j, 8j+8); the rotation partner of lane j is lane j^8 (row_ror:8).
 // --------------------------------------------------------------------------
 // STORE: k heads go (roped) and v heads go (copied) straight into the paged
 // cache at slot_mapping[t] (slot -1: nothing stored), instead of into k_out.
@@ -243,6 +245,19 @@ struct CacheDst {
   const bf16_t* v; int64_t vs_tok, vs_head;
 };
 
+// One wave per token: 16-lane row r of the wave handles heads r, r+4, r+8, ...
+// The token's position, its fp32 cos/sin row, the norm weights and the slot
+// are fetched once per lane; all head loads of a row (up to kRopeBatch) are
+// issued before the first is used.
+#ifndef XV_ROPE_BATCH
+#define XV_ROPE_BATCH 6
+#endif
+#ifndef XV_ROPE_ROWS
+#define XV_ROPE_ROWS 8  // 16-lane rows per token (two waves)
+#endif
+constexpr int kRopeBatch = XV_ROPE_BATCH;
+constexpr int kRopeRows = XV_ROPE_ROWS;
+
 template <bool NORM, bool STORE>
 __global__ __launch_bounds__(256) void rope_kernel(
     const bf16_t* __restrict__ q, int64_t qs_tok, int64_t qs_head,
@@ -252,69 +267,77 @@ __global__ __launch_bounds__(256) void rope_kernel(
     bf16_t* __restrict__ q_out, bf16_t* __restrict__ k_out,
     int64_t num_tokens, int hq, int hkv, CacheDst cd) {
   constexpr int D = 128;
-  const int heads = hq + hkv + (STORE ? hkv : 0);  // STORE: v heads follow the k heads
-  int64_t gh = (int64_t)blockIdx.x * 16 + threadIdx.x / 16;
-  int lane = threadIdx.x & 15;
-  bool active = gh < num_tokens * heads;
-  int64_t tok = active ? gh / heads : 0;
-  int h = active ? (int)(gh - tok * heads) : 0;
-  if constexpr (STORE) {
-    if (h >= hq + hkv) {  // v head: plain copy into the cache (no cross-lane work in this group)
-      const int32_t slot = active ? cd.slots[tok] : -1;
-      if (slot < 0) return;
-      const int vh = h - hq - hkv;
-      const int page = slot / cd.block_size, t = slot - page * cd.block_size;
-      const Vec8 vv = load_vec8(cd.v + tok * cd.vs_tok + (int64_t)vh * cd.vs_head + lane * 8);
-      store_vec8(cd.vc + (int64_t)page * cd.ps + (int64_t)t * cd.ts + (int64_t)vh * cd.hs + lane * 8, vv);
-      return;
-    }
-  }
-  const bool is_q = h < hq;
-  const bf16_t* src = is_q ? q + tok * qs_tok + (int64_t)h * qs_head
-                           : k + tok * ks_tok + (int64_t)(h - hq) * ks_head;
-  float x[8];
-  unpack8(load_vec8(src + lane * 8), x);
-  if constexpr (NORM) {
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-    ss = row16_sum(ss);
-    float rcp = rsqrtf(ss / (float)D + eps);
-    float wf[8];
-    unpack8(load_vec8((is_q ? qw : kw) + lane * 8), wf);
-    // round to bf16 between the norm and the rotation, as the two separate ops do
-#pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16((x[e] * rcp) * wf[e]));
-  }
-  float partner[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) partner[e] = dpp_f<0x128>(x[e]);
-  if (!active) return;
-  int64_t pos = positions[tok];
+  const int64_t tok = ((int64_t)blockIdx.x * 16 + (threadIdx.x >> 4)) / kRopeRows;
+  if (tok >= num_tokens) return;
+  const int row = (threadIdx.x >> 4) % kRopeRows, lane = threadIdx.x & 15;
+  const int nrot = hq + hkv;                       // heads normed and rotated
+  const int heads = nrot + (STORE ? hkv : 0);      // STORE: v heads follow, copied
+  const int64_t pos = positions[tok];
   const float* cs = cos_sin + pos * D + (lane & 7) * 8;
-  float4 c0 = *reinterpret_cast<const float4*>(cs);
-  float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
-  float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
-  float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
-  float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-  float s[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-  float r[8];
-  if (lane < 8) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = x[e] * c[e] - partner[e] * s[e];
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = x[e] * c[e] + partner[e] * s[e];
+  const float4 c0 = *reinterpret_cast<const float4*>(cs);
+  const float4 c1 = *reinterpret_cast<const float4*>(cs + 4);
+  const float4 s0 = *reinterpret_cast<const float4*>(cs + D / 2);
+  const float4 s1 = *reinterpret_cast<const float4*>(cs + D / 2 + 4);
+  const float c[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  const float sn[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+  float wq[8], wk[8];
+  if constexpr (NORM) {
+    unpack8(load_vec8(qw + lane * 8), wq);
+    unpack8(load_vec8(kw + lane * 8), wk);
   }
-  if (is_q) {
-    store_vec8(q_out + (tok * hq + h) * D + lane * 8, pack8(r));
-  } else if constexpr (STORE) {
-    const int32_t slot = cd.slots[tok];
-    if (slot < 0) return;
+  int32_t slot = 0;
+  int64_t cache_off = 0;
+  if constexpr (STORE) {
+    slot = cd.slots[tok];
     const int page = slot / cd.block_size, t = slot - page * cd.block_size;
-    store_vec8(cd.kc + (int64_t)page * cd.ps + (int64_t)t * cd.ts + (int64_t)(h - hq) * cd.hs + lane * 8, pack8(r));
-  } else {
-    store_vec8(k_out + (tok * hkv + (h - hq)) * D + lane * 8, pack8(r));
+    cache_off = (int64_t)page * cd.ps + (int64_t)t * cd.ts + lane * 8;
+  }
+  for (int h0 = row; h0 < heads; h0 += kRopeRows * kRopeBatch) {
+    Vec8 xv[kRopeBatch];
+#pragma unroll
+    for (int j = 0; j < kRopeBatch; ++j) {
+      const int h = h0 + kRopeRows * j;
+      if (h >= heads) break;
+      const bf16_t* src = h < hq ? q + tok * qs_tok + (int64_t)h * qs_head
+                        : h < nrot ? k + tok * ks_tok + (int64_t)(h - hq) * ks_head
+                                   : cd.v + tok * cd.vs_tok + (int64_t)(h - nrot) * cd.vs_head;
+      xv[j] = load_vec8_nt(src + lane * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < kRopeBatch; ++j) {
+      const int h = h0 + kRopeRows * j;
+      if (h >= heads) break;
+      if (STORE && h >= nrot) {  // v head: plain copy into the cache
+        if (slot >= 0) store_vec8_nt(cd.vc + cache_off + (int64_t)(h - nrot) * cd.hs, xv[j]);
+        continue;
+      }
+      const bool is_q = h < hq;
+      float x[8];
+      unpack8(xv[j], x);
+      if constexpr (NORM) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+        ss = row16_sum(ss);
+        const float rcp = rsqrtf(ss / (float)D + eps);
+        // round to bf16 between the norm and the rotation, as the two separate ops do
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = bf16_to_f32(f32_to_bf16((x[e] * rcp) * (is_q ? wq[e] : wk[e])));
+      }
+      float r[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float partner = dpp_f<0x128>(x[e]);  // row_ror:8 -> lane j^8
+        r[e] = lane < 8 ? x[e] * c[e] - partner * sn[e] : x[e] * c[e] + partner * sn[e];
+      }
+      if (is_q) {
+        store_vec8_nt(q_out + (tok * hq + h) * D + lane * 8, pack8(r));
+      } else if constexpr (STORE) {
+        if (slot >= 0) store_vec8_nt(cd.kc + cache_off + (int64_t)(h - hq) * cd.hs, pack8(r));
+      } else {
+        store_vec8_nt(k_out + (tok * hkv + (h - hq)) * D + lane * 8, pack8(r));
+      }
+    }
   }
 }
 
@@ -323,8 +346,7 @@ static int launch_rope_t(const void* q, int64_t qst, int64_t qsh, const void* k,
                          const void* qw, const void* kw, float eps, const int64_t* positions, const float* cs,
                          void* q_out, void* k_out, int64_t T, int hq, int hkv, const CacheDst& cd,
                          hipStream_t stream) {
-  const int64_t heads = T * (hq + hkv + (STORE ? hkv : 0));
-  const unsigned blocks = (unsigned)((heads + 15) / 16);
+  const unsigned blocks = (unsigned)((T * kRopeRows + 15) / 16);
   rope_kernel<NORM, STORE><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
                                                        (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
                                                        (bf16_t*)q_out, (bf16_t*)k_out, T, hq, hkv, cd);
@@ -402,8 +424,8 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const bf16_t* __restr
   unpack8(load_vec8_nt(xr + c), g);
   unpack8(load_vec8_nt(xr + inter + c), u);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = g[e] / (1.0f + __expf(-g[e])) * u[e];
-  store_vec8(out + row * os + c, pack8(r));
+  for (int e = 0; e < 8; ++e) r[e] = g[e] * __builtin_amdgcn_rcpf(1.0f + __expf(-g[e])) * u[e];
+  store_vec8_nt(out + row * os + c, pack8(r));
 }
 
 extern "C" int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,

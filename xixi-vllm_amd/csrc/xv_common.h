@@ -15,15 +15,16 @@ XV_INLINE float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 XV_INLINE float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // fp32 -> bf16 with round-to-nearest-even (torch's rounding); NaN stays NaN.
-XV_INLINE uint32_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return ((u >> 16) | 0x40u) & 0xffffu;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
-}
+// gfx950 converts in hardware (v_cvt_pk_bf16_f32, two values per instruction).
+typedef __bf16 xv_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float xv_f32x2 __attribute__((ext_vector_type(2)));
 XV_INLINE uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+  const xv_bf16x2 h = __builtin_convertvector((xv_f32x2){lo, hi}, xv_bf16x2);
+  uint32_t r;
+  __builtin_memcpy(&r, &h, 4);
+  return r;
 }
+XV_INLINE uint32_t f32_to_bf16(float f) { return pack_bf16x2(f, 0.f) & 0xffffu; }
 
 // Eight bf16 values held as a 16-byte vector.
 struct alignas(16) Vec8 {
@@ -41,6 +42,14 @@ XV_INLINE Vec8 load_vec8_nt(const bf16_t* p) {
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   Vec8 r; r.w[0] = v[0]; r.w[1] = v[1]; r.w[2] = v[2]; r.w[3] = v[3]; return r;
+}
+// Non-temporal streaming store for data written once and not re-read soon.
+// On this part nt loads and stores raise a plain stream copy from ~6.1 to
+// ~6.6 TB/s.
+XV_INLINE void store_vec8_nt(bf16_t* p, const Vec8& r) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 v = {r.w[0], r.w[1], r.w[2], r.w[3]};
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 XV_INLINE void unpack8(const Vec8& v, float* f) {
 #pragma unroll
