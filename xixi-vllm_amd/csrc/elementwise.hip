@@ -57,7 +57,10 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
 // RMSNorm family.  TPR lanes own one row (16 = a DPP row, 64 = a wave); each
 // lane keeps up to VPT 8-element vectors of the row in registers.
 // --------------------------------------------------------------------------
-// Sum over the TPR lanes owning a row (TPR = 256: the whole workgroup, through LDS).
+// Threads per workgroup for TPR lanes per row.
+template <int TPR> constexpr int kNormBlock = TPR > 256 ? TPR : 256;
+
+// Sum over the TPR lanes owning a row (TPR >= 128: its waves, through LDS).
 template <int TPR>
 XV_INLINE float row_sum(float x) {
   if constexpr (TPR == 16) {
@@ -65,19 +68,25 @@ XV_INLINE float row_sum(float x) {
   } else if constexpr (TPR == 64) {
     return wave_sum(x);
   } else {
-    __shared__ float part[4];
+    constexpr int W = TPR / 64;  // waves per row
+    __shared__ float part[kNormBlock<TPR> / 64];
     x = wave_sum(x);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = x;
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) part[wave] = x;
     __syncthreads();
-    return (part[0] + part[1]) + (part[2] + part[3]);
+    const int w0 = wave / W * W;
+    float r = part[w0];
+#pragma unroll
+    for (int i = 1; i < W; ++i) r += part[w0 + i];
+    return r;
   }
 }
 
 template <int TPR, int VPT>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(
+__global__ __launch_bounds__(kNormBlock<TPR>) void rmsnorm_kernel(
     const bf16_t* __restrict__ x, int64_t s_outer, int64_t s_inner, const bf16_t* __restrict__ w,
     bf16_t* __restrict__ out, int64_t n_outer, int64_t n_inner, int hidden, float eps) {
-  const int rows_per_block = 256 / TPR;
+  const int rows_per_block = kNormBlock<TPR> / TPR;
   int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / TPR;
   int lane = threadIdx.x % TPR;
   int64_t rows = n_outer * n_inner;
@@ -117,10 +126,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(
 }
 
 template <int TPR, int VPT>
-__global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
+__global__ __launch_bounds__(kNormBlock<TPR>) void fused_add_rmsnorm_kernel(
     bf16_t* __restrict__ x, int64_t xs, bf16_t* __restrict__ res, int64_t rs,
     const bf16_t* __restrict__ w, int64_t rows, int hidden, float eps) {
-  const int rows_per_block = 256 / TPR;
+  const int rows_per_block = kNormBlock<TPR> / TPR;
   int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / TPR;
   int lane = threadIdx.x % TPR;
   bool active = row < rows;
@@ -168,6 +177,10 @@ __global__ __launch_bounds__(256) void fused_add_rmsnorm_kernel(
   }
 }
 
+#ifndef XV_NORM_LONG_TPR
+#define XV_NORM_LONG_TPR 512  // lanes per row for rows of >= 256 vectors
+#endif
+
 template <template <int, int> class Launcher, typename... Args>
 static int dispatch_norm(int64_t rows, int hidden, hipStream_t stream, Args... args) {
   if (hidden <= 0 || hidden % 8 || hidden > 16384) return (int)hipErrorInvalidValue;
@@ -178,9 +191,12 @@ static int dispatch_norm(int64_t rows, int hidden, hipStream_t stream, Args... a
   // one round overlap the reductions of another); short rows: a wave (or a
   // DPP row) per row
   if (nvec >= 256) {
-    if (nvec <= 512) return Launcher<256, 2>::run(rows, stream, args...);
-    if (nvec <= 1024) return Launcher<256, 4>::run(rows, stream, args...);
-    return Launcher<256, 8>::run(rows, stream, args...);
+    constexpr int T = XV_NORM_LONG_TPR;
+    if (nvec <= T) return Launcher<T, 1>::run(rows, stream, args...);
+    if (nvec <= 2 * T) return Launcher<T, 2>::run(rows, stream, args...);
+    if (nvec <= 4 * T) return Launcher<T, 4>::run(rows, stream, args...);
+    if (nvec <= 8 * T) return Launcher<T, 8>::run(rows, stream, args...);
+    return Launcher<T, 16>::run(rows, stream, args...);
   }
   if (nvec <= 16) return Launcher<16, 1>::run(rows, stream, args...);
   if (nvec <= 32) return Launcher<16, 2>::run(rows, stream, args...);
@@ -196,8 +212,10 @@ template <int TPR, int VPT>
 struct RmsLaunch {
   static int run(int64_t rows, hipStream_t stream, const bf16_t* x, int64_t so, int64_t si,
                  const bf16_t* w, bf16_t* out, int64_t no, int64_t ni, int hidden, float eps) {
-    int64_t blocks = (rows + (256 / TPR) - 1) / (256 / TPR);
-    rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, so, si, w, out, no, ni, hidden, eps);
+    constexpr int rpb = kNormBlock<TPR> / TPR;
+    int64_t blocks = (rows + rpb - 1) / rpb;
+    rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(kNormBlock<TPR>), 0, stream>>>(x, so, si, w, out, no, ni,
+                                                                                         hidden, eps);
     XV_CHECK_LAUNCH();
     return 0;
   }
@@ -206,8 +224,10 @@ template <int TPR, int VPT>
 struct AddRmsLaunch {
   static int run(int64_t rows, hipStream_t stream, bf16_t* x, int64_t xs, bf16_t* r, int64_t rs,
                  const bf16_t* w, int hidden, float eps) {
-    int64_t blocks = (rows + (256 / TPR) - 1) / (256 / TPR);
-    fused_add_rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(x, xs, r, rs, w, rows, hidden, eps);
+    constexpr int rpb = kNormBlock<TPR> / TPR;
+    int64_t blocks = (rows + rpb - 1) / rpb;
+    fused_add_rmsnorm_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(kNormBlock<TPR>), 0, stream>>>(
+        x, xs, r, rs, w, rows, hidden, eps);
     XV_CHECK_LAUNCH();
     return 0;
   }
