@@ -30,8 +30,8 @@ sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
-# 2 x 313494.2 KiB read (FETCH_SIZE counts half on this part) + 3210.9 KiB written.
-MEASURED_TRAFFIC_BYTES = int((2 * 313494.2 + 3210.9) * 1024)
+# 2 x 319061.4 KiB read (FETCH_SIZE counts half on this part) + 3225.3 KiB written.
+MEASURED_TRAFFIC_BYTES = int((2 * 319061.4 + 3225.3) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
