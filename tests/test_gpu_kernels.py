@@ -346,3 +346,25 @@ def test_qk_norm_rope_store_matches_separate_ops(dev, hnd):
     torch.cuda.synchronize()
     assert torch.equal(qf, qo)
     assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
+
+
+def test_paged_decode_workspace_reuse_across_batches(dev):
+    """Calls of different batch sizes share the per-device workspace: split
+    partials of one call must never be taken for the arrival counters of the
+    next, and each call leaves the counters at zero."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = gen(91)
+    for bsz, lo, hi in [(8, 600, 3000), (256, 1, 300), (64, 200, 2500), (3, 4000, 4097), (256, 30, 900)]:
+        ctx = torch.randint(lo, hi, (bsz,), generator=g).tolist()
+        need = sum((c + 15) // 16 for c in ctx)
+        kc, vc, bt, sl = make_paged(ctx, int(need * 1.25) + 4, 8, 128, g)
+        q = randn_bf16((bsz, 32, 128), g)
+        rows = list(range(0, bsz, max(1, bsz // 8)))
+        want = O.paged_decode_attention(f32(q)[rows], f32(kc), f32(vc), bt.numpy()[rows], sl.numpy()[rows])
+        out = paged_decode_attention(q.view(bsz, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev),
+                                     32, 8, 128)
+        torch.cuda.synchronize()
+        print(f"workspace reuse: B {bsz} ctx [{lo},{hi})", flush=True)
+        assert torch.isfinite(out.float()).all()
+        _close(f32(out).reshape(bsz, 32, 128)[rows], want)

@@ -537,31 +537,49 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
 
 // Merge the partials of one (sequence, query head): 64 lanes x 2 dims.  Also
 // writes the zero output of padding rows (cache_seqlens 0).  The partial
-// count comes from the main kernel; the loads of every partial's lse and
-// output are independent, so the merge costs two memory round trips.
+// count comes from the main kernel.  The count, the sequence length and the
+// first two partials (the common split) are loaded together, so a two-way
+// merge costs one memory round trip; further partials are loaded four at a
+// time.
 __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int b = blockIdx.x / a.hq;
   const int h = blockIdx.x - b * a.hq;
   const int lane = threadIdx.x;
+  const int d = lane * 2;
+  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
   const int ctx = a.seqlens[b];
   const int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
-  const int d = lane * 2;
+  // speculative: rows 0 and 1 exist in every workspace (max_parts >= 2)
+  const float l0 = a.ws_lse[row0], l1 = a.ws_lse[row0 + 1];
+  const float2 v0 = *reinterpret_cast<const float2*>(a.ws_o + row0 * kD + d);
+  const float2 v1 = *reinterpret_cast<const float2*>(a.ws_o + (row0 + 1) * kD + d);
   uint32_t* dst = reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)h * kD + d);
   if (ctx <= 0) {
     *dst = 0u;
     return;
   }
   if (n <= 1) return;
-  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
-  float mx = -INFINITY;
-  for (int s = 0; s < n; ++s) mx = fmaxf(mx, a.ws_lse[row0 + s]);
-  float den = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int s = 0; s < n; ++s) {
-    const float w = __builtin_amdgcn_exp2f(a.ws_lse[row0 + s] - mx);
-    const float2 v = *reinterpret_cast<const float2*>(a.ws_o + (row0 + s) * kD + d);
-    den += w;
-    o0 += w * v.x;
-    o1 += w * v.y;
+  float mx = fmaxf(l0, l1);
+  for (int s = 2; s < n; ++s) mx = fmaxf(mx, a.ws_lse[row0 + s]);
+  const float w0 = __builtin_amdgcn_exp2f(l0 - mx), w1 = __builtin_amdgcn_exp2f(l1 - mx);
+  float den = w0 + w1;
+  float o0 = w0 * v0.x + w1 * v1.x, o1 = w0 * v0.y + w1 * v1.y;
+  for (int s0 = 2; s0 < n; s0 += 4) {
+    float ls[4];
+    float2 vs[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t r = row0 + min(s0 + k, n - 1);
+      ls[k] = s0 + k < n ? a.ws_lse[r] : -INFINITY;
+      vs[k] = *reinterpret_cast<const float2*>(a.ws_o + r * kD + d);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float w = __builtin_amdgcn_exp2f(ls[k] - mx);  // 0 past n
+      den += w;
+      o0 += w * vs[k].x;
+      o1 += w * vs[k].y;
+    }
   }
   const float inv = 1.0f / den;
   *dst = pack_bf16x2(o0 * inv, o1 * inv);
