@@ -115,6 +115,67 @@ def _time(torch, fn, iters=50, warmup=5):
     return e0.elapsed_time(e1) / iters * 1e3  # us
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16
+
+
+def prefill_suite(torch, dev, iters: int = 20) -> dict:
+    """Prefill attention tile (MFMA-bound) at the Qwen3-8B attention shape:
+    causal flops = 4*Hq*D*sum(visible keys per query) against the dense bf16
+    MFMA peak.  Cases: a plain causal batch with config-4 prompt lengths
+    (16 sequences, U[128, 2048]); a chunked prefill of 512 new tokens per
+    sequence over a paged cached prefix U[512, 2048]; one 8192-token prompt."""
+    from xvllm.layers.attention import prefill_attention
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    gc = torch.Generator().manual_seed(11)
+    rnd = lambda *shape: torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
+    out = {}
+
+    def rec(name, us, flops, tokens):
+        tf = flops / (us * 1e-6) / 1e12
+        out[name] = {"us": round(us, 1), "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "flops": flops, "q_tokens": tokens}
+
+    def dense_case(qlens):
+        cu = torch.tensor([0] + list(torch.tensor(qlens).cumsum(0).tolist()), dtype=torch.int32, device=dev)
+        T = int(cu[-1])
+        qkv = rnd(T, (HQ + 2 * HKV) * D)
+        q = qkv[:, : HQ * D]
+        k = qkv[:, HQ * D : (HQ + HKV) * D].view(T, HKV, D)
+        v = qkv[:, (HQ + HKV) * D :].view(T, HKV, D)
+        fn = lambda: prefill_attention(q, k, v, cu, cu, max(qlens), HQ, HKV, D)
+        flops = 4 * HQ * D * sum(L * (L + 1) // 2 for L in qlens)
+        return fn, flops, T
+
+    qlens = torch.randint(128, 2049, (16,), generator=gc).tolist()
+    fn, fl, T = dense_case(qlens)
+    rec("prefill_causal_16seq_U128_2048", _time(torch, fn, iters), fl, T)
+    fn, fl, T = dense_case([8192])
+    rec("prefill_causal_1seq_8192", _time(torch, fn, iters), fl, T)
+    # chunked prefill: 512 new tokens over a cached prefix, keys through the block table
+    pre = torch.randint(512, 2049, (16,), generator=gc).tolist()
+    new = [512] * 16
+    klens = [p_ + n_ for p_, n_ in zip(pre, new)]
+    need = [(k_ + PAGE - 1) // PAGE for k_ in klens]
+    nb = sum(need) + 8
+    kc, vc = rnd(nb, PAGE, HKV, D), rnd(nb, PAGE, HKV, D)
+    perm = torch.randperm(nb, generator=gc)
+    bt = torch.full((16, max(need)), -1, dtype=torch.int32)
+    o_ = 0
+    for b, n_ in enumerate(need):
+        bt[b, :n_] = perm[o_ : o_ + n_].to(torch.int32)
+        o_ += n_
+    bt = bt.to(dev)
+    cu_q = torch.tensor([0] + torch.tensor(new).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    cu_k = torch.tensor([0] + torch.tensor(klens).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    q = rnd(sum(new), HQ * D)
+    fn = lambda: prefill_attention(q, None, None, cu_q, cu_k, 512, HQ, HKV, D, k_cache=kc, v_cache=vc,
+                                   block_tables=bt)
+    fl = 4 * HQ * D * sum(sum(p_ + i + 1 for i in range(n_)) for p_, n_ in zip(pre, new))
+    rec("chunked_prefill_16x512_over_U512_2048_paged", _time(torch, fn, iters), fl, sum(new))
+    return out
+
+
 def kernel_suite(torch, dev) -> dict:
     """Config 3 (fused elementwise/reduction set at Qwen3-8B width over 8192
     tokens) and the sampler, each against its algorithmic HBM bytes."""
@@ -290,6 +351,8 @@ def main() -> int:
     ap.add_argument("--no-suite", action="store_true", help="skip the config-3 kernel set and the sampler")
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B decode tok/s measurement")
     ap.add_argument("--e2e-only", action="store_true", help="only the Qwen3-8B decode step (for profiling)")
+    ap.add_argument("--prefill-only", action="store_true", help="only the prefill attention cases (for profiling)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill attention cases")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
@@ -316,6 +379,9 @@ def main() -> int:
     ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
     if args.e2e_only:
         print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
+        return 0
+    if args.prefill_only:
+        print(json.dumps(prefill_suite(torch, dev, iters=args.steps)))
         return 0
     cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1)
     ms, wall = time_decode(torch, cases, args.steps, args.warmup)
@@ -367,6 +433,8 @@ def main() -> int:
     }
     if not args.no_suite:
         line["kernels"] = kernel_suite(torch, dev)
+    if not args.no_prefill:
+        line["prefill"] = prefill_suite(torch, dev)
     if not args.no_e2e:
         del cases
         torch.cuda.empty_cache()
