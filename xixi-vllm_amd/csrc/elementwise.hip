@@ -14,20 +14,46 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
     const bf16_t* __restrict__ value, int64_t vs_tok, int64_t vs_head,
     bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
     int64_t cs_page, int64_t cs_tok, int64_t cs_head, int block_size, const int32_t* __restrict__ slots,
-    int64_t total_chunks, int chunks_per_tok, int chunks_per_head) {
-  int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    int total_chunks, int chunks_per_tok, int chunks_per_head) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total_chunks) return;
-  int64_t tok = idx / chunks_per_tok;
-  int c = (int)(idx - tok * chunks_per_tok);
-  int32_t slot = slots[tok];
+  const int tok = idx / chunks_per_tok;
+  const int c = idx - tok * chunks_per_tok;
+  const int32_t slot = slots[tok];
   if (slot < 0) return;  // padding token (slot -1) writes nothing
-  int h = c / chunks_per_head;
-  int d = (c - h * chunks_per_head) * 8;
-  Vec8 kv = load_vec8_nt(key + tok * ks_tok + h * ks_head + d);
-  Vec8 vv = load_vec8_nt(value + tok * vs_tok + h * vs_head + d);
+  const int h = c / chunks_per_head;
+  const int d = (c - h * chunks_per_head) * 8;
+  const Vec8 kv = load_vec8_nt(key + tok * ks_tok + h * ks_head + d);
+  const Vec8 vv = load_vec8_nt(value + tok * vs_tok + h * vs_head + d);
   const int page = slot / block_size;
   const int t = slot - page * block_size;
-  int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
+  const int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
+  store_vec8_nt(k_cache + dst, kv);
+  store_vec8_nt(v_cache + dst, vv);
+}
+
+// Tokens whose Hkv*D/8 chunks are a multiple of 64: each wave moves 64
+// chunks of one token, so the token, its slot and the page address are wave
+// uniform (one scalar slot load per wave, no per-lane division).
+__global__ __launch_bounds__(256) void store_kvcache_wave_kernel(
+    const bf16_t* __restrict__ key, int64_t ks_tok, int64_t ks_head,
+    const bf16_t* __restrict__ value, int64_t vs_tok, int64_t vs_head,
+    bf16_t* __restrict__ k_cache, bf16_t* __restrict__ v_cache,
+    int64_t cs_page, int64_t cs_tok, int64_t cs_head, int block_size, const int32_t* __restrict__ slots,
+    int num_waves, int waves_per_tok, int chunks_per_head) {
+  const int wv = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (wv >= num_waves) return;
+  const int tok = wv / waves_per_tok;
+  const int c = (wv - tok * waves_per_tok) * 64 + (threadIdx.x & 63);
+  const int32_t slot = __builtin_amdgcn_readfirstlane(slots[tok]);
+  if (slot < 0) return;
+  const int h = c / chunks_per_head;
+  const int d = (c - h * chunks_per_head) * 8;
+  const Vec8 kv = load_vec8_nt(key + tok * ks_tok + h * ks_head + d);
+  const Vec8 vv = load_vec8_nt(value + tok * vs_tok + h * vs_head + d);
+  const int page = slot / block_size;
+  const int t = slot - page * block_size;
+  const int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
   store_vec8_nt(k_cache + dst, kv);
   store_vec8_nt(v_cache + dst, vv);
 }
@@ -41,14 +67,23 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || block_size <= 0)
     return (int)hipErrorInvalidValue;
   if (num_tokens == 0) return 0;
-  int cph = head_dim / 8;
-  int cpt = cph * num_kv_heads;
-  int64_t total = num_tokens * cpt;
-  int64_t blocks = (total + 255) / 256;
-  store_kvcache_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(
-      (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok,
-      value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_page_stride, cache_tok_stride,
-      cache_head_stride, block_size, slot_mapping, total, cpt, cph);
+  const int cph = head_dim / 8;
+  const int cpt = cph * num_kv_heads;
+  if (num_tokens * cpt >= ((int64_t)1 << 31)) return (int)hipErrorInvalidValue;  // 32-bit chunk indices
+  if (cpt % 64 == 0) {
+    const int wpt = cpt / 64;
+    const int waves = (int)num_tokens * wpt;
+    store_kvcache_wave_kernel<<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream>>>(
+        (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok,
+        value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_page_stride, cache_tok_stride,
+        cache_head_stride, block_size, slot_mapping, waves, wpt, cph);
+  } else {
+    const int total = (int)(num_tokens * cpt);
+    store_kvcache_kernel<<<dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream>>>(
+        (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok,
+        value_stride_head, (bf16_t*)k_cache, (bf16_t*)v_cache, cache_page_stride, cache_tok_stride,
+        cache_head_stride, block_size, slot_mapping, total, cpt, cph);
+  }
   XV_CHECK_LAUNCH();
   return 0;
 }
