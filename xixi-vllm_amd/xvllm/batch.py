@@ -79,6 +79,21 @@ class Batch:
         self._row_len = np.full(max_bs, -1, dtype=np.int64)   # entries of each host row in sync
         self._row_sid = np.full(max_bs, -1, dtype=np.int64)   # sequence that owns the row
         self._samp_key = None
+        # the pinned staging buffers feed non-blocking H2D copies: a build
+        # waits for the previous build's copies before overwriting them (a
+        # step that runs decode and prefill stages both into the same buffers)
+        self._h2d_done = torch.cuda.Event() if torch.device(device).type == "cuda" else None
+        self._h2d_pending = False
+
+    def _wait_staging(self) -> None:
+        if self._h2d_pending:
+            self._h2d_done.synchronize()
+            self._h2d_pending = False
+
+    def _staged(self) -> None:
+        if self._h2d_done is not None:
+            self._h2d_done.record()
+            self._h2d_pending = True
 
     # ------------------------------------------------------------ block tables
     def _sync_block_tables(self, seqs: list[SeqSchedule]) -> None:
@@ -129,6 +144,7 @@ class Batch:
     # ------------------------------------------------------------ decode
     def build_decode(self, seqs: list[SeqSchedule], *, pad_to: int | None = None) -> None:
         n = len(seqs)
+        self._wait_staging()
         self._sync_block_tables(seqs)
         pos = np.fromiter((s.num_cached_tokens for s in seqs), np.int64, n)
         ids = np.fromiter((s.token_ids[-1] for s in seqs), np.int64, n)
@@ -149,9 +165,11 @@ class Batch:
             self.block_tables[n:pad_to].fill_(-1)
             self._row_sid[n:pad_to] = -1
             self._row_len[n:pad_to] = -1
+        self._staged()
 
     # ------------------------------------------------------------ prefill
     def build_prefill(self, seqs: list[SeqSchedule]) -> tuple[int, int, int, bool]:
+        self._wait_staging()
         ids, pos, slot = self._h_ids.numpy(), self._h_pos.numpy(), self._h_slot.numpy()
         cuq, cuk = self._h_cuq.numpy(), self._h_cuk.numpy()
         cuq[0] = cuk[0] = 0
@@ -175,4 +193,5 @@ class Batch:
         if has_cache:
             self._sync_block_tables(seqs)
         self._sync_sampling(seqs)
+        self._staged()
         return nt, max_q, max_k, has_cache
