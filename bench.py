@@ -308,6 +308,80 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
             "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}
 
 
+def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
+    """Config 5: Qwen3-32B-shaped decode (64 layers, hidden 5120, 64 q / 8 kv
+    heads, FFN 25600, random bf16 weights ~N(0,0.02)), batch 32 at context
+    32768; 16 requests share an 8192-token prefix mapped to the same KV pages,
+    16 are independent; top-p 0.95 over the 151936 vocab with seeded draws.
+    The 64 layers' KV (275 GB per sequence, 243 GB of unique pages) does not
+    fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
+    layer i reads pool layer i % pool_layers: every layer streams the same
+    bytes in the same pattern as with a full pool (what this leaves out: the
+    real memory footprint and the TLB reach of 243 GB)."""
+    from xvllm.batch import SeqSchedule
+    from xvllm.config import QWEN3_32B
+    from xvllm.kv_pool import KVPool
+    from xvllm.model_runner import ModelRunner
+    from xvllm.models import Qwen3ForCausalLM
+
+    cfg = QWEN3_32B
+    bsz, ctx, prefix, shared = 32, 32768, 8192, 16
+    npg, ppg = ctx // PAGE, prefix // PAGE
+    unique = ppg + shared * (npg - ppg) + (bsz - shared) * npg
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+            kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
+                        num_layers=pool_layers)
+    finally:
+        torch.set_default_dtype(torch.float32)
+    kv.kv_cache.normal_()
+    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx, device=dev)
+    runner.generator = torch.Generator(device=dev).manual_seed(5)
+    g = torch.Generator().manual_seed(55)
+    perm = torch.randperm(unique, generator=g).tolist()
+    prefix_pages, o = perm[:ppg], ppg
+    seqs = []
+    for i in range(bsz):
+        if i < shared:
+            bt = prefix_pages + perm[o : o + npg - ppg]
+            o += npg - ppg
+        else:
+            bt = perm[o : o + npg]
+            o += npg
+        seqs.append(SeqSchedule(seq_id=i, token_ids=[int(torch.randint(0, cfg.vocab_size, (1,), generator=g))],
+                                num_cached_tokens=ctx - 1, block_table=bt, temperature=1.0, top_p=0.95))
+    runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
+
+    def step():
+        return runner._sample_logits(runner.decode_hidden(bsz), bsz)
+
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ids = step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
+    per_tok_layer = cfg.num_key_value_heads * 128 * 2 * 2
+    kv_seq = bsz * ctx * cfg.num_hidden_layers * per_tok_layer
+    kv_unique = unique * PAGE * cfg.num_hidden_layers * per_tok_layer
+    roof_ms = (wbytes + kv_seq) / (HBM_PEAK_GBS * 1e9) * 1e3
+    runner.destroy()
+    assert ids.shape[0] == bsz
+    return {"model": "Qwen3-32B-shaped (64 layers, 64q/8kv, FFN 25600)", "batch": bsz, "context": ctx,
+            "shared_prefix": f"{shared} requests x {prefix} tokens", "sampling": "top-p 0.95 (T 1.0)",
+            "kv_pool_layers": pool_layers, "ms_per_step": round(ms, 3), "tok_per_s": round(bsz / (ms * 1e-3), 1),
+            "weight_bytes": wbytes, "kv_bytes_per_seq": kv_seq, "kv_bytes_unique_pages": kv_unique,
+            "roofline_ms": round(roof_ms, 3), "frac_of_roofline": round(roof_ms / ms, 4),
+            "achieved_GB/s_per_seq_bytes": round((wbytes + kv_seq) / (ms * 1e-3) / 1e9, 1)}
+
+
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
               max_num_seqs: int = 256, max_num_batched_tokens: int = 8192) -> dict:
     """Config 4: Qwen3-8B (random bf16 weights ~N(0,0.02)) serving 256 requests
@@ -467,6 +541,8 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill attention cases")
     ap.add_argument("--serve", action="store_true", help="also run config 4 (256 requests, greedy and sampled)")
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
+    ap.add_argument("--config5", action="store_true", help="also run config 5 (Qwen3-32B-shaped long-context decode)")
+    ap.add_argument("--config5-only", action="store_true", help="only config 5 (for profiling)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
@@ -493,6 +569,9 @@ def main() -> int:
     ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
     if args.e2e_only:
         print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
+        return 0
+    if args.config5_only:
+        print(json.dumps(decode_config5(torch, dev)))
         return 0
     if args.serve_only:
         print(json.dumps({"serve_greedy": serve_e2e(torch, dev, sampled=False),
@@ -558,6 +637,9 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["decode_e2e"] = decode_e2e(torch, dev, ctx)
         line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
+    if args.config5:
+        torch.cuda.empty_cache()
+        line["config5"] = decode_config5(torch, dev)
     if args.serve:
         torch.cuda.empty_cache()
         line["serve_greedy"] = serve_e2e(torch, dev, sampled=False)
