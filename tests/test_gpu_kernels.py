@@ -223,6 +223,9 @@ def test_silu_and_mul(dev, t, inter):
         (16, 8, [70, 5], [70, 200], True),                      # Qwen3-0.6B heads
         (64, 8, [33], [129], True),                             # group 8
         (8, 8, [20, 0, 9], [20, 0, 40], False),                 # MHA, an empty sequence
+        (32, 8, [777, 64], [777, 64], False),                   # long prompt: many tiles, odd tail
+        (32, 8, [300, 129], [2100, 1129], True),                # long chunks over long cached prefixes
+        (16, 8, [161], [1000], True),                           # group 2, 64-query blocks
     ],
 )
 def test_prefill_attention(dev, hq, hkv, qlens, klens, paged):
@@ -368,3 +371,46 @@ def test_paged_decode_workspace_reuse_across_batches(dev):
         print(f"workspace reuse: B {bsz} ctx [{lo},{hi})", flush=True)
         assert torch.isfinite(out.float()).all()
         _close(f32(out).reshape(bsz, 32, 128)[rows], want)
+
+
+# ------------------------------------------------------------------ config 3 at full size
+def test_config3_elementwise_full_size(dev):
+    """Config 3 shapes (T 8192, Qwen3-8B width) through each fused kernel; 64
+    seeded rows checked against the oracle (every op is row-wise), the whole
+    output checked finite, the residual of add+RMSNorm bit-exact."""
+    import xvllm.layers.ops  # noqa: F401
+    from xvllm.layers.rotary import build_cos_sin_cache
+
+    g = gen(33)
+    T, H, I, HQ_, HKV_, D_ = 8192, 4096, 12288, 32, 8, 128
+    rows = torch.randperm(T, generator=g)[:64].sort().values
+    r = rows.numpy()
+    # residual-add + RMSNorm
+    x, res = randn_bf16((T, H), g), randn_bf16((T, H), g)
+    w = randn_bf16((H,), g, 0.1, 1.0)
+    xd, rd = x.to(dev), res.to(dev)
+    torch.ops.vllm.fused_add_rmsnorm(xd, rd, w.to(dev), 1e-6)
+    torch.cuda.synchronize()
+    want_x, want_r = O.fused_add_rmsnorm(f32(x)[r], f32(res)[r], f32(w), 1e-6)
+    assert torch.isfinite(xd.float()).all()
+    _close(f32(xd.cpu())[r], want_x)
+    assert np.array_equal(f32(rd.cpu())[r], want_r)
+    del x, res, xd, rd
+    # q/k RMSNorm + RoPE (theta 1e6, positions U[0, 32768))
+    q, k = randn_bf16((T, HQ_, D_), g), randn_bf16((T, HKV_, D_), g)
+    qw, kw = randn_bf16((D_,), g, 0.1, 1.0), randn_bf16((D_,), g, 0.1, 1.0)
+    pos = torch.randint(0, 32768, (T,), generator=g)
+    cs = build_cos_sin_cache(D_, 32768, 1e6)
+    qo, ko = torch.ops.xv.qk_norm_rope(q.to(dev), k.to(dev), qw.to(dev), kw.to(dev), 1e-6, pos.to(dev), cs.to(dev))
+    torch.cuda.synchronize()
+    want_q, want_k = O.qk_norm_rope(f32(q)[r], f32(k)[r], f32(qw), f32(kw), 1e-6, pos.numpy()[r], cs.numpy())
+    for got, want in ((qo, want_q), (ko, want_k)):
+        assert torch.isfinite(got.float()).all()
+        _close(f32(got.cpu())[r], want)
+    del q, k, qo, ko
+    # SiLU(gate) * up at width 12288
+    xg = randn_bf16((T, 2 * I), g)
+    out = torch.ops.vllm.silu_and_mul(xg.to(dev))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    _close(f32(out.cpu())[r], O.silu_and_mul(f32(xg)[r]))
