@@ -527,6 +527,65 @@ def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
     }
 
 
+def cpu_baseline_rows(budget_s: float = 1.0) -> dict:
+    """The oracle (the CPU restatement of each reference op) timed on the host,
+    one thread, on bounded samples of the config-3 / prefill / sampler
+    workloads; each row is repeated until `budget_s` is used, after one
+    untimed call."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    import oracle.ops as O
+    import oracle.sampler as S
+
+    rng = np.random.default_rng(8)
+    out = {}
+
+    def run(name, fn, units, unit, sample):
+        fn()  # first call (page-in of numpy's temporaries) untimed
+        t_used, n = 0.0, 0
+        while t_used < budget_s:
+            t0 = time.perf_counter()
+            fn()
+            t_used += time.perf_counter() - t0
+            n += 1
+        out[name] = {"value": round(units * n / t_used, 3), "unit": unit, "cores": 1, "kind": "port",
+                     "sample": f"{sample}, {n} repetitions, {t_used:.1f} s"}
+
+    r = lambda *sh: rng.standard_normal(sh, dtype=np.float32)
+    with threadpool_limits(limits=1):
+        T = 1024
+        k, v = r(T, HKV, D), r(T, HKV, D)
+        kc, vc = np.zeros((1024, PAGE, HKV, D), np.float32), np.zeros((1024, PAGE, HKV, D), np.float32)
+        slots = rng.permutation(1024 * PAGE)[:T]
+        run("store_kvcache", lambda: O.store_kvcache(k, v, kc.reshape(-1, HKV, D), vc.reshape(-1, HKV, D), slots),
+            (2 * T * HKV * D * 2 * 2 + 4 * T) / 1e9, "GB/s", f"{T} tokens x 8 kv heads x 128")
+        x, res, w = r(128, 4096), r(128, 4096), r(4096)
+        run("fused_add_rmsnorm", lambda: O.fused_add_rmsnorm(x, res, w, 1e-6), 128 * 4096 * 2 * 4 / 1e9, "GB/s",
+            "128 rows x 4096")
+        q, kk, qw, kw = r(256, HQ, D), r(256, HKV, D), r(D), r(D)
+        pos, cs = rng.integers(0, 32768, 256), O.build_cos_sin_cache(D, 32768, 1e6)
+        run("qk_norm_rope", lambda: O.qk_norm_rope(q, kk, qw, kw, 1e-6, pos, cs),
+            256 * (HQ + HKV) * D * 2 * 2 / 1e9, "GB/s", "256 tokens x (32 + 8) heads x 128")
+        xg = r(64, 2 * 12288)
+        run("silu_and_mul", lambda: O.silu_and_mul(xg), 64 * 3 * 12288 * 2 / 1e9, "GB/s", "64 rows x 12288")
+        L = 512
+        qp, kp, vp = r(L, HQ, D), r(L, HKV, D), r(L, HKV, D)
+        cu = np.array([0, L], np.int32)
+        run("prefill_attention", lambda: O.prefill_attention(qp, cu, cu, k=kp, v=vp),
+            4 * HQ * D * L * (L + 1) / 2 / 1e12, "TFLOP/s", f"one causal {L}-token prompt, 32 q / 8 kv heads")
+        V = 151936
+        bits = (rng.standard_normal((4, V)).astype(np.float32) * 2).view(np.uint32) >> 16
+        logits = bits.astype(np.uint16)
+        t = np.full(4, 0.7, np.float32)
+        run("sampler_k50_p0.9", lambda: S.sample(logits, t, np.full(4, 0.9, np.float32), np.full(4, 50, np.int32),
+                                                 None, rng.random(4).astype(np.float32), 2 | 4),
+            4 * V * 2 / 1e9, "GB/s", "4 rows x 151936 (C oracle)")
+        run("sampler_greedy", lambda: S.sample(logits, np.zeros(4, np.float32), None, None, None, None, 1),
+            4 * V * 2 / 1e9, "GB/s", "4 rows x 151936 (C oracle)")
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -646,6 +705,7 @@ def main() -> int:
         line["serve_sampled"] = serve_e2e(torch, dev, sampled=True)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctx)
+        line["cpu_baseline_rows"] = cpu_baseline_rows()
     print(json.dumps(line))
     return 0
 
