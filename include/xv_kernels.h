@@ -199,7 +199,10 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  * over the kept set in ascending id order with the explicit uniform
  * uniforms[b] in [0, 1), masses in 2^-40 fixed point (exact integer sums).
  * flags: XV_SAMPLE_* bits mirroring the reference's host-side switches.
- * workspace: at least xv_sampler_workspace_size(B, V) bytes.
+ * workspace: xv_sampler_workspace_size(B, V) bytes, zero-filled before its
+ *   first use (each call leaves it zero), used by all-greedy calls to spread a
+ *   row over several workgroups; NULL selects one workgroup per row.  Calls
+ *   sharing a workspace must be ordered on one stream.
  */
 #define XV_SAMPLE_ALL_GREEDY 1
 #define XV_SAMPLE_USE_TOP_K  2

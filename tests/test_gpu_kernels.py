@@ -414,3 +414,30 @@ def test_config3_elementwise_full_size(dev):
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
     _close(f32(out.cpu())[r], O.silu_and_mul(f32(xg)[r]))
+
+
+@pytest.mark.parametrize("b,v", [(1, 151936), (7, 4099), (64, 151936), (300, 32000)])
+def test_greedy_multi_workgroup_bitexact(dev, b, v):
+    """All-greedy batches spread each row over several workgroups (one 64-bit
+    atomic max per wave).  Against the C oracle: ties at the maximum (lowest id
+    wins), -0 vs +0 (equal), NaN entries skipped, an all-NaN row (id 0); and a
+    second call on the same workspace (its slots must have been cleared)."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(b + v)
+    x = torch.round(torch.randn((b, v), generator=g) * 4) / 4  # few distinct values: ties at the max
+    x = x.to(torch.bfloat16)
+    bits = x.view(torch.int16)
+    if b >= 7:
+        bits[1, :] = torch.tensor(0x7FC0, dtype=torch.int16)  # all-NaN row
+        bits[2, :] = torch.tensor(-32768, dtype=torch.int16)  # all -0.0 ...
+        bits[2, 5:9] = 0                                      # ... a few +0.0 after the first ids
+        bits[3, ::5] = torch.tensor(0x7FC0, dtype=torch.int16)  # NaNs among values
+    for call in range(2):
+        xs = x if call == 0 else x.flip(1).contiguous()
+        want = S.sample(xs.view(torch.int16).numpy().view(np.uint16), np.zeros(b, np.float32), None, None, None,
+                        None, 1)
+        got = sample(xs.to(dev), None, all_greedy=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), want), f"call {call}: {got.cpu().numpy()[:8]} vs {want[:8]}"

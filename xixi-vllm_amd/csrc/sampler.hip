@@ -851,21 +851,120 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
   if (t == 0) out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
 }
 
+// ---------------------------------------------------------------------------
+// All-greedy batches over several workgroups per row (a small batch would
+// leave most CUs idle with one workgroup per row).  A lane keeps the largest
+// logit of its ids and the lowest id holding it (float compares: -0 equals
+// +0, NaN never wins), as the one-workgroup path does.  Each workgroup then
+// folds its best into the row's 64-bit slot with one atomic max of
+//   order key << 32 | (2^32 - 1 - id)
+// (the largest logit wins, among equal logits the lowest id) and counts
+// itself in the row's arrival counter; the last workgroup of the row writes the id
+// and clears both words for the next call.  Every atomic is awaited before
+// the next one is issued, so the count is only bumped after the workgroup's
+// max has been performed.  Atomics on one cache line serialise, so each row
+// has its own line and is cut into at most 32 segments.
+constexpr int kGreedyThreads = 256;
+constexpr int kGreedyUnroll = 8;
+constexpr int kGreedyLine = 16;  // u64 words per row: its slot, then its arrival counter, one 128-byte line
+
+__global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf16_t* __restrict__ logits,
+                                                                        int64_t stride, int V, int seg_len,
+                                                                        unsigned long long* __restrict__ slots,
+                                                                        unsigned int* __restrict__ arrivals,
+                                                                        int64_t* __restrict__ out_ids) {
+  const int b = blockIdx.y;
+  const bf16_t* row = logits + (int64_t)b * stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = blockIdx.x * seg_len, end = min(V, beg + seg_len);
+  float fm = -INFINITY;
+  int bid = -1;
+  constexpr int step = kGreedyThreads * 8;
+  for (int i0 = beg + threadIdx.x * 8; i0 < end; i0 += kGreedyUnroll * step) {
+    uint32_t bits[kGreedyUnroll][8];
+#pragma unroll
+    for (int u = 0; u < kGreedyUnroll; ++u)
+      if (i0 + u * step < end) load8(row, V, i0 + u * step, vec_ok, bits[u]);
+#pragma unroll
+    for (int u = 0; u < kGreedyUnroll; ++u) {
+      const int i = i0 + u * step;
+      if (i >= end) break;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float v = bf16_to_f32(bits[u][k]);
+        const bool better = v > fm && i + k < end;  // ids ascend within a lane: keeps the lowest
+        fm = better ? v : fm;
+        bid = better ? i + k : bid;
+      }
+    }
+  }
+  unsigned long long best = 0;
+  if (bid >= 0) {
+    const uint32_t fb = __float_as_uint(fm) >> 16;
+    best = ((unsigned long long)order_key(fb == 0x8000u ? 0u : fb) << 32) | (0xffffffffu - (uint32_t)bid);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long y = __shfl_xor(best, o);
+    best = y > best ? y : best;
+  }
+  __shared__ unsigned long long wbest[kGreedyThreads / 64];
+  if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < kGreedyThreads / 64; ++w) best = wbest[w] > best ? wbest[w] : best;
+    const unsigned int waves = gridDim.x;  // arrivals per row: one per workgroup
+    // returning atomics: each result is awaited before the next is issued
+    unsigned long long seen = 0;
+    unsigned long long* slot = slots + (int64_t)b * kGreedyLine;
+    unsigned int* arrival = arrivals + (int64_t)b * 2 * kGreedyLine;
+    if (best) seen = __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // (a slot never holds all ones -- keys fit 16 bits -- so the increment is 1,
+    // but it depends on the max's result, which keeps the two in order)
+    const unsigned int inc = seen == ~0ull ? 0u : 1u;
+    const unsigned int n = __hip_atomic_fetch_add(arrival, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (n == waves - 1) {
+      const unsigned long long c = __hip_atomic_fetch_max(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      out_ids[b] = c ? (int64_t)(0xffffffffu - (uint32_t)c) : 0;  // all-NaN row: 0, as the one-workgroup path
+      __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(arrival, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 }  // namespace
 
+// Workspace: one 128-byte line per row (a 64-bit slot and a 32-bit arrival
+// counter) for the multi-workgroup greedy path; the other paths keep their
+// scratch in LDS.
 extern "C" size_t xv_sampler_workspace_size(int batch, int vocab) {
-  (void)batch; (void)vocab;
-  return 0;  // all scratch lives in LDS
+  (void)vocab;
+  return ((size_t)(batch > 0 ? batch : 0) * kGreedyLine * 8 + 255) / 256 * 256;
 }
 
 extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
                          const float* temperatures, const float* top_ps, const int32_t* top_ks,
                          const float* min_ps, const float* uniforms, int flags,
                          int64_t* out_ids, void* workspace, size_t workspace_bytes, hipStream_t stream) {
-  (void)workspace; (void)workspace_bytes;
   if (batch < 0 || vocab <= 0 || logits_stride < vocab) return (int)hipErrorInvalidValue;
   if (!(flags & XV_SAMPLE_ALL_GREEDY) && temperatures == nullptr) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
+  // All-greedy batches: several workgroups per row, about 1024 in all.
+  if ((flags & XV_SAMPLE_ALL_GREEDY) && workspace != nullptr &&
+      workspace_bytes >= xv_sampler_workspace_size(batch, vocab) && batch <= 65535) {
+    // segments of whole 8-id vectors
+    const int segs = max(1, min(32, 1024 / batch));
+    const int seg_len = ((vocab + segs - 1) / segs + 7) / 8 * 8;
+    // one 128-byte line per row: atomics on one line serialise, so rows do not share
+    unsigned long long* slots = (unsigned long long*)workspace;
+    unsigned int* arrivals = (unsigned int*)(slots + 1);
+    greedy_segment_kernel<<<dim3((unsigned)((vocab + seg_len - 1) / seg_len), (unsigned)batch),
+                            kGreedyThreads, 0, stream>>>((const bf16_t*)logits, logits_stride, vocab, seg_len, slots,
+                                                         arrivals, out_ids);
+    XV_CHECK_LAUNCH();
+    return 0;
+  }
   sample_kernel<<<dim3((unsigned)batch), dim3(kThreads), 0, stream>>>(
       (const bf16_t*)logits, logits_stride, vocab, temperatures, top_ps, top_ks, min_ps, uniforms, flags, out_ids);
   XV_CHECK_LAUNCH();

@@ -22,6 +22,21 @@ from . import _C
 from ._torch_glue import ptr, require_bf16, require_cuda, stream_of
 
 
+_WORKSPACE: dict[tuple[str, int | None], torch.Tensor] = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Per-device sampler workspace, zero-filled once and grown on demand (the
+    kernels leave it zero after every call).  Calls on one device share it and
+    must be ordered on one stream."""
+    key = (device.type, device.index)
+    ws = _WORKSPACE.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        _WORKSPACE[key] = ws
+    return ws
+
+
 def sample(
     logits: torch.Tensor,
     temperatures: torch.Tensor | None,
@@ -63,10 +78,12 @@ def sample(
     tps, tks, mps, us = prep(top_ps, torch.float32), prep(top_ks, torch.int32), prep(min_ps, torch.float32), prep(uniforms, torch.float32)
     if out is None:
         out = torch.empty(bsz, dtype=torch.int64, device=logits.device)
+    L = _C.lib()
+    ws = _workspace(logits.device, L.xv_sampler_workspace_size(bsz, vocab))
     _C.check(
-        _C.lib().xv_sample(
+        L.xv_sample(
             ptr(logits), logits.stride(0), bsz, vocab, ptr(temps), ptr(tps), ptr(tks), ptr(mps), ptr(us), flags,
-            ptr(out), None, 0, stream_of(logits),
+            ptr(out), ptr(ws), ws.numel(), stream_of(logits),
         ),
         "xv_sample",
     )
