@@ -68,8 +68,8 @@ XV_INLINE __amdgpu_buffer_rsrc_t rsrc(const bf16_t* base, uint32_t bytes) {
 }
 
 // Wave w moves keys key0+16w .. +15 of the tile (one cache page when paged):
-// 4 LDS-DMA instructions for K and 4 for V, each 4 whole rows.
-template <bool PAGED>
+// 4 LDS-DMA instructions for K and/or 4 for V, each 4 whole rows.
+template <bool PAGED, bool DO_K, bool DO_V>
 XV_INLINE void load_rows(char* buf, const PrefillArgs& a, int b, int kvh, int key0, int k0, int k_len, int page,
                          int wave, int lane) {
   const int j0 = key0 + 16 * wave;
@@ -92,9 +92,11 @@ XV_INLINE void load_rows(char* buf, const PrefillArgs& a, int b, int kvh, int ke
     const int R = 16 * wave + r;        // row within the tile
     const int vo_k = (int)(r * rs * 2) + ((slot ^ swz_k(R)) << 4);
     const int vo_v = (int)(r * rs * 2) + ((slot ^ swz_v(R)) << 4);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + (16 * wave + 4 * s) * 256), 16, vo_k, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kTile + (16 * wave + 4 * s) * 256), 16, vo_v, 0,
-                                             0, 0);
+    if (DO_K)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + (16 * wave + 4 * s) * 256), 16, vo_k, 0, 0, 0);
+    if (DO_V)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kTile + (16 * wave + 4 * s) * 256), 16, vo_v,
+                                               0, 0, 0);
   }
 }
 
@@ -261,36 +263,24 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     const int j = t * kKeys + 16 * wave;
     return j < k_len ? __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.bt_stride + j / 16]) : 0;
   };
-  int page_next = ntiles > 0 ? page_of(0) : 0;
-  if (ntiles > 0) load_rows<PAGED>(lds, a, b, kvh, 0, k0, k_len, page_next, wave, lane);
-  if (ntiles > 1) page_next = page_of(1);
   const LdsAddr ad = lds_addr(lds, lane);
-  // one tile: wait for it, start the next one's loads, compute
-  auto tile = [&](auto par_tag, int t) {
+  // S^T of one tile from K buffer PAR
+  auto s_tile = [&](auto par_tag, floatx16_t (&s)[2]) {
     constexpr int PAR = decltype(par_tag)::value;
-    __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();  // tile t is in LDS; every wave is done with tile t-1
-    if (t + 1 < ntiles) {
-      load_rows<PAGED>(lds + (1 - PAR) * kBuf, a, b, kvh, (t + 1) * kKeys, k0, k_len, page_next, wave, lane);
-      if (t + 2 < ntiles) page_next = page_of(t + 2);
-    }
+    bf16x8_t kf[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[0][r] = s[1][r] = 0.f;
+    read_k16<PAR>(kf, ad);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[u], qb[u], s[0], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);  // the wait below stays behind these MFMAs
+    k_wait_rest(kf);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[8 + u], qb[u], s[1], 0, 0, 0);
+  };
+  // online softmax of tile t's scores s -> P (bf16), O and l rescaled as needed
+  auto softmax = [&](int t, floatx16_t (&s)[2], bf16x8_t (&pb)[2][2]) {
     const int key0 = t * kKeys;
-    if (key0 >= wave_kend) return;
-    // ---- S^T = K Q^T ----
-    floatx16_t s[2];
-    {
-      bf16x8_t kf[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) s[0][r] = s[1][r] = 0.f;
-      read_k16<PAR>(kf, ad);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s[0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[u], qb[u], s[0], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);  // the wait below stays behind these MFMAs
-      k_wait_rest(kf);
-#pragma unroll
-      for (int u = 0; u < 8; ++u) s[1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[8 + u], qb[u], s[1], 0, 0, 0);
-    }
-    // ---- mask, online softmax over the lane's 32 keys + its partner half ----
     // (on raw scores: scale > 0 keeps the order; p = exp2(s*scale - m*scale))
     if (key0 + kKeys > wave_kfull) {  // the tile crosses some query's diagonal
 #pragma unroll
@@ -317,7 +307,6 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
       for (int n = 0; n < 4; ++n) o[n] *= alpha;
     }
     const float nm = m_run == -INFINITY ? 0.f : -m_run;  // fully masked so far: p = 0
-    bf16x8_t pb[2][2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -333,7 +322,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
         }
         __builtin_memcpy(&pb[mt][kk], w, 16);
       }
-    // ---- O^T += V^T P^T ----
+  };
+  // O^T += V^T P^T from V buffer PAR
+  auto pv_tile = [&](auto par_tag, const bf16x8_t (&pb)[2][2]) {
+    constexpr int PAR = decltype(par_tag)::value;
 #pragma unroll
     for (int k2 = 0; k2 < 2; ++k2) {  // key-steps 2k2, 2k2+1 (= key tile mt = k2)
       short4_t vt[16];
@@ -352,9 +344,39 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
           o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vt_operand(vt, n, j), pb[k2][j], o[n], 0, 0, 0);
     }
   };
+
+  // Software pipeline, one tile deep: iteration t computes S(t+1) from K
+  // buffer (t+1)&1 while the softmax of tile t (scores from the previous
+  // iteration) runs on the VALU, then O += P(t) V(t) from V buffer t&1.  K
+  // therefore runs a tile ahead of V: iteration t loads K(t+2) into the K
+  // buffer S(t) used and V(t+1) into the V buffer P(t-1) V(t-1) used, both
+  // freed by the barrier at its top.
+  int pv_page = ntiles > 1 ? page_of(1) : 0, pk_page = ntiles > 2 ? page_of(2) : 0;
+  if (ntiles > 0) load_rows<PAGED, true, true>(lds, a, b, kvh, 0, k0, k_len, page_of(0), wave, lane);
+  if (ntiles > 1) load_rows<PAGED, true, false>(lds + kBuf, a, b, kvh, kKeys, k0, k_len, pv_page, wave, lane);
+  __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  // scores of even tiles in s_even, of odd tiles in s_odd (no copies)
+  floatx16_t s_even[2], s_odd[2];
+  if (ntiles > 0 && 0 < wave_kend) s_tile(std::integral_constant<int, 0>{}, s_even);
+  auto iter = [&](auto par_tag, int t, floatx16_t (&sc)[2], floatx16_t (&sn)[2]) {
+    constexpr int PAR = decltype(par_tag)::value;  // t & 1
+    __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();  // K(t+1) and V(t) are in LDS; every wave is done with iteration t-1
+    if (t + 2 < ntiles) load_rows<PAGED, true, false>(lds + PAR * kBuf, a, b, kvh, (t + 2) * kKeys, k0, k_len, pk_page, wave, lane);
+    if (t + 1 < ntiles) load_rows<PAGED, false, true>(lds + (1 - PAR) * kBuf, a, b, kvh, (t + 1) * kKeys, k0, k_len, pv_page, wave, lane);
+    pv_page = pk_page;
+    if (t + 3 < ntiles) pk_page = page_of(t + 3);
+    if (t + 1 < ntiles && (t + 1) * kKeys < wave_kend) s_tile(std::integral_constant<int, 1 - PAR>{}, sn);
+    if (t * kKeys < wave_kend) {
+      bf16x8_t pb[2][2];
+      softmax(t, sc, pb);
+      pv_tile(par_tag, pb);
+    }
+  };
   for (int t = 0; t < ntiles; t += 2) {
-    tile(std::integral_constant<int, 0>{}, t);
-    if (t + 1 < ntiles) tile(std::integral_constant<int, 1>{}, t + 1);
+    iter(std::integral_constant<int, 0>{}, t, s_even, s_odd);
+    if (t + 1 < ntiles) iter(std::integral_constant<int, 1>{}, t + 1, s_odd, s_even);
   }
   // ---- normalise and write: lane holds O[my_q][32n + 8j + 4(l/32) + r] ----
   const float lsum = xor32_sum(l_run);
