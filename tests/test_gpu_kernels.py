@@ -259,6 +259,8 @@ def _sampler_case(g, b, v, std=2.0, ties=False):
     x = torch.randn((b, v), generator=g) * std
     if ties is True:
         x = torch.round(x * 4) / 4  # few distinct values: ties everywhere
+    if ties == "massive":
+        x = torch.round(torch.randn((b, v), generator=g)) / 2  # ~7 values, tie groups of up to ~58k ids
     return x.to(torch.bfloat16)
 
 
@@ -273,9 +275,17 @@ def _sampler_case(g, b, v, std=2.0, ties=False):
         ("minp", 8, 151936, 8, 1.0, 1.0, 0, 0.1, False),
         ("all_filters_ties", 8, 32000, 2 | 4 | 8, 0.8, 0.8, 300, 0.02, True),
         ("odd_vocab", 5, 1003, 2 | 4, 1.1, 0.6, 7, 0.0, False),
-        # near-flat rows: the boundary bucket overflows LDS -> the row-wide radix-select path
-        ("flat_fallback_topp", 4, 151936, 4, 1.0, 0.5, 0, 0.0, "flat"),
-        ("flat_fallback_topk", 4, 151936, 2 | 4, 1.0, 0.9, 20000, 0.0, "flat"),
+        # near-flat rows: the bucket scale adapts to the row's span
+        ("flat_topp", 4, 151936, 4, 1.0, 0.5, 0, 0.0, "flat"),
+        ("flat_topk", 4, 151936, 2 | 4, 1.0, 0.9, 20000, 0.0, "flat"),
+        ("flat_topp0.95_b32", 32, 151936, 4, 1.0, 0.95, 0, 0.0, "flat"),
+        ("flat_all_odd_vocab", 6, 151935, 2 | 4 | 8, 1.0, 0.7, 30000, 0.3, "flat"),
+        ("flat_minp", 4, 151936, 8, 0.5, 1.0, 0, 0.9, "flat"),
+        # tie groups larger than LDS: the boundary bucket overflows -> the row-wide radix-select path
+        ("ties_fallback_topp", 4, 151936, 4, 1.0, 0.5, 0, 0.0, "massive"),
+        ("ties_fallback_topk", 4, 151936, 2 | 4, 1.0, 0.9, 20000, 0.0, "massive"),
+        ("ties_fallback_all_odd_vocab", 6, 151935, 2 | 4 | 8, 0.8, 0.7, 30000, 0.3, "massive"),
+        ("ties_fallback_minp", 4, 151936, 8, 1.0, 1.0, 0, 0.5, "massive"),
     ],
 )
 def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, ties):

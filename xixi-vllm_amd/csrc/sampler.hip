@@ -28,6 +28,11 @@
 
 #pragma clang fp contract(off)
 
+// Phase timestamps for out-of-tree timing builds; compiled out here.
+#ifndef XV_SAMPLER_TIMESTAMP
+#define XV_SAMPLER_TIMESTAMP(slot)
+#endif
+
 namespace {
 
 constexpr int kThreads = 1024;
@@ -66,9 +71,18 @@ XV_INLINE float log2_ratio(uint32_t bits, float inv_t, float zmax) {
 }
 XV_INLINE float exp_of(uint32_t bits, float inv_t, float zmax) { return sampler_exp2(log2_ratio(bits, inv_t, zmax)); }
 XV_INLINE int64_t mass_of(float e) { return (int64_t)(e * 1099511627776.0f); }
-XV_INLINE int bucket_of(float d) {
-  const float u = -d * 16.0f;
+// Bucket of a candidate d below the max: floor(-d * bs), the last bucket
+// holding everything further.  bs is per row (bucket_scale); any bs > 0 keeps
+// the buckets monotone in the key, which is all the boundary search needs.
+XV_INLINE int bucket_of(float d, float bs) {
+  const float u = -d * bs;
   return u < 255.0f ? (int)u : 255;
+}
+// 16 buckets per binary order, finer when the row spans less than 255/16
+// orders below its max (near-flat rows), so that the smallest candidate lands
+// in the last bucket and the row spreads over all of them.
+XV_INLINE float bucket_scale(float dmin) {
+  return (-dmin * 16.0f >= 255.0f || !(-dmin > 1e-30f)) ? 16.0f : 255.0f / -dmin;
 }
 
 // Load the 8 logits of thread t in tile j (bits, 0xffff = NaN for padding).
@@ -112,17 +126,17 @@ XV_INLINE void for_each_strided(const bf16_t* row, int V, bool vec_ok, F&& f) {
   }
 }
 
-template <typename F>
+template <int CH = kChunk, typename F>
 XV_INLINE void for_each_elem(const bf16_t* row, int V, bool vec_ok, F&& f) {
   const int C = range_len(V);
   const int i0 = threadIdx.x * C, i1 = min(V, i0 + C);
-  for (int c = i0; c < i1; c += 8 * kChunk) {
-    uint32_t bits[kChunk][8];
+  for (int c = i0; c < i1; c += 8 * CH) {
+    uint32_t bits[CH][8];
 #pragma unroll
-    for (int v = 0; v < kChunk; ++v)
+    for (int v = 0; v < CH; ++v)
       if (c + 8 * v < i1) load8(row, V, c + 8 * v, vec_ok, bits[v]);
 #pragma unroll
-    for (int v = 0; v < kChunk; ++v)
+    for (int v = 0; v < CH; ++v)
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const int id = c + 8 * v + k;
@@ -240,32 +254,94 @@ XV_INLINE bool earlier(const Boundary& a, const Boundary& b) {
   return a.key > b.key || (a.key == b.key && a.tie < b.tie);
 }
 
+// Call f(bits, id) for every slot of a lane-interleaved layout like that of
+// for_each_strided (kChunkAll vectors per step) on every lane of every wave: slots at or past V come as
+// 0xffff (key 0), so f may use wave-wide operations.
+constexpr int kChunkAll = 8;
+template <typename F>
+XV_INLINE void for_each_strided_all(const bf16_t* row, int V, bool vec_ok, F&& f) {
+  const int nvec = (V + 7) / 8;
+  for (int c = 0; c * kChunkAll * kThreads < nvec; ++c) {
+    uint32_t w[kChunkAll][4];  // packed pairs, low half first
+#pragma unroll
+    for (int v = 0; v < kChunkAll; ++v) {
+      const int base = ((c * kChunkAll + v) * kThreads + threadIdx.x) * 8;
+      if (vec_ok && base + 8 <= V) {
+        const Vec8 x = load_vec8(row + base);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[v][k] = x.w[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          w[v][k] = (base + 2 * k < V ? (uint32_t)row[base + 2 * k] : 0xffffu) |
+                    (base + 2 * k + 1 < V ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kChunkAll; ++v)
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        f((w[v][k >> 1] >> (16 * (k & 1))) & 0xffffu, ((c * kChunkAll + v) * kThreads + threadIdx.x) * 8 + k);
+  }
+}
+
+// Add one count (CNT) and the mass m (MASS) to bin `bin` of the LDS
+// histograms for every lane with `on`.  The lanes of each of the wave's first
+// four distinct bins are summed first and added with one atomic per
+// histogram: near-flat rows put nearly every candidate into two or three
+// high-byte bins, where per-lane atomics to one address serialise.  Lanes of
+// further bins add their own.  Called by the whole wave.
+template <bool CNT, bool MASS>
+XV_INLINE void hist_add(uint32_t* cnt, unsigned long long* mass, bool on, int bin, int64_t m) {
+  const int lane = threadIdx.x & 63;
+  bool pending = on;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const unsigned long long todo = __ballot(pending);
+    if (todo == 0ull) break;
+    const int lead = __builtin_ctzll(todo);
+    const int lb = __shfl(bin, lead);
+    const bool mine = pending && bin == lb;
+    const unsigned long long mm = __ballot(mine);
+    const int64_t sm = MASS ? wave_sum_l(mine ? m : 0) : 0;
+    if (lane == lead) {
+      if (CNT) atomicAdd(&cnt[lb], (uint32_t)__popcll(mm));
+      if (MASS) atomicAdd(&mass[lb], (unsigned long long)sm);
+    }
+    pending = pending && !mine;
+  }
+  if (pending) {
+    if (CNT) atomicAdd(&cnt[bin], 1u);
+    if (MASS) atomicAdd(&mass[bin], (unsigned long long)m);
+  }
+}
+
+XV_INLINE void clear_hist(Shared& s) {
+  __syncthreads();
+  for (int i = threadIdx.x; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
+  __syncthreads();
+}
+
 // Exact cut-offs by a two-level (high byte, low byte) radix select over LDS
 // histograms of the whole row: the fallback when the boundary bucket of the
 // fast path holds more candidates than LDS does (very flat distributions).
-XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t,
-                                float zmax, int top_k, float top_p, float min_p, bool use_k, bool use_p,
-                                bool use_m, Boundary& bd_out, int64_t& id_cut_out, int64_t& M_out) {
+// Histogram passes read the row in chunks of kChunk vectors per thread (a few
+// memory round trips per pass).
+XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok, float inv_t, float zmax,
+                                int top_k, float top_p, float min_p, bool use_k, bool use_p, bool use_m,
+                                Boundary& bd_out, int64_t& id_cut_out, int64_t& M_out) {
   const int t = threadIdx.x;
   Boundary bd = {1u, kTieAll};
   if (use_k || use_p || use_m) {
     // ---- pass 2: high-byte histogram of counts and masses; min-p key ----
-    for (int i = t; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
-    __syncthreads();
+    clear_hist(s);
     uint32_t kmin_p = 0xffffffffu;
-    for (int j = 0; j < ntiles; ++j) {
-      uint32_t bits[8];
-      load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t key = order_key(bits[k]);
-        if (!key) continue;
-        const float e = exp_of(bits[k], inv_t, zmax);
-        if (use_m && e >= min_p) kmin_p = min(kmin_p, key);
-        atomicAdd(&s.cnt[key >> 8], 1u);
-        atomicAdd(&s.mass[key >> 8], (unsigned long long)mass_of(e));
-      }
-    }
+    for_each_strided_all(row, V, vec_ok, [&](uint32_t bits, int) {
+      const uint32_t key = order_key(bits);
+      const float e = exp_of(bits, inv_t, zmax);
+      if (use_m && key && e >= min_p) kmin_p = min(kmin_p, key);
+      hist_add<true, true>(s.cnt, s.mass, key != 0, (int)(key >> 8), mass_of(e));
+    });
     kmin_p = use_m ? block_min_u(s, kmin_p) : 0u;
     __syncthreads();
 
@@ -292,19 +368,11 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
       // ---- pass 3: low-byte histogram inside the top-k high bin ----
       const int hb = s.b_hb;
       const int64_t c_above = s.b_tie;
-      __syncthreads();
-      for (int i = t; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
-      __syncthreads();
-      for (int j = 0; j < ntiles; ++j) {
-        uint32_t bits[8];
-        load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t key = order_key(bits[k]);
-          if (!key || (int)(key >> 8) != hb) continue;
-          atomicAdd(&s.cnt[key & 255], 1u);
-        }
-      }
+      clear_hist(s);
+      for_each_strided_all(row, V, vec_ok, [&](uint32_t bits, int) {
+        const uint32_t key = order_key(bits);
+        hist_add<true, false>(s.cnt, s.mass, key != 0 && (int)(key >> 8) == hb, (int)(key & 255), 0);
+      });
       __syncthreads();
       if (t == 0) {
         int64_t c = c_above;
@@ -321,15 +389,9 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
       bk.tie = s.b_tie;
       // mass of the top-k set: everything above the boundary key plus tie_k+1 copies
       int64_t above = 0;
-      for (int j = 0; j < ntiles; ++j) {
-        uint32_t bits[8];
-        load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t key = order_key(bits[k]);
-          if (key > bk.key) above += mass_of(exp_of(bits[k], inv_t, zmax));
-        }
-      }
+      for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
+        if (order_key(bits) > bk.key) above += mass_of(exp_of(bits, inv_t, zmax));
+      });
       above = block_sum_l(s, above);
       total_k = above + (bk.tie + 1) * mass_of(exp_of(key_to_bits(bk.key), inv_t, zmax));
     } else {
@@ -340,19 +402,13 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
     if (use_p) {
       // ---- pass 4: first rank whose inclusive mass exceeds floor(top_p * total_k) ----
       const int64_t thr = (int64_t)floor((double)top_p * (double)total_k);
-      // high-byte masses are still in s.mass only when top-k did not reuse them: rebuild
-      __syncthreads();
-      for (int i = t; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
-      __syncthreads();
-      for (int j = 0; j < ntiles; ++j) {
-        uint32_t bits[8];
-        load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t key = order_key(bits[k]);
-          if (!key) continue;
-          atomicAdd(&s.mass[key >> 8], (unsigned long long)mass_of(exp_of(bits[k], inv_t, zmax)));
-        }
+      if (use_k) {
+        // pass 3 reused the histograms: rebuild the high-byte masses
+        clear_hist(s);
+        for_each_strided_all(row, V, vec_ok, [&](uint32_t bits, int) {
+          const uint32_t key = order_key(bits);
+          hist_add<false, true>(s.cnt, s.mass, key != 0, (int)(key >> 8), mass_of(exp_of(bits, inv_t, zmax)));
+        });
       }
       __syncthreads();
       if (t == 0) {
@@ -370,19 +426,12 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
       const int hb = s.b_hb;
       const int64_t m_above = s.b_total;
       if (hb >= 0) {
-        __syncthreads();
-        for (int i = t; i < 256; i += kThreads) { s.cnt[i] = 0; s.mass[i] = 0; }
-        __syncthreads();
-        for (int j = 0; j < ntiles; ++j) {
-          uint32_t bits[8];
-          load8(row, V, j * kTile + t * 8, vec_ok, bits);
-#pragma unroll
-          for (int k = 0; k < 8; ++k) {
-            const uint32_t key = order_key(bits[k]);
-            if (!key || (int)(key >> 8) != hb) continue;
-            atomicAdd(&s.mass[key & 255], (unsigned long long)mass_of(exp_of(bits[k], inv_t, zmax)));
-          }
-        }
+        clear_hist(s);
+        for_each_strided_all(row, V, vec_ok, [&](uint32_t bits, int) {
+          const uint32_t key = order_key(bits);
+          const bool in = key != 0 && (int)(key >> 8) == hb;
+          hist_add<false, true>(s.cnt, s.mass, in, (int)(key & 255), in ? mass_of(exp_of(bits, inv_t, zmax)) : 0);
+        });
         __syncthreads();
         if (t == 0) {
           int64_t m = m_above;
@@ -409,42 +458,36 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
     }
   }
 
-  // ---- pass 5: id of the boundary tie (when only part of the ties is kept) and kept mass ----
-  int64_t id_cut = kTieAll;  // kept: key > bd.key, or key == bd.key and id <= id_cut
-  int64_t M = 0;
-  {
-    int64_t carry = 0;  // ties of bd.key seen in earlier tiles
-    if (t == 0) s.b_id = kTieAll;
-    for (int j = 0; j < ntiles; ++j) {
-      uint32_t bits[8];
-      const int base = j * kTile + t * 8;
-      load8(row, V, base, vec_ok, bits);
-      int64_t nt = 0;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) nt += order_key(bits[k]) == bd.key;
-      int64_t tile_ties;
-      int64_t r = carry + block_excl_scan(s, nt, &tile_ties);
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t key = order_key(bits[k]);
-        if (!key) continue;
-        bool kept = key > bd.key;
-        if (key == bd.key) {
-          kept = r <= bd.tie;
-          if (r == bd.tie) s.b_id = base + k;
-          ++r;
-        }
-        if (kept) M += mass_of(exp_of(bits[k], inv_t, zmax));
+  // ---- pass 5: kept mass, and the id of the last kept tie of the boundary key ----
+  // Thread t owns the contiguous ids of for_each_elem, so one block scan of the
+  // per-thread tie counts ranks the ties in id order.  Every tie has the same
+  // mass q.
+  int64_t above = 0, nt = 0;
+  for_each_elem(row, V, vec_ok, [&](uint32_t bits, int) {
+    const uint32_t key = order_key(bits);
+    if (key > bd.key) above += mass_of(exp_of(bits, inv_t, zmax));
+    nt += key == bd.key;
+  });
+  int64_t ties;
+  const int64_t r0 = block_excl_scan(s, nt, &ties);
+  const int64_t kept_ties = bd.tie == kTieAll ? ties : min(ties, bd.tie + 1);
+  const int64_t q = kept_ties ? mass_of(exp_of(key_to_bits(bd.key), inv_t, zmax)) : 0;
+  const int64_t M = block_sum_l(s, above) + kept_ties * q;
+  if (t == 0) s.b_id = kTieAll;
+  __syncthreads();
+  if (bd.tie != kTieAll && bd.tie >= r0 && bd.tie < r0 + nt) {
+    int64_t r = r0;
+    for_each_elem<2>(row, V, vec_ok, [&](uint32_t bits, int id) {  // one thread: few registers
+      if (order_key(bits) == bd.key) {
+        if (r == bd.tie) s.b_id = id;
+        ++r;
       }
-      carry += tile_ties;
-    }
-    M = block_sum_l(s, M);
-    id_cut = s.b_id;
-    __syncthreads();  // every thread has read b_id before it is reset below
+    });
   }
-
+  __syncthreads();
+  id_cut_out = s.b_id;
+  __syncthreads();  // every thread has read b_id before it is reset
   bd_out = bd;
-  id_cut_out = id_cut;
   M_out = M;
 }
 
@@ -494,7 +537,7 @@ XV_INLINE void sort_cand_desc(FastShared& fs, int n) {
 // descending (key descending, id ascending).  Returns the count; a count above
 // kMaxCand means the bucket did not fit (nothing sorted).
 XV_INLINE int gather_bucket(FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t,
-                            float zmax, int target, int target_lo = -1) {
+                            float zmax, float bs, int target, int target_lo = -1) {
   if (target_lo < 0) target_lo = target;  // gather buckets target_lo .. target
   const int t = threadIdx.x;
   __syncthreads();
@@ -503,7 +546,7 @@ XV_INLINE int gather_bucket(FastShared& fs, const bf16_t* row, int V, bool vec_o
   for_each_strided(row, V, vec_ok, [&](uint32_t bits, int id) {
     const uint32_t key = order_key(bits);
     if (!key) return;
-    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax));
+    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax), bs);
     if (bkt < target_lo || bkt > target) return;
     const int slot = atomicAdd(&fs.ncand, 1);
     if (slot < kMaxCand)
@@ -570,7 +613,7 @@ XV_INLINE uint32_t minp_key(Shared& s, const bf16_t* row, int V, bool vec_ok, in
 // the buckets up to the one holding rank k-1 is gathered and sorted; the
 // top-k set, its mass, the top-p and min-p cuts all come from that list.
 XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
-                             float inv_t, float zmax, int top_k, float top_p, float min_p, bool use_p, bool use_m,
+                             float inv_t, float zmax, float bs, int top_k, float top_p, float min_p, bool use_p, bool use_m,
                              uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
   const int t = threadIdx.x, w = t >> 6;
   for (int i = t; i < kWaves * kBuckets; i += kThreads) (&fs.wcnt[0][0])[i] = 0u;
@@ -578,10 +621,11 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   int64_t far_c = 0;
   for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
     if (!order_key(bits)) return;
-    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax));
+    const int bkt = bucket_of(log2_ratio(bits, inv_t, zmax), bs);
     if (bkt < kBuckets - 1) atomicAdd(&fs.wcnt[w][bkt], 1u);
     else far_c += 1;
   });
+  XV_SAMPLER_TIMESTAMP(5);
   far_c = block_sum_l(s, far_c);
   __syncthreads();
   if (t < kBuckets) {
@@ -602,7 +646,8 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   }
   if (bk >= kBuckets - 1 || upto > kMaxCand) return false;  // rank k-1 far out or too many: exact row-wide path
   const uint32_t kminp = use_m ? minp_key(s, row, V, vec_ok, ntiles, inv_t, zmax, min_p) : 0xffffffffu;
-  const int n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bk, 0);
+  const int n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bk, 0);
+  XV_SAMPLER_TIMESTAMP(6);
   if (n > kMaxCand) return false;
   const int64_t total_k = list_mass_prefix(s, fs, n, top_k, inv_t, zmax);
   int64_t jcut = (int64_t)top_k - 1;
@@ -625,10 +670,10 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
 // Fast path: kept set = key > key_cut, or key == key_cut and id <= id_cut;
 // M = its mass.  Returns false when a boundary bucket overflowed the list.
 XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
-                             float inv_t, float zmax, int top_k, float top_p, float min_p, bool use_k, bool use_p,
+                             float inv_t, float zmax, float bs, int top_k, float top_p, float min_p, bool use_k, bool use_p,
                              bool use_m, uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
   const int t = threadIdx.x, w = t >> 6;
-  if (use_k) return topk_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_p, use_m,
+  if (use_k) return topk_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, top_k, top_p, min_p, use_p, use_m,
                                   key_cut, id_cut, M, list_kept);
   // ---- pass 2: every candidate's mass, binned by distance below the max ----
   for (int i = t; i < kWaves * kBuckets; i += kThreads) {
@@ -644,7 +689,7 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     const float d = log2_ratio(bits, inv_t, zmax);
     const float e = sampler_exp2(d);
     const int64_t q = mass_of(e);
-    const int bkt = bucket_of(d);
+    const int bkt = bucket_of(d, bs);
     if (bkt < kBuckets - 1) {
       atomicAdd(&fs.wcnt[w][bkt], 1u);
       atomicAdd(&fs.wmass[w][bkt], (unsigned long long)q);
@@ -654,6 +699,7 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     }
     if (use_m && e >= min_p) kminp = min(kminp, key);
   });
+  XV_SAMPLER_TIMESTAMP(5);
   far_c = block_sum_l(s, far_c);
   far_m = block_sum_l(s, far_m);
   if (use_m) kminp = block_min_u(s, kminp);
@@ -688,7 +734,8 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   int64_t total_k = total;
   int nk = 0;
   if (bk < kBuckets) {
-    nk = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bk);
+    if (s.cnt[bk] > (uint32_t)kMaxCand) return false;  // known before gathering
+    nk = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bk);
     if (nk > kMaxCand) return false;
     total_k = mk_before + list_mass_prefix(s, fs, nk, top_k - ck_before, inv_t, zmax);
   }
@@ -703,12 +750,13 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     }
   }
   int bm = kBuckets;
-  if (use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), inv_t, zmax));
+  if (use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), inv_t, zmax), bs);
   const int bf = min(bk, min(bp, bm));
   if (bf >= kBuckets) return true;  // no cut-off limits the row: everything kept
   int n = nk;
   if (bf != bk) {
-    n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bf);
+    if (s.cnt[bf] > (uint32_t)kMaxCand) return false;
+    n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bf);
     if (n > kMaxCand) return false;
   }
   // ---- exact cut inside the boundary bucket ----
@@ -760,12 +808,19 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
     return;
   }
 
+  XV_SAMPLER_TIMESTAMP(0);
   // ---- pass 1: the largest key ----
-  uint32_t kmax = 0;
-  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) { kmax = max(kmax, order_key(bits)); });
+  uint32_t kmax = 0, kmin = 0xffffffffu;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
+    const uint32_t key = order_key(bits);
+    kmax = max(kmax, key);
+    if (key) kmin = min(kmin, key);
+  });
   kmax = block_max_u(s, kmax);
+  kmin = block_min_u(s, kmin);
   const float inv_t = 1.0f / temp;
   const float zmax = bf16_to_f32(key_to_bits(kmax)) * inv_t;
+  const float bs = kmax ? bucket_scale(log2_ratio(key_to_bits(kmin), inv_t, zmax)) : 16.0f;
 
   const int top_k = ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
   const float top_p = ((flags & XV_SAMPLE_USE_TOP_P) && top_ps) ? top_ps[b] : 1.0f;
@@ -773,18 +828,21 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
   const bool use_k = top_k > 0 && top_k < V;
   const bool use_p = top_p < 1.0f;
   const bool use_m = min_p > 0.0f;
+  XV_SAMPLER_TIMESTAMP(1);
 
   uint32_t key_cut;
   int64_t id_cut, M;
   int list_kept = 0;  // > 0: the kept set is the sorted list prefix fs.cand[0, list_kept)
-  if (!fast_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m,
+  if (!fast_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, top_k, top_p, min_p, use_k, use_p, use_m,
                      key_cut, id_cut, M, list_kept)) {
     list_kept = 0;
     Boundary bd;
-    general_boundary(s, row, V, vec_ok, ntiles, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m, bd, id_cut,
+    general_boundary(s, row, V, vec_ok, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m, bd, id_cut,
                      M);
     key_cut = bd.key;
+    XV_SAMPLER_TIMESTAMP(3);
   }
+  XV_SAMPLER_TIMESTAMP(2);
 
   // ---- last pass: inverse-CDF draw in ascending id order (exp for kept ids only) ----
   // Thread t owns the contiguous ids [t*C, t*C + C), C a multiple of 8, so one
@@ -820,6 +878,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
     }
     found = block_min_l(s, found);
     if (t == 0) out_ids[b] = found == kTieAll ? 0 : found;
+    XV_SAMPLER_TIMESTAMP(4);
     return;
   }
   const int C = ((V + kThreads - 1) / kThreads + 7) / 8 * 8;
@@ -849,6 +908,7 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
   }
   __syncthreads();
   if (t == 0) out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
+  XV_SAMPLER_TIMESTAMP(4);
 }
 
 // ---------------------------------------------------------------------------
