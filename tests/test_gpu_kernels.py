@@ -288,7 +288,8 @@ def _sampler_case(g, b, v, std=2.0, ties=False):
         ("ties_fallback_minp", 4, 151936, 8, 1.0, 1.0, 0, 0.5, "massive"),
     ],
 )
-def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, ties):
+@pytest.mark.parametrize("multi_wg", [True, False], ids=["multi_wg", "one_wg"])
+def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, ties, multi_wg):
     import oracle.sampler as S
     from xvllm.sampler import sample
 
@@ -305,9 +306,33 @@ def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, tie
                     mps.numpy(), u.numpy(), flags)
     got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev),
                  all_greedy=bool(flags & 1), use_top_k=bool(flags & 2), use_top_p=bool(flags & 4),
-                 use_min_p=bool(flags & 8))
+                 use_min_p=bool(flags & 8), multi_workgroup=multi_wg)
     torch.cuda.synchronize()
     assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
+
+
+def test_sampler_nan_rows_paths_agree(dev):
+    """Rows with NaN logits (some, all) and a row of equal logits: the
+    multi-workgroup path gives the ids of the one-workgroup path."""
+    from xvllm.sampler import sample
+
+    g = gen(5)
+    b, v = 6, 151936
+    logits = _sampler_case(g, b, v, std=1.0)
+    logits[0, ::7] = float("nan")
+    logits[1] = float("nan")
+    logits[2] = 0.25
+    logits[3, :100] = float("nan")
+    logits[3, 5000] = float("inf")
+    temps = torch.tensor([1.0, 0.8, 1.0, 0.7, 0.0, 1.3])
+    tps = torch.full((b,), 0.9)
+    tks = torch.full((b,), 40, dtype=torch.int32)
+    u = torch.rand(b, generator=g)
+    for kw in (dict(use_top_p=True), dict(use_top_k=True, use_top_p=True), {}):
+        args = (logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), None, u.to(dev))
+        got = sample(*args, **kw)
+        want = sample(*args, **kw, multi_workgroup=False)
+        assert torch.equal(got, want), (kw, got, want)
 
 
 def test_sampler_many_draws_bitexact(dev):

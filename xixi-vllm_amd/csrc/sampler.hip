@@ -75,8 +75,8 @@ XV_INLINE int64_t mass_of(float e) { return (int64_t)(e * 1099511627776.0f); }
 // holding everything further.  bs is per row (bucket_scale); any bs > 0 keeps
 // the buckets monotone in the key, which is all the boundary search needs.
 XV_INLINE int bucket_of(float d, float bs) {
-  const float u = -d * bs;
-  return u < 255.0f ? (int)u : 255;
+  const float u = -d * bs;  // >= 0 for every candidate (d <= 0); NaN -> last bucket
+  return u < 255.0f ? (u > 0.0f ? (int)u : 0) : 255;
 }
 // 16 buckets per binary order, finer when the row spans less than 255/16
 // orders below its max (near-flat rows), so that the smallest candidate lands
@@ -775,16 +775,49 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   return true;
 }
 
-__global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restrict__ logits, int64_t stride, int V,
-                                                          const float* __restrict__ temps,
-                                                          const float* __restrict__ top_ps,
-                                                          const int32_t* __restrict__ top_ks,
-                                                          const float* __restrict__ min_ps,
-                                                          const float* __restrict__ uniforms, int flags,
-                                                          int64_t* __restrict__ out_ids) {
-  __shared__ Shared s;
-  __shared__ FastShared fs;
-  const int b = blockIdx.x;
+// Inverse-CDF draw over a kept set held as the sorted list fs.cand[0, n):
+// re-key it as (~id << 32 | key), so that the descending sort puts ids in
+// ascending order, then scan its masses.  Returns the first id whose inclusive
+// mass exceeds rdraw (kTieAll: none).
+XV_INLINE int64_t list_draw(Shared& s, FastShared& fs, int n, float inv_t, float zmax, int64_t rdraw) {
+  const int t = threadIdx.x;
+  __syncthreads();
+  for (int i = t; i < n; i += kThreads) {
+    const unsigned long long c = fs.cand[i];
+    fs.cand[i] = ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c);
+  }
+  __syncthreads();
+  sort_cand_desc(fs, n);
+  auto entry_mass = [&](unsigned long long c) {
+    return mass_of(exp_of(key_to_bits((uint32_t)(c & 0xffffffffu)), inv_t, zmax));
+  };
+  const int per = (n + kThreads - 1) / kThreads;
+  const int j0 = t * per, j1 = min(n, j0 + per);
+  int64_t local = 0;
+  for (int j = j0; j < j1; ++j) local += entry_mass(fs.cand[j]);
+  int64_t tot;
+  int64_t cum = block_excl_scan(s, local, &tot);
+  int64_t found = kTieAll;
+  for (int j = j0; j < j1; ++j) {
+    cum += entry_mass(fs.cand[j]);
+    if (cum > rdraw) { found = 0xffffffffu - (uint32_t)(fs.cand[j] >> 32); break; }
+  }
+  return block_min_l(s, found);
+}
+
+// The draw point floor(u * M), clamped to [0, M).
+XV_INLINE int64_t draw_point(float u, int64_t M) {
+  int64_t r = (int64_t)((double)u * (double)M);
+  if (r >= M) r = M - 1;
+  if (r < 0) r = 0;
+  return r;
+}
+
+// The whole sampler for row b by one kThreads workgroup.
+XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __restrict__ logits, int64_t stride, int V,
+                          const float* __restrict__ temps, const float* __restrict__ top_ps,
+                          const int32_t* __restrict__ top_ks, const float* __restrict__ min_ps,
+                          const float* __restrict__ uniforms, int flags, int64_t* __restrict__ out_ids) {
   const int t = threadIdx.x;
   const bf16_t* row = logits + (int64_t)b * stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
@@ -848,35 +881,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
   // Thread t owns the contiguous ids [t*C, t*C + C), C a multiple of 8, so one
   // block scan orders the whole row.
   const float u = uniforms ? uniforms[b] : 0.5f;
-  int64_t rdraw = (int64_t)((double)u * (double)M);
-  if (rdraw >= M) rdraw = M - 1;
-  if (rdraw < 0) rdraw = 0;
+  const int64_t rdraw = draw_point(u, M);
   if (list_kept > 0) {
-    // The kept set is in LDS: re-key it as (~id << 32 | key), so the
-    // descending sort puts ids in ascending order, then scan its masses.
-    const int n = list_kept;
-    __syncthreads();
-    for (int i = t; i < n; i += kThreads) {
-      const unsigned long long c = fs.cand[i];
-      fs.cand[i] = ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c);
-    }
-    __syncthreads();
-    sort_cand_desc(fs, n);
-    auto entry_mass = [&](unsigned long long c) {
-      return mass_of(exp_of(key_to_bits((uint32_t)(c & 0xffffffffu)), inv_t, zmax));
-    };
-    const int per = (n + kThreads - 1) / kThreads;
-    const int j0 = t * per, j1 = min(n, j0 + per);
-    int64_t local = 0;
-    for (int j = j0; j < j1; ++j) local += entry_mass(fs.cand[j]);
-    int64_t tot;
-    int64_t cum = block_excl_scan(s, local, &tot);
-    int64_t found = kTieAll;
-    for (int j = j0; j < j1; ++j) {
-      cum += entry_mass(fs.cand[j]);
-      if (cum > rdraw) { found = 0xffffffffu - (uint32_t)(fs.cand[j] >> 32); break; }
-    }
-    found = block_min_l(s, found);
+    const int64_t found = list_draw(s, fs, list_kept, inv_t, zmax, rdraw);
     if (t == 0) out_ids[b] = found == kTieAll ? 0 : found;
     XV_SAMPLER_TIMESTAMP(4);
     return;
@@ -909,6 +916,18 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
   __syncthreads();
   if (t == 0) out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
   XV_SAMPLER_TIMESTAMP(4);
+}
+
+__global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restrict__ logits, int64_t stride, int V,
+                                                          const float* __restrict__ temps,
+                                                          const float* __restrict__ top_ps,
+                                                          const int32_t* __restrict__ top_ks,
+                                                          const float* __restrict__ min_ps,
+                                                          const float* __restrict__ uniforms, int flags,
+                                                          int64_t* __restrict__ out_ids) {
+  __shared__ Shared s;
+  __shared__ FastShared fs;
+  sample_row(s, fs, blockIdx.x, logits, stride, V, temps, top_ps, top_ks, min_ps, uniforms, flags, out_ids);
 }
 
 // ---------------------------------------------------------------------------
@@ -993,14 +1012,762 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Sampled rows over several workgroups per row (batches given a workspace).
+//
+// A row is cut into R segments of whole 8-id vectors, one kSegThreads
+// workgroup each, and the one-workgroup algorithm above runs as a chain of
+// launches (a launch boundary makes one kernel's global writes visible to the
+// next, across XCDs):
+//   1. seg_stats:  per segment, the largest and smallest key and the greedy best;
+//   2. seg_hist:   per segment, bucket counts and masses, and the min-p key;
+//   3. row_plan:   per row, the summed histograms give the bucket(s) holding the
+//                  cut-offs (greedy and all-NaN rows finish here);
+//   4. seg_gather: the candidates of those buckets, appended to the row's list;
+//   5. row_cut:    per row, the sorted list gives the exact cut and the kept
+//                  mass (top-k rows draw from the list and finish); a row whose
+//                  buckets hold more candidates than LDS runs sample_row;
+//   6. seg_kept:   per segment, the kept mass;
+//   7. row_draw:   per row, the segment holding floor(u * M), then the id in it.
+// Buckets, masses, cuts and the draw are those of the one-workgroup path, so
+// the ids are identical to it.
+
+constexpr int kSegThreads = 256;
+constexpr int kSegWaves = kSegThreads / 64;
+#ifndef XV_SEG_MAX
+#define XV_SEG_MAX 32
+#endif
+#ifndef XV_SEG_CHUNK
+#define XV_SEG_CHUNK 4
+#endif
+#ifndef XV_SEG_TARGET
+#define XV_SEG_TARGET 2048
+#endif
+constexpr int kMaxSegs = XV_SEG_MAX;
+constexpr int kSegChunk = XV_SEG_CHUNK;
+constexpr int kSegMaxBatch = 128;
+
+enum : int { kPlanDone = 0, kPlanGather = 1, kPlanDraw = 2, kPlanFallback = 3 };
+
+struct __attribute__((aligned(128))) RowPlan {
+  int status;
+  int lo, hi;          // bucket range gathered
+  int use_k;           // the list is the top-k candidates (draw from the list)
+  int cut_p, cut_m;    // the top-p / min-p cut falls in the gathered bucket
+  uint32_t kminp;      // min-p key (0xffffffff: none)
+  uint32_t cand_count; // appended by seg_gather
+  uint32_t key_cut;
+  uint32_t klo, khi;   // keys of buckets lo..hi: exactly [klo, khi]
+  float zmax, inv_t, bs;
+  int64_t thr, mp_before, m_before, id_cut, M;
+};
+
+struct SegArgs {
+  const bf16_t* logits;
+  int64_t stride;
+  int V, R, seg_len, flags;
+  const float* temps;
+  const float* top_ps;
+  const int32_t* top_ks;
+  const float* min_ps;
+  const float* uniforms;
+  int64_t* out_ids;
+  RowPlan* plans;               // [B]
+  uint32_t* seg_kmax;           // [B * R]
+  uint32_t* seg_kmin;           // [B * R]
+  uint32_t* seg_minp;           // [B * R]
+  unsigned long long* seg_best; // [B * R] greedy (key << 32 | ~id)
+  int64_t* seg_kept;            // [B * R]
+  uint32_t* seg_cnt;            // [B * R * kBuckets]
+  unsigned long long* seg_mass; // [B * R * kBuckets]
+  unsigned long long* cand;     // [B * kMaxCand]
+};
+
+struct RowParams {
+  bool greedy, use_k, use_p, use_m;
+  int top_k;
+  float temp, top_p, min_p;
+};
+XV_INLINE RowParams row_params(const SegArgs& a, int b) {
+  RowParams p;
+  p.temp = a.temps[b];
+  p.greedy = p.temp <= 1e-5f;
+  p.top_k = ((a.flags & XV_SAMPLE_USE_TOP_K) && a.top_ks) ? a.top_ks[b] : a.V;
+  p.top_p = ((a.flags & XV_SAMPLE_USE_TOP_P) && a.top_ps) ? a.top_ps[b] : 1.0f;
+  p.min_p = ((a.flags & XV_SAMPLE_USE_MIN_P) && a.min_ps) ? a.min_ps[b] : 0.0f;
+  p.use_k = p.top_k > 0 && p.top_k < a.V;
+  p.use_p = p.top_p < 1.0f;
+  p.use_m = p.min_p > 0.0f;
+  return p;
+}
+
+// f(bits, id) for every id of segment [beg, end) on every lane: vector vi of
+// the segment is (c * kSegChunk + v) * kSegThreads + t; ids ascend within a
+// lane; slots outside the segment come as 0xffff (key 0).
+template <typename F>
+XV_INLINE void for_seg(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) {
+  const int nvec = (end - beg + 7) / 8;
+  for (int c = 0; c * kSegChunk * kSegThreads < nvec; ++c) {
+    uint32_t w[kSegChunk][4];
+#pragma unroll
+    for (int v = 0; v < kSegChunk; ++v) {
+      const int base = beg + ((c * kSegChunk + v) * kSegThreads + (int)threadIdx.x) * 8;
+      if (vec_ok && base + 8 <= end) {
+        const Vec8 x = load_vec8(row + base);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[v][k] = x.w[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          w[v][k] = (base + 2 * k < end ? (uint32_t)row[base + 2 * k] : 0xffffu) |
+                    (base + 2 * k + 1 < end ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < kSegChunk; ++v) {
+      const int base = beg + ((c * kSegChunk + v) * kSegThreads + (int)threadIdx.x) * 8;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) f((w[v][k >> 1] >> (16 * (k & 1))) & 0xffffu, base + k);
+    }
+  }
+}
+
+struct SegRed {
+  unsigned long long u[kSegWaves];
+  int64_t l[kSegWaves];
+};
+XV_INLINE uint32_t seg_max_u(SegRed& r, uint32_t x) {
+  x = wave_max_u(x);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) r.u[threadIdx.x >> 6] = x;
+  __syncthreads();
+  uint32_t m = (uint32_t)r.u[0];
+  for (int i = 1; i < kSegWaves; ++i) m = max(m, (uint32_t)r.u[i]);
+  return m;
+}
+XV_INLINE uint32_t seg_min_u(SegRed& r, uint32_t x) {
+  x = wave_min_u(x);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) r.u[threadIdx.x >> 6] = x;
+  __syncthreads();
+  uint32_t m = (uint32_t)r.u[0];
+  for (int i = 1; i < kSegWaves; ++i) m = min(m, (uint32_t)r.u[i]);
+  return m;
+}
+XV_INLINE unsigned long long seg_max_ull(SegRed& r, unsigned long long x) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long y = __shfl_xor(x, o);
+    x = y > x ? y : x;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) r.u[threadIdx.x >> 6] = x;
+  __syncthreads();
+  unsigned long long m = r.u[0];
+  for (int i = 1; i < kSegWaves; ++i) m = r.u[i] > m ? r.u[i] : m;
+  return m;
+}
+XV_INLINE int64_t seg_sum_l(SegRed& r, int64_t x) {
+  x = wave_sum_l(x);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) r.l[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int64_t m = 0;
+  for (int i = 0; i < kSegWaves; ++i) m += r.l[i];
+  return m;
+}
+XV_INLINE int64_t seg_min_l(SegRed& r, int64_t x) {
+  for (int o = 32; o > 0; o >>= 1) {
+    const int64_t y = __shfl_xor(x, o);
+    x = y < x ? y : x;
+  }
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) r.l[threadIdx.x >> 6] = x;
+  __syncthreads();
+  int64_t m = r.l[0];
+  for (int i = 1; i < kSegWaves; ++i) m = r.l[i] < m ? r.l[i] : m;
+  return m;
+}
+// Inclusive prefix sum over the workgroup (thread order).
+XV_INLINE int64_t seg_incl_scan(SegRed& r, int64_t x) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  __syncthreads();
+  if (lane == 63) r.l[w] = x;
+  __syncthreads();
+  for (int i = 0; i < w; ++i) x += r.l[i];
+  return x;
+}
+
+// Row max / min keys from the segment stats, and the row constants.
+struct RowConsts {
+  uint32_t kmax, kmin;
+  float inv_t, zmax, bs;
+};
+XV_INLINE RowConsts row_consts(const SegArgs& a, int b, float temp) {
+  // every wave reduces the R <= 64 segment values itself: one load per lane
+  RowConsts c;
+  const int lane = threadIdx.x & 63;
+  c.kmax = wave_max_u(lane < a.R ? a.seg_kmax[b * a.R + lane] : 0u);
+  c.kmin = wave_min_u(lane < a.R ? a.seg_kmin[b * a.R + lane] : 0xffffffffu);
+  c.inv_t = 1.0f / temp;
+  c.zmax = bf16_to_f32(key_to_bits(c.kmax)) * c.inv_t;
+  c.bs = c.kmax ? bucket_scale(log2_ratio(key_to_bits(c.kmin), c.inv_t, c.zmax)) : 16.0f;
+  return c;
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_stats_kernel(SegArgs a) {
+  __shared__ SegRed red;
+  const int b = blockIdx.y, r = blockIdx.x;
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  if (a.temps[b] <= 1e-5f) {  // greedy row: the segment's best (value, then lowest id)
+    float fm = -INFINITY;
+    int bid = -1;
+    for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int id) {
+      const float v = bf16_to_f32(bits);  // NaN (and padding) never compares greater
+      const bool better = v > fm;         // ids ascend within a lane: keeps the lowest
+      fm = better ? v : fm;
+      bid = better ? id : bid;
+    });
+    unsigned long long best = 0;
+    if (bid >= 0) {
+      const uint32_t fb = __float_as_uint(fm) >> 16;
+      best = ((unsigned long long)order_key(fb == 0x8000u ? 0u : fb) << 32) | (0xffffffffu - (uint32_t)bid);
+    }
+    best = seg_max_ull(red, best);
+    if (threadIdx.x == 0) a.seg_best[b * a.R + r] = best;
+    return;
+  }
+  uint32_t kmax = 0, kmin = 0xffffffffu;
+  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) {
+    const uint32_t key = order_key(bits);
+    kmax = max(kmax, key);
+    kmin = min(kmin, key ? key : 0xffffffffu);
+  });
+  kmax = seg_max_u(red, kmax);
+  kmin = seg_min_u(red, kmin);
+  if (threadIdx.x == 0) {
+    a.seg_kmax[b * a.R + r] = kmax;
+    a.seg_kmin[b * a.R + r] = kmin;
+  }
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(SegArgs a) {
+  __shared__ SegRed red;
+  __shared__ uint32_t wcnt[kSegWaves][kBuckets];
+  __shared__ unsigned long long wmass[kSegWaves][kBuckets];
+  const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x, w = t >> 6;
+  const RowParams p = row_params(a, b);
+  if (p.greedy) return;
+  const RowConsts rc = row_consts(a, b, p.temp);
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  for (int i = t; i < kSegWaves * kBuckets; i += kSegThreads) {
+    (&wcnt[0][0])[i] = 0u;
+    (&wmass[0][0])[i] = 0ull;
+  }
+  __syncthreads();
+  int64_t far_c = 0, far_m = 0;
+  uint32_t kminp = 0xffffffffu;
+  if (p.use_k) {
+    // counts only: the sorted top-k list gives every mass the cut needs; the
+    // min-p key needs an exp only within half a binary order of its threshold
+    const float d_lo = __log2f(p.min_p) - 0.5f;
+    for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) {
+      const uint32_t key = order_key(bits);
+      if (!key) return;
+      const float d = log2_ratio(bits, rc.inv_t, rc.zmax);
+      const int bkt = bucket_of(d, rc.bs);
+      if (bkt < kBuckets - 1) atomicAdd(&wcnt[w][bkt], 1u);
+      else far_c += 1;
+      if (p.use_m && d >= d_lo && sampler_exp2(d) >= p.min_p) kminp = min(kminp, key);
+    });
+  } else {
+    for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) {
+      const uint32_t key = order_key(bits);
+      if (!key) return;
+      const float d = log2_ratio(bits, rc.inv_t, rc.zmax);
+      const float e = sampler_exp2(d);
+      const int64_t q = mass_of(e);
+      const int bkt = bucket_of(d, rc.bs);
+      if (bkt < kBuckets - 1) {
+        atomicAdd(&wcnt[w][bkt], 1u);
+        atomicAdd(&wmass[w][bkt], (unsigned long long)q);
+      } else {
+        far_c += 1;
+        far_m += q;
+      }
+      if (p.use_m && e >= p.min_p) kminp = min(kminp, key);
+    });
+  }
+  far_c = seg_sum_l(red, far_c);
+  far_m = seg_sum_l(red, far_m);
+  kminp = seg_min_u(red, kminp);
+  __syncthreads();
+  const int64_t o = ((int64_t)b * a.R + r) * kBuckets;
+  for (int i = t; i < kBuckets; i += kSegThreads) {
+    uint32_t c = 0;
+    unsigned long long m = 0;
+    for (int ww = 0; ww < kSegWaves; ++ww) { c += wcnt[ww][i]; m += wmass[ww][i]; }
+    if (i == kBuckets - 1) { c += (uint32_t)far_c; m += (unsigned long long)far_m; }
+    a.seg_cnt[o + i] = c;
+    if (!p.use_k) a.seg_mass[o + i] = m;  // top-k rows take their masses from the list
+  }
+  if (t == 0) a.seg_minp[b * a.R + r] = kminp;
+}
+
+// One thread per bucket (kSegThreads == kBuckets).
+__global__ __launch_bounds__(kSegThreads) void row_plan_kernel(SegArgs a) {
+  static_assert(kSegThreads == kBuckets, "one thread per bucket");
+  __shared__ SegRed red;
+  const int b = blockIdx.x, t = threadIdx.x;
+  RowPlan& plan = a.plans[b];
+  const RowParams p = row_params(a, b);
+  if (p.greedy) {
+    unsigned long long best = t < a.R ? a.seg_best[b * a.R + t] : 0ull;
+    best = seg_max_ull(red, best);
+    if (t == 0) {
+      a.out_ids[b] = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
+      plan.status = kPlanDone;
+    }
+    return;
+  }
+  const RowConsts rc = row_consts(a, b, p.temp);
+  if (rc.kmax == 0) {  // every logit NaN: nothing has mass
+    if (t == 0) {
+      a.out_ids[b] = 0;
+      plan.status = kPlanDone;
+    }
+    return;
+  }
+  int64_t cnt = 0, mass = 0;
+  for (int i0 = 0; i0 < a.R; i0 += 8) {  // eight segments' loads in flight
+    uint32_t c8[8];
+    unsigned long long m8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t o = ((int64_t)b * a.R + min(i0 + j, a.R - 1)) * kBuckets + t;
+      c8[j] = a.seg_cnt[o];
+      m8[j] = p.use_k ? 0ull : a.seg_mass[o];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (i0 + j < a.R) {
+        cnt += c8[j];
+        mass += (int64_t)m8[j];
+      }
+  }
+  const uint32_t kminp = wave_min_u((t & 63) < a.R ? a.seg_minp[b * a.R + (t & 63)] : 0xffffffffu);
+  const int64_t cnt_incl = seg_incl_scan(red, cnt);
+  const int64_t mass_incl = seg_incl_scan(red, mass);
+  const int64_t total = seg_sum_l(red, mass);
+  int status = kPlanDraw, lo = 0, hi = 0, cut_p = 0, cut_m = 0;
+  int64_t thr = 0, mp_before = 0, m_before = 0;
+  if (p.use_k) {
+    // rank k-1 lies in the first bucket whose inclusive count reaches k
+    const int bk = (int)seg_min_l(red, cnt_incl >= p.top_k ? t : kBuckets);
+    __syncthreads();
+    if (t == bk) red.l[0] = cnt_incl;  // candidates in buckets 0..bk
+    __syncthreads();
+    const int64_t upto = bk < kBuckets ? red.l[0] : 0;
+    status = (bk >= kBuckets - 1 || upto > kMaxCand) ? kPlanFallback : kPlanGather;
+    lo = 0;
+    hi = bk;
+  } else if (p.use_p || p.use_m) {
+    int bp = kBuckets;
+    if (p.use_p) {
+      thr = (int64_t)floor((double)p.top_p * (double)total);
+      bp = (int)seg_min_l(red, mass_incl > thr ? t : kBuckets);
+    }
+    int bm = kBuckets;
+    if (p.use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), rc.inv_t, rc.zmax), rc.bs);
+    const int bf = min(bp, bm);
+    if (bf < kBuckets) {
+      __syncthreads();
+      if (t == bf) {
+        red.l[0] = cnt;
+        red.l[1] = mass_incl - mass;  // mass of the buckets before bf
+      }
+      __syncthreads();
+      const int64_t nbf = red.l[0];
+      m_before = red.l[1];
+      mp_before = m_before;
+      status = nbf > kMaxCand ? kPlanFallback : kPlanGather;
+      lo = hi = bf;
+      cut_p = bp == bf;
+      cut_m = bm == bf;
+    }
+  }
+  if (t == 0) {
+    if (status == kPlanGather) {
+      // Buckets fall as keys rise over the keys of non-NaN values, [1, 0xff80]
+      // (+inf), so buckets lo..hi hold exactly the keys of an interval; find
+      // its ends with the same bucket function.
+      constexpr uint32_t kInfKey = 0xff80u;
+      auto bkt = [&](uint32_t k) { return bucket_of(log2_ratio(key_to_bits(k), rc.inv_t, rc.zmax), rc.bs); };
+      uint32_t l = 1, h = kInfKey;  // smallest key with bucket <= hi
+      if (bkt(kInfKey) > hi) {
+        l = kInfKey + 1;  // empty (cannot happen: the plan's buckets are non-empty)
+      } else {
+        while (l < h) {
+          const uint32_t m = (l + h) >> 1;
+          if (bkt(m) <= hi) h = m; else l = m + 1;
+        }
+      }
+      plan.klo = l;
+      l = 1; h = kInfKey;             // largest key with bucket >= lo
+      if (bkt(1) < lo) {
+        plan.khi = 0u;  // empty (cannot happen: the plan's buckets are non-empty)
+      } else {
+        while (l < h) {
+          const uint32_t m = (l + h + 1) >> 1;
+          if (bkt(m) >= lo) l = m; else h = m - 1;
+        }
+        plan.khi = l;
+      }
+    }
+    plan.status = status;
+    plan.lo = lo;
+    plan.hi = hi;
+    plan.use_k = p.use_k;
+    plan.cut_p = cut_p;
+    plan.cut_m = cut_m;
+    plan.kminp = kminp;
+    plan.cand_count = 0;
+    plan.zmax = rc.zmax;
+    plan.inv_t = rc.inv_t;
+    plan.bs = rc.bs;
+    plan.thr = thr;
+    plan.mp_before = mp_before;
+    plan.m_before = m_before;
+    plan.key_cut = 1u;  // no cut: every candidate kept
+    plan.id_cut = kTieAll;
+    plan.M = total;
+  }
+}
+
+// Two passes over the segment (the second from L2): count the candidates of
+// the plan's key interval, reserve their slots in the row's list with one atomic per
+// workgroup, then write them.  No LDS staging, so occupancy stays high.
+__global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
+  __shared__ SegRed red;
+  __shared__ uint32_t base_lds;
+  const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x;
+  const RowPlan& plan = a.plans[b];
+  if (plan.status != kPlanGather) return;
+  const uint32_t klo = plan.klo, khi = plan.khi;
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  auto in_plan = [&](uint32_t bits) {
+    const uint32_t key = order_key(bits);  // 0 (NaN) is below klo >= 1
+    return key >= klo && key <= khi;
+  };
+  int64_t mine = 0;
+  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) { mine += in_plan(bits); });
+  const int64_t incl = seg_incl_scan(red, mine);
+  __syncthreads();
+  if (t == kSegThreads - 1) {
+    base_lds = incl ? __hip_atomic_fetch_add(&a.plans[b].cand_count, (uint32_t)incl, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT)
+                    : 0u;
+  }
+  __syncthreads();
+  if (mine == 0) return;
+  int64_t slot = (int64_t)base_lds + incl - mine;
+  unsigned long long* dst = a.cand + (int64_t)b * kMaxCand;
+  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int id) {
+    if (!in_plan(bits)) return;
+    if (slot < kMaxCand)
+      dst[slot] = ((unsigned long long)order_key(bits) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
+    ++slot;
+  });
+}
+
+// List operations on at most 64 candidates held one per lane, by one wave
+// (no workgroup barriers).  Bitonic sort of the wave, descending; zeros
+// (padding) sort last.
+XV_INLINE unsigned long long wave_sort_desc(unsigned long long c) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const unsigned long long o = __shfl_xor(c, stride);
+      const bool take_max = ((lane & size) == 0) == ((lane & stride) == 0);
+      c = take_max ? (o > c ? o : c) : (o < c ? o : c);
+    }
+  return c;
+}
+XV_INLINE int64_t wave_incl_scan_l(int64_t x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int64_t y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+// First lane whose predicate holds, `none` if no lane's does.
+XV_INLINE int64_t wave_first(bool pred, int64_t none) {
+  const unsigned long long m = __ballot(pred);
+  return m ? (int64_t)__builtin_ctzll(m) : none;
+}
+
+// row_cut for a list of n <= 64 candidates, wave 0 alone: the same cut, kept
+// mass and draw as the workgroup list functions.
+XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n) {
+  const int lane = threadIdx.x & 63;
+  const float inv_t = plan.inv_t, zmax = plan.zmax;
+  unsigned long long c = lane < n ? a.cand[(int64_t)b * kMaxCand + lane] : 0ull;
+  c = wave_sort_desc(c);
+  const int64_t q = lane < n ? cand_mass(c, inv_t, zmax) : 0;
+  const int64_t incl = wave_incl_scan_l(q);
+  const uint32_t key = cand_key(c);
+  const uint32_t kminp = plan.kminp;
+  int64_t jcut;
+  if (plan.use_k) {
+    const int64_t total_k = wave_sum_l(lane < p.top_k ? q : 0);
+    jcut = (int64_t)p.top_k - 1;
+    if (p.use_p) {
+      const int64_t thr = (int64_t)floor((double)p.top_p * (double)total_k);
+      jcut = min(jcut, wave_first(lane < n && incl > thr, n));
+    }
+    const uint32_t last = cand_key(__shfl(c, n - 1));
+    if (p.use_m && kminp != 0xffffffffu && kminp >= last)
+      jcut = min(jcut, (int64_t)__popcll(__ballot(lane < n && key >= kminp)) - 1);
+  } else {
+    jcut = kTieAll;
+    if (plan.cut_p) jcut = min(jcut, wave_first(lane < n && plan.mp_before + incl > plan.thr, n));
+    if (plan.cut_m) jcut = min(jcut, (int64_t)__popcll(__ballot(lane < n && key >= kminp)) - 1);
+  }
+  if (jcut >= n) jcut = n - 1;
+  if (jcut < 0) jcut = 0;
+  const unsigned long long edge = __shfl(c, (int)jcut);
+  const int64_t m_list = wave_sum_l(lane <= jcut ? q : 0);
+  if (plan.use_k) {
+    // the kept list in ascending id order: re-keyed (~id << 32 | key), sorted descending
+    const float u = a.uniforms ? a.uniforms[b] : 0.5f;
+    const int64_t rdraw = draw_point(u, m_list);
+    unsigned long long e =
+        lane <= jcut ? ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c) : 0ull;
+    e = wave_sort_desc(e);
+    const int64_t qe = lane <= jcut ? mass_of(exp_of(key_to_bits((uint32_t)(e & 0xffffffffu)), inv_t, zmax)) : 0;
+    const int64_t ie = wave_incl_scan_l(qe);
+    const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
+    const unsigned long long ef = __shfl(e, fi < 0 ? 0 : (int)fi);
+    if (lane == 0) {
+      a.out_ids[b] = fi < 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(ef >> 32));
+      plan.status = kPlanDone;
+    }
+    return;
+  }
+  if (lane == 0) {
+    plan.key_cut = cand_key(edge);
+    plan.id_cut = cand_id(edge);
+    plan.M = plan.m_before + m_list;
+    plan.status = kPlanDraw;
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
+  __shared__ Shared s;
+  __shared__ FastShared fs;
+  const int b = blockIdx.x, t = threadIdx.x;
+  RowPlan& plan = a.plans[b];
+  int status = plan.status;
+  // a gathered list is never empty (the cut's bucket holds its own boundary
+  // candidate); should it be, the one-workgroup path takes the row
+  if (status == kPlanGather && plan.cand_count == 0u) status = kPlanFallback;
+  if (status == kPlanFallback) {
+    sample_row(s, fs, b, a.logits, a.stride, a.V, a.temps, a.top_ps, a.top_ks, a.min_ps, a.uniforms,
+               a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
+    __syncthreads();
+    if (t == 0) plan.status = kPlanDone;
+    return;
+  }
+  if (status != kPlanGather) return;
+  const RowParams p = row_params(a, b);
+  const float inv_t = plan.inv_t, zmax = plan.zmax;
+  const int n = (int)min(plan.cand_count, (uint32_t)kMaxCand);
+  if (n <= 64) {
+    if (t < 64) row_cut_wave(a, plan, p, b, n);
+    return;
+  }
+  const unsigned long long* src = a.cand + (int64_t)b * kMaxCand;
+  for (int i = t; i < n; i += kThreads) fs.cand[i] = src[i];
+  __syncthreads();
+  sort_cand_desc(fs, n);
+  int64_t jcut;
+  if (plan.use_k) {
+    // the list is every candidate down to rank k-1 (as topk_boundary)
+    const int64_t total_k = list_mass_prefix(s, fs, n, p.top_k, inv_t, zmax);
+    jcut = (int64_t)p.top_k - 1;
+    if (p.use_p) {
+      const int64_t thr = (int64_t)floor((double)p.top_p * (double)total_k);
+      jcut = min(jcut, list_first_exceed(s, fs, n, 0, thr, inv_t, zmax));
+    }
+    const uint32_t kminp = plan.kminp;
+    if (p.use_m && kminp != 0xffffffffu && kminp >= cand_key(fs.cand[n - 1]))
+      jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
+  } else {
+    // the list is the bucket of the earliest cut (as fast_boundary)
+    jcut = kTieAll;
+    if (plan.cut_p) jcut = min(jcut, list_first_exceed(s, fs, n, plan.mp_before, plan.thr, inv_t, zmax));
+    if (plan.cut_m) jcut = min(jcut, list_count_ge(s, fs, n, plan.kminp) - 1);
+  }
+  if (jcut >= n) jcut = n - 1;
+  if (jcut < 0) jcut = 0;
+  const unsigned long long edge = fs.cand[jcut];
+  if (plan.use_k) {
+    const int64_t M = list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+    const float u = a.uniforms ? a.uniforms[b] : 0.5f;
+    const int64_t found = list_draw(s, fs, (int)jcut + 1, inv_t, zmax, draw_point(u, M));
+    if (t == 0) {
+      a.out_ids[b] = found == kTieAll ? 0 : found;
+      plan.status = kPlanDone;
+    }
+    return;
+  }
+  const int64_t M = plan.m_before + list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+  if (t == 0) {
+    plan.key_cut = cand_key(edge);
+    plan.id_cut = cand_id(edge);
+    plan.M = M;
+    plan.status = kPlanDraw;
+  }
+}
+
+XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t id_cut, float inv_t, float zmax) {
+  const uint32_t key = order_key(bits);
+  const bool kept = key && (key > key_cut || (key == key_cut && (int64_t)id <= id_cut));
+  return kept ? mass_of(exp_of(bits, inv_t, zmax)) : 0;
+}
+
+__global__ __launch_bounds__(kSegThreads) void seg_kept_kernel(SegArgs a) {
+  __shared__ SegRed red;
+  const int b = blockIdx.y, r = blockIdx.x;
+  const RowPlan& plan = a.plans[b];
+  if (plan.status != kPlanDraw) return;
+  const uint32_t key_cut = plan.key_cut;
+  const int64_t id_cut = plan.id_cut;
+  const float inv_t = plan.inv_t, zmax = plan.zmax;
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  int64_t m = 0;
+  for_seg(row, vec_ok, beg, end,
+          [&](uint32_t bits, int id) { m += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax); });
+  m = seg_sum_l(red, m);
+  if (threadIdx.x == 0) a.seg_kept[b * a.R + r] = m;
+}
+
+__global__ __launch_bounds__(kSegThreads) void row_draw_kernel(SegArgs a) {
+  __shared__ SegRed red;
+  __shared__ int64_t pick;
+  const int b = blockIdx.x, t = threadIdx.x;
+  const RowPlan& plan = a.plans[b];
+  if (plan.status != kPlanDraw) return;
+  const uint32_t key_cut = plan.key_cut;
+  const int64_t id_cut = plan.id_cut;
+  const float inv_t = plan.inv_t, zmax = plan.zmax;
+  const float u = a.uniforms ? a.uniforms[b] : 0.5f;
+  const int64_t rdraw = draw_point(u, plan.M);
+  // the segment holding rdraw: inclusive sums of the segment masses
+  const int64_t sm = t < a.R ? a.seg_kept[b * a.R + t] : 0;
+  const int64_t incl = seg_incl_scan(red, sm);
+  const int r = (int)seg_min_l(red, (t < a.R && rdraw < incl) ? t : kMaxSegs);
+  if (r >= a.R) {  // no kept mass (cannot happen for a row with a finite logit)
+    if (t == 0) a.out_ids[b] = 0;
+    return;
+  }
+  __syncthreads();
+  if (t == r) pick = incl - sm;  // mass of the segments before r
+  __syncthreads();
+  const int64_t rr = rdraw - pick;
+  // inside segment r, in id order: thread t owns [beg + t*C, beg + t*C + C)
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  const int C = ((end - beg + kSegThreads - 1) / kSegThreads + 7) / 8 * 8;
+  const int i0 = min(end, beg + t * C), i1 = min(end, i0 + C);
+  auto scan_range = [&](auto&& f) {
+    for (int i = i0; i < i1; i += 8 * kSegChunk) {
+      uint32_t bits[kSegChunk][8];
+#pragma unroll
+      for (int v = 0; v < kSegChunk; ++v)
+        if (i + 8 * v < i1) load8(row, i1, i + 8 * v, vec_ok, bits[v]);  // i0 and C are multiples of 8
+#pragma unroll
+      for (int v = 0; v < kSegChunk; ++v)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (i + 8 * v + k < i1) f(bits[v][k], i + 8 * v + k);
+    }
+  };
+  int64_t mine = 0;
+  scan_range([&](uint32_t bits, int id) { mine += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax); });
+  const int64_t cum_incl = seg_incl_scan(red, mine);
+  int64_t cum = cum_incl - mine;
+  __syncthreads();
+  if (t == 0) pick = -1;
+  __syncthreads();
+  if (cum <= rr && rr < cum_incl) {
+    int64_t found = -1;
+    scan_range([&](uint32_t bits, int id) {
+      if (found >= 0) return;
+      cum += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax);
+      if (cum > rr) found = id;
+    });
+    pick = found;
+  }
+  __syncthreads();
+  if (t == 0) a.out_ids[b] = pick >= 0 ? pick : 0;
+}
+
 }  // namespace
 
 // Workspace: one 128-byte line per row (a 64-bit slot and a 32-bit arrival
-// counter) for the multi-workgroup greedy path; the other paths keep their
-// scratch in LDS.
+// counter) for the multi-workgroup greedy path, then the per-row plans,
+// per-segment statistics and histograms and the per-row candidate lists of the
+// multi-workgroup sampled path.
+namespace {
+struct SegLayout {
+  int R, seg_len;
+  size_t plans, kmax, kmin, minp, best, kept, cnt, mass, cand, total;
+};
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+SegLayout seg_layout(int batch, int vocab) {
+  SegLayout L;
+  // about 2048 segment workgroups in all, at least 2048 ids per segment
+  int segs = max(1, min(kMaxSegs, XV_SEG_TARGET / max(batch, 1)));
+  segs = max(1, min(segs, vocab / 2048));
+  L.seg_len = ((vocab + segs - 1) / segs + 7) / 8 * 8;
+  L.R = (vocab + L.seg_len - 1) / L.seg_len;
+  const size_t B = (size_t)max(batch, 0), BR = B * L.R;
+  size_t o = align256(B * kGreedyLine * 8);
+  L.plans = o; o = align256(o + B * sizeof(RowPlan));
+  L.kmax = o;  o = align256(o + BR * 4);
+  L.kmin = o;  o = align256(o + BR * 4);
+  L.minp = o;  o = align256(o + BR * 4);
+  L.best = o;  o = align256(o + BR * 8);
+  L.kept = o;  o = align256(o + BR * 8);
+  L.cnt = o;   o = align256(o + BR * kBuckets * 4);
+  L.mass = o;  o = align256(o + BR * kBuckets * 8);
+  L.cand = o;  o = align256(o + B * kMaxCand * 8);
+  L.total = o;
+  return L;
+}
+}  // namespace
+
 extern "C" size_t xv_sampler_workspace_size(int batch, int vocab) {
-  (void)vocab;
-  return ((size_t)(batch > 0 ? batch : 0) * kGreedyLine * 8 + 255) / 256 * 256;
+  if (batch <= 0 || vocab <= 0) return 256;
+  return seg_layout(batch, vocab).total;
 }
 
 extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
@@ -1022,6 +1789,43 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     greedy_segment_kernel<<<dim3((unsigned)((vocab + seg_len - 1) / seg_len), (unsigned)batch),
                             kGreedyThreads, 0, stream>>>((const bf16_t*)logits, logits_stride, vocab, seg_len, slots,
                                                          arrivals, out_ids);
+    XV_CHECK_LAUNCH();
+    return 0;
+  }
+  // Sampled (or mixed) batches of up to kSegMaxBatch rows: several workgroups
+  // per row.  Larger batches fill the device with one workgroup per row, which
+  // reads each row fewer times.
+  if (workspace != nullptr && batch <= kSegMaxBatch && workspace_bytes >= xv_sampler_workspace_size(batch, vocab)) {
+    const SegLayout L = seg_layout(batch, vocab);
+    char* w = (char*)workspace;
+    SegArgs a;
+    a.logits = (const bf16_t*)logits; a.stride = logits_stride;
+    a.V = vocab; a.R = L.R; a.seg_len = L.seg_len; a.flags = flags & ~XV_SAMPLE_ALL_GREEDY;
+    a.temps = temperatures; a.top_ps = top_ps; a.top_ks = top_ks; a.min_ps = min_ps; a.uniforms = uniforms;
+    a.out_ids = out_ids;
+    a.plans = (RowPlan*)(w + L.plans);
+    a.seg_kmax = (uint32_t*)(w + L.kmax);
+    a.seg_kmin = (uint32_t*)(w + L.kmin);
+    a.seg_minp = (uint32_t*)(w + L.minp);
+    a.seg_best = (unsigned long long*)(w + L.best);
+    a.seg_kept = (int64_t*)(w + L.kept);
+    a.seg_cnt = (uint32_t*)(w + L.cnt);
+    a.seg_mass = (unsigned long long*)(w + L.mass);
+    a.cand = (unsigned long long*)(w + L.cand);
+    const dim3 segs((unsigned)L.R, (unsigned)batch), rows((unsigned)batch);
+    seg_stats_kernel<<<segs, kSegThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    seg_hist_kernel<<<segs, kSegThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    row_plan_kernel<<<rows, kSegThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    seg_gather_kernel<<<segs, kSegThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    row_cut_kernel<<<rows, kThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    seg_kept_kernel<<<segs, kSegThreads, 0, stream>>>(a);
+    XV_CHECK_LAUNCH();
+    row_draw_kernel<<<rows, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     return 0;
   }

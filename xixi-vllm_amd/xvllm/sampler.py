@@ -50,8 +50,13 @@ def sample(
     use_top_p: bool = False,
     use_min_p: bool = False,
     out: torch.Tensor | None = None,
+    multi_workgroup: bool = True,
 ) -> torch.Tensor:
-    """Raw entry: bf16 logits [B, V] -> int64 ids [B] (graph-capturable)."""
+    """Raw entry: bf16 logits [B, V] -> int64 ids [B] (graph-capturable).
+
+    With `multi_workgroup` (the default) the kernels get a workspace and split
+    each row over several workgroups; without it one workgroup takes a row.
+    Both give the same ids."""
     require_cuda(logits)
     require_bf16(logits)
     if logits.stride(-1) != 1:
@@ -79,11 +84,11 @@ def sample(
     if out is None:
         out = torch.empty(bsz, dtype=torch.int64, device=logits.device)
     L = _C.lib()
-    ws = _workspace(logits.device, L.xv_sampler_workspace_size(bsz, vocab))
+    ws = _workspace(logits.device, L.xv_sampler_workspace_size(bsz, vocab)) if multi_workgroup else None
     _C.check(
         L.xv_sample(
             ptr(logits), logits.stride(0), bsz, vocab, ptr(temps), ptr(tps), ptr(tks), ptr(mps), ptr(us), flags,
-            ptr(out), ptr(ws), ws.numel(), stream_of(logits),
+            ptr(out), ptr(ws), ws.numel() if ws is not None else 0, stream_of(logits),
         ),
         "xv_sample",
     )
