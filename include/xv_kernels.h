@@ -200,9 +200,11 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  * uniforms[b] in [0, 1), masses in 2^-40 fixed point (exact integer sums).
  * flags: XV_SAMPLE_* bits mirroring the reference's host-side switches.
  * workspace: xv_sampler_workspace_size(B, V) bytes, zero-filled before its
- *   first use (each call leaves it zero), used by all-greedy calls to spread a
- *   row over several workgroups; NULL selects one workgroup per row.  Calls
- *   sharing a workspace must be ordered on one stream.
+ *   first use (each call leaves its greedy counters zero).  With it, all-greedy
+ *   calls and calls of up to 128 rows spread each row over several workgroups
+ *   (larger sampled batches take one workgroup per row, which fills the
+ *   device); NULL selects one workgroup per row.  Both give identical ids.
+ *   Calls sharing a workspace must be ordered on one stream.
  */
 #define XV_SAMPLE_ALL_GREEDY 1
 #define XV_SAMPLE_USE_TOP_K  2
