@@ -96,6 +96,8 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
  *         element (row, kvh, d) at row*kv_stride_tok + kvh*kv_stride_head + d.
  *   out : element (tok, h, d) at tok*out_stride_tok + h*D + d.
  * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 when paged.
+ * Rows move by 16-byte LDS-DMA: q, k, v, k_cache and v_cache 16-byte aligned,
+ * every stride a multiple of 8 elements (hipErrorInvalidValue otherwise).
  */
 int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                          const void* k, const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,
