@@ -63,7 +63,8 @@ int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
  *              second kernel.  No initial contents are required.  Calls
  *              sharing a workspace must be ordered on one stream.
  * Query head h reads kv head h / (Hq / Hkv).  scale multiplies q.k (1/sqrt(D) in the reference).
- * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16, batch <= 256,
+ * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 (batches above
+ * 256 run as consecutive launches of 256 sequences on the same workspace),
  * head rows of 256 contiguous bytes with head_stride*(Hkv-1) + D <= tok_stride
  * or tok_stride == D (the reference's [page][token][head][d] pool, or a
  * [page][head][token][d] pool).  q, k_cache, v_cache 16-byte aligned and every

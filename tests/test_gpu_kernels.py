@@ -107,6 +107,61 @@ def test_paged_decode_many_short_sequences(dev):
     _close(f32(out).reshape(256, 32, 128), want)
 
 
+def test_paged_decode_batch_above_256(dev):
+    """B 300: two launches of the kernel pair (256 + 44 sequences) on one
+    workspace, with padding rows on both sides of the cut."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = gen(300)
+    ctx = torch.randint(0, 200, (300,), generator=g).tolist()
+    ctx[255] = ctx[256] = 0
+    ctx[299] = 1
+    need = sum((c + 15) // 16 for c in ctx)
+    kc, vc, bt, sl = make_paged(ctx, int(need * 1.25) + 4, 8, 128, g)
+    q = randn_bf16((300, 32, 128), g)
+    want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
+    out = paged_decode_attention(q.view(300, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), 32, 8, 128)
+    torch.cuda.synchronize()
+    _close(f32(out).reshape(300, 32, 128), want)
+
+
+@pytest.mark.parametrize("ctxlen,bsz", [(32768, 2), (131072, 1)])
+def test_paged_decode_single_long_sequence(dev, ctxlen, bsz):
+    """A few sequences of 32k / 128k tokens (block tables of 2048 / 8192
+    pages): every wave streams part of one sequence, and the merge combines
+    up to max_blocks / min-range partials per head.  K/V drawn on the device;
+    checked against a plain fp32 torch softmax attention over the gathered
+    keys (the numpy oracle is too slow at this length)."""
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = torch.Generator(device=dev).manual_seed(ctxlen)
+    hq, hkv, d = 32, 8, 128
+    npg = ctxlen // 16
+    pool = bsz * npg + 3
+    kc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    perm = torch.randperm(pool, generator=gen(ctxlen))[: bsz * npg].to(torch.int32)
+    bt = perm.view(bsz, npg).to(dev)
+    sl = torch.full((bsz,), ctxlen, dtype=torch.int32, device=dev)
+    sl[-1] = ctxlen - 9
+    q = torch.randn((bsz, hq * d), generator=g, device=dev).to(torch.bfloat16)
+    out = paged_decode_attention(q, kc, vc, bt, sl, hq, hkv, d)
+    torch.cuda.synchronize()
+    for r in range(bsz):
+        # reference on the GPU in fp32 (exact softmax over the gathered keys)
+        n = int(sl[r])
+        pages = bt[r].long()
+        k = kc[pages].reshape(-1, hkv, d)[:n].float()
+        v = vc[pages].reshape(-1, hkv, d)[:n].float()
+        qr = q[r].view(hq, d).float()
+        kh = k.repeat_interleave(hq // hkv, dim=1)  # [n, hq, d]
+        vh = v.repeat_interleave(hq // hkv, dim=1)
+        s = torch.einsum("hd,nhd->hn", qr, kh) / math.sqrt(d)
+        want = torch.einsum("hn,nhd->hd", torch.softmax(s, dim=-1), vh)
+        _close(f32(out[r].cpu()).reshape(1, hq, d), want.cpu().numpy().reshape(1, hq, d))
+    assert torch.isfinite(out.float()).all()
+
+
 def test_paged_decode_long_ranges(dev):
     """B 64 x ctx 8192: each wave streams ~256 pages, crossing page-id table
     windows.  K/V are drawn on the device; the oracle gets only the pages of

@@ -638,7 +638,20 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   const int group = num_q_heads / num_kv_heads;
   if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
   if (batch == 0) return 0;
-  if (batch > kMaxBatch) return (int)hipErrorInvalidValue;
+  if (batch > kMaxBatch) {
+    // chunks of kMaxBatch sequences, in stream order on the same workspace
+    // (every call leaves its counters zero)
+    for (int c0 = 0; c0 < batch; c0 += kMaxBatch) {
+      const int rc = xv_paged_decode_attention(
+          (const bf16_t*)q + (int64_t)c0 * q_stride_tok, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride,
+          tok_stride, head_stride, block_tables + (int64_t)c0 * bt_stride, bt_stride, cache_seqlens + c0,
+          (bf16_t*)out + (int64_t)c0 * out_stride_tok, out_stride_tok, workspace, workspace_bytes,
+          min(kMaxBatch, batch - c0), num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale,
+          stream);
+      if (rc) return rc;
+    }
+    return 0;
+  }
   // rows move by 16-byte LDS-DMA: aligned bases, strides in whole 16-byte units
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
       (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
