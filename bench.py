@@ -672,12 +672,13 @@ def main() -> int:
 
     sweep = {}
     if not args.no_sweep:
-        for bsz in (1, 8, 64, 256):
-            c2 = [2048] * bsz
+        # config 2's batch sweep at ctx 2048, and one long single-sequence decode
+        for bsz, clen in ((1, 2048), (8, 2048), (64, 2048), (256, 2048), (1, 32768)):
+            c2 = [clen] * bsz
             cs = make_case(torch, c2, layers=4 if bsz <= 64 else 2, dev=dev, seed=args.seed + bsz)
             m2 = time_decode_graph(torch, cs) * 1e-3
-            sweep[f"B{bsz}_ctx2048"] = {"us": round(m2 * 1e3, 2), "GB/s": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9, 1),
-                                        "frac": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            sweep[f"B{bsz}_ctx{clen}"] = {"us": round(m2 * 1e3, 2), "GB/s": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9, 1),
+                                          "frac": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             del cs
         torch.cuda.empty_cache()
 

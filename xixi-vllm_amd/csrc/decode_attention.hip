@@ -535,12 +535,16 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   XV_DECODE_TIMESTAMP(2);
 }
 
-// Merge the partials of one (sequence, query head): 64 lanes x 2 dims.  Also
+// Merge the partials of one (sequence, query head) with one wave.  Also
 // writes the zero output of padding rows (cache_seqlens 0).  The partial
-// count comes from the main kernel.  The count, the sequence length and the
-// first two partials (the common split) are loaded together, so a two-way
-// merge costs one memory round trip; further partials are loaded four at a
-// time.
+// count comes from the main kernel.  The count, the sequence length, the
+// first two partials (the common split, 2 dims per lane) and the
+// log2-sum-exp of partial `lane` are loaded together, so a two-way merge costs
+// one memory round trip.  More partials: lane j holds partial j's weight
+// (j < 64, then j - 64, j - 128 in two more registers); four groups of 16
+// lanes take every fourth partial, 8 dims per lane, eight partials per batch
+// of loads, and the groups are summed by lane swaps.
+constexpr int kMergeMaxParts = 192;
 __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int b = blockIdx.x / a.hq;
   const int h = blockIdx.x - b * a.hq;
@@ -549,44 +553,87 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
   const int ctx = a.seqlens[b];
   const int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
-  // speculative: rows 0 and 1 exist in every workspace (max_parts >= 2)
+  // speculative: rows 0 and 1 exist in every workspace (max_parts >= 2), rows < max_parts too
   const float l0 = a.ws_lse[row0], l1 = a.ws_lse[row0 + 1];
   const float2 v0 = *reinterpret_cast<const float2*>(a.ws_o + row0 * kD + d);
   const float2 v1 = *reinterpret_cast<const float2*>(a.ws_o + (row0 + 1) * kD + d);
-  uint32_t* dst = reinterpret_cast<uint32_t*>(a.out + (int64_t)b * a.out_st + (int64_t)h * kD + d);
+  const float lmine = lane < a.max_parts ? a.ws_lse[row0 + lane] : -INFINITY;
+  bf16_t* orow = a.out + (int64_t)b * a.out_st + (int64_t)h * kD;
   if (ctx <= 0) {
-    *dst = 0u;
+    *reinterpret_cast<uint32_t*>(orow + d) = 0u;
     return;
   }
   if (n <= 1) return;
-  float mx = fmaxf(l0, l1);
-  for (int s = 2; s < n; ++s) mx = fmaxf(mx, a.ws_lse[row0 + s]);
-  const float w0 = __builtin_amdgcn_exp2f(l0 - mx), w1 = __builtin_amdgcn_exp2f(l1 - mx);
-  float den = w0 + w1;
-  float o0 = w0 * v0.x + w1 * v1.x, o1 = w0 * v0.y + w1 * v1.y;
-  for (int s0 = 2; s0 < n; s0 += 4) {
-    float ls[4];
-    float2 vs[4];
+  if (n == 2) {
+    const float mx = fmaxf(l0, l1);
+    const float w0 = __builtin_amdgcn_exp2f(l0 - mx), w1 = __builtin_amdgcn_exp2f(l1 - mx);
+    const float inv = 1.0f / (w0 + w1);
+    *reinterpret_cast<uint32_t*>(orow + d) =
+        pack_bf16x2((w0 * v0.x + w1 * v1.x) * inv, (w0 * v0.y + w1 * v1.y) * inv);
+    return;
+  }
+  // weights: lane j holds partials j, 64 + j, 128 + j
+  const float la = lane < n ? lmine : -INFINITY;
+  const float lb = 64 + lane < n ? a.ws_lse[row0 + 64 + lane] : -INFINITY;
+  const float lc = 128 + lane < n ? a.ws_lse[row0 + 128 + lane] : -INFINITY;
+  float mx = fmaxf(la, fmaxf(lb, lc));
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int64_t r = row0 + min(s0 + k, n - 1);
-      ls[k] = s0 + k < n ? a.ws_lse[r] : -INFINITY;
-      vs[k] = *reinterpret_cast<const float2*>(a.ws_o + r * kD + d);
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const float wa = lane < n ? __builtin_amdgcn_exp2f(la - mx) : 0.f;
+  const float wb = 64 + lane < n ? __builtin_amdgcn_exp2f(lb - mx) : 0.f;
+  const float wc = 128 + lane < n ? __builtin_amdgcn_exp2f(lc - mx) : 0.f;
+  float den = wa + wb + wc;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+  const int g = lane >> 4, i = lane & 15;  // group g: partials g, g + 4, ...; dims 8i .. 8i + 7
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < n; j0 += 32) {
+    float4 v[8][2];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int j = min(j0 + 4 * k + g, n - 1);
+      const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
+      v[k][0] = src[0];
+      v[k][1] = src[1];
     }
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const float w = __builtin_amdgcn_exp2f(ls[k] - mx);  // 0 past n
-      den += w;
-      o0 += w * vs[k].x;
-      o1 += w * vs[k].y;
+    for (int k = 0; k < 8; ++k) {
+      // partial j's weight sits in lane j mod 64, in the register of its
+      // 64-block; j differs between groups, so fetch all three and pick
+      const int j = j0 + 4 * k + g;
+      const int jj = j & 63;
+      const float w_a = __shfl(wa, jj), w_b = __shfl(wb, jj), w_c = __shfl(wc, jj);
+      const float w = j < n ? (j < 64 ? w_a : j < 128 ? w_b : w_c) : 0.f;
+      acc[0] += w * v[k][0].x; acc[1] += w * v[k][0].y; acc[2] += w * v[k][0].z; acc[3] += w * v[k][0].w;
+      acc[4] += w * v[k][1].x; acc[5] += w * v[k][1].y; acc[6] += w * v[k][1].z; acc[7] += w * v[k][1].w;
     }
   }
-  const float inv = 1.0f / den;
-  *dst = pack_bf16x2(o0 * inv, o1 * inv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    acc[e] += __shfl_xor(acc[e], 16);
+    acc[e] += __shfl_xor(acc[e], 32);
+  }
+  if (g == 0) {
+    const float inv = 1.0f / den;
+    uint32_t* o = reinterpret_cast<uint32_t*>(orow + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+  }
 }
 
-// Minimum pages per wave range: bounds the partial count per (sequence, head).
-int min_range_pages(int max_blocks_per_seq) { return max(8, (max_blocks_per_seq + 31) / 32); }
+// Minimum pages per wave range.  It bounds the partials per (sequence, head),
+// parts = ceil(max_blocks / lmin) + 1, by P: at most 129, and fewer when the
+// workspace for batch x q heads x P partials would pass kPartBudget.  Small
+// batches of long sequences thus still fill every wave slot, and at least two
+// pages per range keep the page pipeline busy.
+constexpr int kMaxParts = 129;
+constexpr size_t kPartBudget = (size_t)32 << 20;
+static_assert(kMaxParts <= kMergeMaxParts, "the merge holds at most kMergeMaxParts weights per head");
+int min_range_pages(int batch, int num_q_heads, int max_blocks_per_seq) {
+  const size_t per_part = (size_t)max(batch, 1) * max(num_q_heads, 1) * (kD + 1) * sizeof(float);
+  const int P = (int)max((size_t)3, min((size_t)kMaxParts, kPartBudget / per_part));
+  return max(2, (max_blocks_per_seq + P - 2) / (P - 1));
+}
 
 int waves_for(int group) {
   // resident single-wave workgroups: CUs x per-CU occupancy (queried once per device)
@@ -614,12 +661,23 @@ int waves_for(int group) {
 // Workspace layout: [partial counts int32, B*Hkv, padded to 256 B][partial outputs fp32][partial log2-sum-exp fp32]
 size_t counter_bytes(int batch, int num_kv_heads) { return ((size_t)batch * num_kv_heads * 4 + 255) / 256 * 256; }
 
+// Workspace of one launch of `batch` <= kMaxBatch sequences.
+size_t chunk_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_blocks_per_seq) {
+  const int lmin = min_range_pages(batch, num_q_heads, max_blocks_per_seq);
+  const int parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
+  return counter_bytes(batch, num_kv_heads) + (size_t)batch * num_q_heads * parts * ((size_t)kD + 1) * sizeof(float);
+}
+
 extern "C" size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int max_blocks_per_seq, int block_size, int head_dim) {
   (void)block_size;
+  (void)head_dim;
   if (batch <= 0 || max_blocks_per_seq <= 0 || num_kv_heads <= 0) return 256;
-  const int parts = (max_blocks_per_seq + min_range_pages(max_blocks_per_seq) - 1) / min_range_pages(max_blocks_per_seq) + 1;
-  return counter_bytes(batch, num_kv_heads) + (size_t)batch * num_q_heads * parts * ((size_t)head_dim + 1) * sizeof(float);
+  // batches above kMaxBatch run in chunks of kMaxBatch and one remainder
+  size_t need = chunk_workspace_bytes(min(batch, kMaxBatch), num_q_heads, num_kv_heads, max_blocks_per_seq);
+  if (batch > kMaxBatch && batch % kMaxBatch)
+    need = max(need, chunk_workspace_bytes(batch % kMaxBatch, num_q_heads, num_kv_heads, max_blocks_per_seq));
+  return need;
 }
 
 extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -656,8 +714,7 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
       (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
     return (int)hipErrorInvalidValue;
-  const size_t need = xv_paged_decode_workspace_size(batch, num_q_heads, num_kv_heads, max_blocks_per_seq,
-                                                     block_size, head_dim);
+  const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_blocks_per_seq);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
   DecodeArgs a;
   a.q = (const bf16_t*)q; a.q_st = q_stride_tok; a.q_sh = q_stride_head;
@@ -665,7 +722,7 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   a.page_stride = page_stride; a.tok_stride = tok_stride; a.head_stride = head_stride;
   a.bt = block_tables; a.bt_stride = bt_stride; a.seqlens = cache_seqlens;
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
-  const int lmin = min_range_pages(max_blocks_per_seq);
+  const int lmin = min_range_pages(batch, num_q_heads, max_blocks_per_seq);
   a.max_parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
   a.ws_nparts = (int*)workspace;
   a.ws_o = (float*)((char*)workspace + counter_bytes(batch, num_kv_heads));
