@@ -1,5 +1,9 @@
 // Vocab-wide sampler for gfx950: greedy argmax, temperature / top-k / top-p /
-// min-p with an explicit uniform per row, one 1024-thread workgroup per row.
+// min-p with an explicit uniform per row.  Three launch shapes share the
+// arithmetic below: one 1024-thread workgroup per row (sample_kernel), the
+// all-greedy argmax over several workgroups per row (greedy_segment_kernel),
+// and the sampled path over several workgroups per row for batches of up to
+// kSegMaxBatch rows (the seg_* / row_* chain); all give the same ids.
 //
 // Candidates are ordered by descending logit, ties by ascending id.  Every
 // candidate's probability mass is an exact int64
@@ -8,10 +12,11 @@
 // oracle, so kept sets, masses and token ids are bit-identical to it.
 //
 // Fast path (every row whose boundary fits in LDS):
-//   1. one pass: max key;
+//   1. one pass: max and min keys;
 //   2. one pass: q of every candidate, binned by distance below the max,
-//      bucket = min(255, floor(-16 d)) (1/16 of a binary order per bucket;
-//      per-wave LDS histograms of counts and masses, the far bucket in registers);
+//      bucket = min(255, floor(-bs d)) with bs = 16 buckets per binary order,
+//      or finer for rows spanning less than 255/16 orders (per-wave LDS
+//      histograms of counts and masses, the far bucket in registers);
 //   3. the buckets give the bucket holding each cut-off: top-k (by count),
 //      top-p (first bucket whose inclusive mass exceeds floor(top_p * mass of
 //      the top-k set)), min-p (bucket of the smallest key whose probability
@@ -37,7 +42,6 @@ namespace {
 
 constexpr int kThreads = 1024;
 constexpr int kWaves = kThreads / 64;
-constexpr int kTile = kThreads * 8;
 constexpr int64_t kTieAll = 0x7fffffffffffffffll;
 constexpr int kBuckets = 256;
 constexpr int kMaxCand = 8192;  // candidates of one bucket sorted in LDS
@@ -536,7 +540,7 @@ XV_INLINE void sort_cand_desc(FastShared& fs, int n) {
 // Gather the candidates of bucket `target` into fs.cand and bitonic-sort them
 // descending (key descending, id ascending).  Returns the count; a count above
 // kMaxCand means the bucket did not fit (nothing sorted).
-XV_INLINE int gather_bucket(FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t,
+XV_INLINE int gather_bucket(FastShared& fs, const bf16_t* row, int V, bool vec_ok, float inv_t,
                             float zmax, float bs, int target, int target_lo = -1) {
   if (target_lo < 0) target_lo = target;  // gather buckets target_lo .. target
   const int t = threadIdx.x;
@@ -596,7 +600,7 @@ XV_INLINE int64_t list_count_ge(Shared& s, const FastShared& fs, int n, uint32_t
 // Smallest key whose probability reaches min_p of the largest (0xffffffff:
 // none).  Only candidates within half a binary order of the threshold need an
 // exp: below that their probability is certainly under min_p.
-XV_INLINE uint32_t minp_key(Shared& s, const bf16_t* row, int V, bool vec_ok, int ntiles, float inv_t, float zmax,
+XV_INLINE uint32_t minp_key(Shared& s, const bf16_t* row, int V, bool vec_ok, float inv_t, float zmax,
                             float min_p) {
   const float d_lo = __log2f(min_p) - 0.5f;
   uint32_t kminp = 0xffffffffu;
@@ -612,7 +616,7 @@ XV_INLINE uint32_t minp_key(Shared& s, const bf16_t* row, int V, bool vec_ok, in
 // Fast path with top-k: bucket counts only (no exp), then every candidate of
 // the buckets up to the one holding rank k-1 is gathered and sorted; the
 // top-k set, its mass, the top-p and min-p cuts all come from that list.
-XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
+XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok,
                              float inv_t, float zmax, float bs, int top_k, float top_p, float min_p, bool use_p, bool use_m,
                              uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
   const int t = threadIdx.x, w = t >> 6;
@@ -645,8 +649,8 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     }
   }
   if (bk >= kBuckets - 1 || upto > kMaxCand) return false;  // rank k-1 far out or too many: exact row-wide path
-  const uint32_t kminp = use_m ? minp_key(s, row, V, vec_ok, ntiles, inv_t, zmax, min_p) : 0xffffffffu;
-  const int n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bk, 0);
+  const uint32_t kminp = use_m ? minp_key(s, row, V, vec_ok, inv_t, zmax, min_p) : 0xffffffffu;
+  const int n = gather_bucket(fs, row, V, vec_ok, inv_t, zmax, bs, bk, 0);
   XV_SAMPLER_TIMESTAMP(6);
   if (n > kMaxCand) return false;
   const int64_t total_k = list_mass_prefix(s, fs, n, top_k, inv_t, zmax);
@@ -669,11 +673,11 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
 
 // Fast path: kept set = key > key_cut, or key == key_cut and id <= id_cut;
 // M = its mass.  Returns false when a boundary bucket overflowed the list.
-XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok, int ntiles,
+XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V, bool vec_ok,
                              float inv_t, float zmax, float bs, int top_k, float top_p, float min_p, bool use_k, bool use_p,
                              bool use_m, uint32_t& key_cut, int64_t& id_cut, int64_t& M, int& list_kept) {
   const int t = threadIdx.x, w = t >> 6;
-  if (use_k) return topk_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, top_k, top_p, min_p, use_p, use_m,
+  if (use_k) return topk_boundary(s, fs, row, V, vec_ok, inv_t, zmax, bs, top_k, top_p, min_p, use_p, use_m,
                                   key_cut, id_cut, M, list_kept);
   // ---- pass 2: every candidate's mass, binned by distance below the max ----
   for (int i = t; i < kWaves * kBuckets; i += kThreads) {
@@ -735,7 +739,7 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   int nk = 0;
   if (bk < kBuckets) {
     if (s.cnt[bk] > (uint32_t)kMaxCand) return false;  // known before gathering
-    nk = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bk);
+    nk = gather_bucket(fs, row, V, vec_ok, inv_t, zmax, bs, bk);
     if (nk > kMaxCand) return false;
     total_k = mk_before + list_mass_prefix(s, fs, nk, top_k - ck_before, inv_t, zmax);
   }
@@ -756,7 +760,7 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   int n = nk;
   if (bf != bk) {
     if (s.cnt[bf] > (uint32_t)kMaxCand) return false;
-    n = gather_bucket(fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, bf);
+    n = gather_bucket(fs, row, V, vec_ok, inv_t, zmax, bs, bf);
     if (n > kMaxCand) return false;
   }
   // ---- exact cut inside the boundary bucket ----
@@ -821,7 +825,6 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   const int t = threadIdx.x;
   const bf16_t* row = logits + (int64_t)b * stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
-  const int ntiles = (V + kTile - 1) / kTile;
   const float temp = temps ? temps[b] : 1.0f;
   const bool greedy = (flags & XV_SAMPLE_ALL_GREEDY) || temp <= 1e-5f;
 
@@ -866,7 +869,7 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   uint32_t key_cut;
   int64_t id_cut, M;
   int list_kept = 0;  // > 0: the kept set is the sorted list prefix fs.cand[0, list_kept)
-  if (!fast_boundary(s, fs, row, V, vec_ok, ntiles, inv_t, zmax, bs, top_k, top_p, min_p, use_k, use_p, use_m,
+  if (!fast_boundary(s, fs, row, V, vec_ok, inv_t, zmax, bs, top_k, top_p, min_p, use_k, use_p, use_m,
                      key_cut, id_cut, M, list_kept)) {
     list_kept = 0;
     Boundary bd;
