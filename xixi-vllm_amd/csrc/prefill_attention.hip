@@ -222,14 +222,18 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: keeps per-wave values scalar
   const int l32 = lane & 31, h = lane >> 5;
-  const int b = blockIdx.z;
-  const int kvh = G == 8 ? (int)blockIdx.y >> 1 : (int)blockIdx.y;
-  const int head = G == 8 ? kvh * 8 + ((int)blockIdx.y & 1) * 4 + wave : kvh * G + wave % GW;
+  // XCD-aware order: workgroups go round-robin to the 8 XCDs, so with the head
+  // slot fastest every XCD serves the same kv head(s) and keeps their K/V tiles
+  // in its own L2; each head carries the same work, which balances the XCDs.
+  const int hsel = blockIdx.x, rank = blockIdx.y, b = blockIdx.z;
+  const int kvh = G == 8 ? hsel >> 1 : hsel;
+  const int head = G == 8 ? kvh * 8 + (hsel & 1) * 4 + wave : kvh * G + wave % GW;
   const int q0 = a.cu_q[b], q_len = a.cu_q[b + 1] - q0;
   const int k0 = a.cu_k[b], k_len = a.cu_k[b + 1] - k0;
-  // the longest (last) query blocks of the causal triangle are dispatched first
-  const int qb0 = (a.qblocks - 1 - (int)blockIdx.x) * kBlockQ;
-  if (qb0 >= q_len) return;
+  // rank from the sequence's own end: the last (longest) block of the causal
+  // triangle is dispatched first, then the next-to-last, ...
+  const int qb0 = ((q_len + kBlockQ - 1) / kBlockQ - 1 - rank) * kBlockQ;
+  if (qb0 < 0) return;
   const int shift = k_len - q_len;  // bottom-right alignment
   const int qw0 = qb0 + (wave / GW) * 32;  // the wave's first query
   const int my_q = qw0 + l32;
@@ -442,7 +446,8 @@ extern "C" int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   const int gw = group < 4 ? group : 4;
   const int block_q = 32 * (4 / gw);
   a.qblocks = (max_seqlen_q + block_q - 1) / block_q;
-  dim3 grid((unsigned)a.qblocks, (unsigned)(num_kv_heads * (group == 8 ? 2 : 1)), (unsigned)batch);
+  if (a.qblocks > 65535 || batch > 65535) return (int)hipErrorInvalidValue;  // grid y / z limits
+  const dim3 grid((unsigned)(num_kv_heads * (group == 8 ? 2 : 1)), (unsigned)a.qblocks, (unsigned)batch);
   switch (group) {
     case 1: launch<1>(a, grid, stream); break;
     case 2: launch<2>(a, grid, stream); break;
