@@ -226,8 +226,10 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   // slot fastest every XCD serves the same kv head(s) and keeps their K/V tiles
   // in its own L2; each head carries the same work, which balances the XCDs.
   const int hsel = blockIdx.x, rank = blockIdx.y, b = blockIdx.z;
-  const int kvh = G == 8 ? hsel >> 1 : hsel;
-  const int head = G == 8 ? kvh * 8 + (hsel & 1) * 4 + wave : kvh * G + wave % GW;
+  // group 8: two slots per kv head (query heads 0-3 and 4-7), slot = half * Hkv
+  // + kvh, so both halves of a kv head land on the same XCD
+  const int kvh = G == 8 ? hsel % a.hkv : hsel;
+  const int head = G == 8 ? kvh * 8 + (hsel / a.hkv) * 4 + wave : kvh * G + wave % GW;
   const int q0 = a.cu_q[b], q_len = a.cu_q[b + 1] - q0;
   const int k0 = a.cu_k[b], k_len = a.cu_k[b + 1] - k0;
   // rank from the sequence's own end: the last (longest) block of the causal
