@@ -38,8 +38,8 @@ def slots_for_range(block_table, start: int, end: int, block_size: int) -> np.nd
     return (bt[p // block_size] * block_size + p % block_size).astype(np.int32)
 
 
-def _pinned(shape, dtype, fill=None):
-    t = torch.empty(shape, dtype=dtype, pin_memory=True)
+def _pinned(shape, dtype, fill=None, pin=True):
+    t = torch.empty(shape, dtype=dtype, pin_memory=pin)
     if fill is not None:
         t.fill_(fill)
     return t
@@ -65,16 +65,18 @@ class Batch:
         self.all_greedy, self.any_greedy = True, False
         self.use_top_k = self.use_top_p = self.use_min_p = False
         self.max_top_k = 0
-        # pinned host staging
-        self._h_ids = _pinned((max_tokens,), torch.int64)
-        self._h_pos = _pinned((max_tokens,), torch.int64)
-        self._h_slot = _pinned((max_tokens,), torch.int32, -1)
-        self._h_csl = _pinned((max_bs,), torch.int32)
-        self._h_cuq = _pinned((max_bs + 1,), torch.int32)
-        self._h_cuk = _pinned((max_bs + 1,), torch.int32)
-        self._h_bt = _pinned((max_bs, max_blocks), torch.int32, -1)
-        self._h_samp = _pinned((4, max_bs), torch.float32)
-        self._h_topk = _pinned((max_bs,), torch.int32)
+        # pinned host staging (plain host memory when the buffers live on the CPU,
+        # which runs the same host logic without a GPU)
+        pin = torch.device(device).type == "cuda"
+        self._h_ids = _pinned((max_tokens,), torch.int64, pin=pin)
+        self._h_pos = _pinned((max_tokens,), torch.int64, pin=pin)
+        self._h_slot = _pinned((max_tokens,), torch.int32, -1, pin=pin)
+        self._h_csl = _pinned((max_bs,), torch.int32, pin=pin)
+        self._h_cuq = _pinned((max_bs + 1,), torch.int32, pin=pin)
+        self._h_cuk = _pinned((max_bs + 1,), torch.int32, pin=pin)
+        self._h_bt = _pinned((max_bs, max_blocks), torch.int32, -1, pin=pin)
+        self._h_samp = _pinned((4, max_bs), torch.float32, pin=pin)
+        self._h_topk = _pinned((max_bs,), torch.int32, pin=pin)
         self._bt_np = self._h_bt.numpy()
         self._row_len = np.full(max_bs, -1, dtype=np.int64)   # entries of each host row in sync
         self._row_sid = np.full(max_bs, -1, dtype=np.int64)   # sequence that owns the row
