@@ -68,7 +68,8 @@ int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
  * head rows of 256 contiguous bytes with head_stride*(Hkv-1) + D <= tok_stride
  * or tok_stride == D (the reference's [page][token][head][d] pool, or a
  * [page][head][token][d] pool).  q, k_cache, v_cache 16-byte aligned and every
- * stride a multiple of 8 elements (rows move by 16-byte LDS-DMA).
+ * input stride a multiple of 8 elements (rows move by 16-byte LDS-DMA); out
+ * 4-byte aligned with an even out_stride_tok.
  */
 size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                       int max_blocks_per_seq, int block_size, int head_dim);
@@ -98,7 +99,8 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
  *   out : element (tok, h, d) at tok*out_stride_tok + h*D + d.
  * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 when paged.
  * Rows move by 16-byte LDS-DMA: q, k, v, k_cache and v_cache 16-byte aligned,
- * every stride a multiple of 8 elements (hipErrorInvalidValue otherwise).
+ * every input stride a multiple of 8 elements; out 8-byte aligned with
+ * out_stride_tok a multiple of 4 (hipErrorInvalidValue otherwise).
  */
 int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
                          const void* k, const void* v, int64_t kv_stride_tok, int64_t kv_stride_head,

@@ -1,0 +1,96 @@
+"""Host-side argument checks of the C ABI, run without a GPU: every call below
+is malformed (bad sizes, misaligned pointers, strides not in 16-byte units, a
+short workspace), so the entry point returns hipErrorInvalidValue before any
+HIP call; pointers are fake and never dereferenced.  Also the workspace-size
+queries, which are pure host arithmetic."""
+import ctypes as C
+
+import pytest
+
+INVALID = 1  # hipErrorInvalidValue
+A = 0x10000  # a 16-byte aligned fake address
+U = A + 8    # 8 bytes off
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from xvllm import _C
+
+    if not _C.lib_path().exists():
+        pytest.fail("libxv_kernels.so is not built (run __graft_entry__.build())")
+    return _C.lib()
+
+
+def _decode(lib, **kw):
+    a = dict(q=A, qst=4096, qsh=128, kc=A, vc=A, ps=16384, ts=1024, hs=128, bt=A, bts=256, sl=A, out=A, ost=4096,
+             ws=A, wsb=1 << 30, B=64, Hq=32, Hkv=8, D=128, BS=16, maxb=256, scale=0.088)
+    a.update(kw)
+    return lib.xv_paged_decode_attention(a["q"], a["qst"], a["qsh"], a["kc"], a["vc"], a["ps"], a["ts"], a["hs"],
+                                         a["bt"], a["bts"], a["sl"], a["out"], a["ost"], a["ws"], a["wsb"], a["B"],
+                                         a["Hq"], a["Hkv"], a["D"], a["BS"], a["maxb"], a["scale"], None)
+
+
+def test_decode_rejects_bad_layouts(lib):
+    for kw in (dict(D=64), dict(BS=32), dict(Hq=12), dict(Hq=128), dict(q=U), dict(kc=U), dict(qst=4100),
+               dict(ts=1028), dict(out=A + 2), dict(ost=4097), dict(ws=None), dict(wsb=1024), dict(maxb=0)):
+        assert _decode(lib, **kw) == INVALID, kw
+    assert _decode(lib, B=0) == 0  # nothing to do
+
+
+def _prefill(lib, **kw):
+    a = dict(q=A, qst=4096, qsh=128, k=A, v=A, kvst=1024, kvsh=128, kc=None, vc=None, ps=0, ts=0, hs=0, bt=None,
+             bts=0, cuq=A, cuk=A, out=A, ost=4096, B=4, maxq=512, Hq=32, Hkv=8, D=128, BS=16, scale=0.088)
+    a.update(kw)
+    return lib.xv_prefill_attention(a["q"], a["qst"], a["qsh"], a["k"], a["v"], a["kvst"], a["kvsh"], a["kc"],
+                                    a["vc"], a["ps"], a["ts"], a["hs"], a["bt"], a["bts"], a["cuq"], a["cuk"],
+                                    a["out"], a["ost"], a["B"], a["maxq"], a["Hq"], a["Hkv"], a["D"], a["BS"],
+                                    a["scale"], None)
+
+
+def test_prefill_rejects_bad_layouts(lib):
+    for kw in (dict(D=64), dict(Hq=24), dict(k=None), dict(k=U), dict(kvst=1020), dict(q=U), dict(qsh=130),
+               dict(out=A + 4), dict(ost=4098), dict(bt=A, kc=A, vc=A, BS=32), dict(bt=A, kc=None, vc=A),
+               dict(bt=A, kc=U, vc=A, BS=16), dict(maxq=32 * 65536)):
+        assert _prefill(lib, **kw) == INVALID, kw
+    assert _prefill(lib, B=0) == 0 and _prefill(lib, maxq=0) == 0
+
+
+def test_elementwise_entry_points_reject_bad_layouts(lib):
+    s = None
+    # store: head_dim not a multiple of 8, misaligned key, cache stride not in 16-byte units
+    assert lib.xv_store_kvcache(A, 1024, 128, A, 1024, 128, A, A, 16384, 1024, 128, 16, A, 4, 8, 100, s) == INVALID
+    assert lib.xv_store_kvcache(U, 1024, 128, A, 1024, 128, A, A, 16384, 1024, 128, 16, A, 4, 8, 128, s) == INVALID
+    assert lib.xv_store_kvcache(A, 1024, 128, A, 1024, 128, A, A, 16384, 1020, 128, 16, A, 4, 8, 128, s) == INVALID
+    # norms: hidden not a multiple of 8 / too long, misaligned rows or strides
+    assert lib.xv_rmsnorm(A, 4096, 0, A, A, 4, 1, 4100, C.c_float(1e-6), s) == INVALID
+    assert lib.xv_rmsnorm(A, 4096, 0, A, A, 4, 1, 32768, C.c_float(1e-6), s) == INVALID
+    assert lib.xv_rmsnorm(U, 4096, 0, A, A, 4, 1, 4096, C.c_float(1e-6), s) == INVALID
+    assert lib.xv_fused_add_rmsnorm(A, 4100, A, 4096, A, 4, 4096, C.c_float(1e-6), s) == INVALID
+    assert lib.xv_fused_add_rmsnorm(A, 4096, U, 4096, A, 4, 4096, C.c_float(1e-6), s) == INVALID
+    # RoPE: head_dim other than 128, misaligned q
+    assert lib.xv_rotary_embedding(A, 4096, 128, A, 1024, 128, A, A, A, A, 4, 32, 8, 64, s) == INVALID
+    assert lib.xv_rotary_embedding(U, 4096, 128, A, 1024, 128, A, A, A, A, 4, 32, 8, 128, s) == INVALID
+    assert lib.xv_qk_norm_rope(A, 4096, 130, A, 1024, 128, A, A, C.c_float(1e-6), A, A, A, A, 4, 32, 8, 128,
+                               s) == INVALID
+    # SiLU-and-mul: inter_size not a multiple of 8, misaligned output
+    assert lib.xv_silu_and_mul(A, 24576, A, 12288, 4, 12290, s) == INVALID
+    assert lib.xv_silu_and_mul(A, 24576, U, 12288, 4, 12288, s) == INVALID
+    # sampler: bad sizes, sampled rows without temperatures
+    assert lib.xv_sample(A, 100, 4, 200, A, None, None, None, None, 0, A, None, 0, s) == INVALID
+    assert lib.xv_sample(A, 151936, 4, 151936, None, None, None, None, None, 0, A, None, 0, s) == INVALID
+    assert lib.xv_sample(A, 151936, 4, 0, A, None, None, None, None, 0, A, None, 0, s) == INVALID
+
+
+def test_workspace_sizes(lib):
+    ws = lambda b, hq, hkv, maxb: lib.xv_paged_decode_workspace_size(b, hq, hkv, maxb, 16, 128)
+    # the partial budget keeps every batch within ~32 MB of partials plus counters
+    for b in (1, 8, 64, 256, 300, 1000):
+        for maxb in (1, 128, 2048, 8192):
+            assert 256 <= ws(b, 32, 8, maxb) <= (33 << 20), (b, maxb)
+    assert ws(0, 32, 8, 128) == 256
+    # one long sequence: up to 129 partials per head
+    assert ws(1, 32, 8, 8192) >= 32 * 129 * 129 * 4
+    sw = lambda b, v: lib.xv_sampler_workspace_size(b, v)
+    assert sw(0, 151936) == 256 and sw(64, 151936) % 256 == 0
+    assert sw(64, 151936) >= 64 * 8192 * 8  # the per-row candidate lists
+    assert sw(256, 151936) >= sw(64, 151936)

@@ -714,6 +714,7 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
       (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
     return (int)hipErrorInvalidValue;
+  if ((uintptr_t)out & 3 || out_stride_tok & 1) return (int)hipErrorInvalidValue;  // bf16 pairs stored as 4 bytes
   const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_blocks_per_seq);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
   DecodeArgs a;

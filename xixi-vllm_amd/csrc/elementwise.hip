@@ -66,6 +66,11 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
                                 int num_kv_heads, int head_dim, hipStream_t stream) {
   if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || block_size <= 0)
     return (int)hipErrorInvalidValue;
+  if (!xv_al16(key) || !xv_al16(value) || !xv_al16(k_cache) || !xv_al16(v_cache) ||
+      !xv_st8(key_stride_tok) || !xv_st8(key_stride_head) || !xv_st8(value_stride_tok) ||
+      !xv_st8(value_stride_head) || !xv_st8(cache_page_stride) || !xv_st8(cache_tok_stride) ||
+      !xv_st8(cache_head_stride))
+    return (int)hipErrorInvalidValue;  // 16-byte chunks
   if (num_tokens == 0) return 0;
   const int cph = head_dim / 8;
   const int cpt = cph * num_kv_heads;
@@ -272,6 +277,8 @@ extern "C" int xv_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_strid
                           const void* weight, void* out, int64_t n_outer, int64_t n_inner,
                           int hidden, float eps, hipStream_t stream) {
   if (n_outer < 0 || n_inner < 0) return (int)hipErrorInvalidValue;
+  if (!xv_al16(x) || !xv_al16(weight) || !xv_al16(out) || !xv_st8(x_stride_outer) || !xv_st8(x_stride_inner))
+    return (int)hipErrorInvalidValue;
   return dispatch_norm<RmsLaunch>(n_outer * n_inner, hidden, stream, (const bf16_t*)x, x_stride_outer,
                                   x_stride_inner, (const bf16_t*)weight, (bf16_t*)out, n_outer, n_inner,
                                   hidden, eps);
@@ -281,6 +288,8 @@ extern "C" int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, i
                                     const void* weight, int64_t rows, int hidden, float eps,
                                     hipStream_t stream) {
   if (rows < 0) return (int)hipErrorInvalidValue;
+  if (!xv_al16(x) || !xv_al16(residual) || !xv_al16(weight) || !xv_st8(x_stride) || !xv_st8(residual_stride))
+    return (int)hipErrorInvalidValue;
   return dispatch_norm<AddRmsLaunch>(rows, hidden, stream, (bf16_t*)x, x_stride, (bf16_t*)residual,
                                      residual_stride, (const bf16_t*)weight, hidden, eps);
 }
@@ -401,6 +410,13 @@ static int launch_rope_t(const void* q, int64_t qst, int64_t qsh, const void* k,
                          const void* qw, const void* kw, float eps, const int64_t* positions, const float* cs,
                          void* q_out, void* k_out, int64_t T, int hq, int hkv, const CacheDst& cd,
                          hipStream_t stream) {
+  // rows and weights move as 16-byte vectors, the fp32 table as float4
+  if (!xv_al16(q) || !xv_al16(k) || !xv_al16(qw) || !xv_al16(kw) || !xv_al16(cs) || !xv_al16(q_out) ||
+      !xv_al16(k_out) || !xv_st8(qst) || !xv_st8(qsh) || !xv_st8(kst) || !xv_st8(ksh))
+    return (int)hipErrorInvalidValue;
+  if (STORE && (!xv_al16(cd.kc) || !xv_al16(cd.vc) || !xv_al16(cd.v) || !xv_st8(cd.ps) || !xv_st8(cd.ts) ||
+                !xv_st8(cd.hs) || !xv_st8(cd.vs_tok) || !xv_st8(cd.vs_head)))
+    return (int)hipErrorInvalidValue;
   const unsigned blocks = (unsigned)((T * kRopeRows + 15) / 16);
   rope_kernel<NORM, STORE><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
                                                        (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
@@ -486,6 +502,7 @@ __global__ __launch_bounds__(256) void silu_and_mul_kernel(const bf16_t* __restr
 extern "C" int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stride,
                                int64_t num_tokens, int inter_size, hipStream_t stream) {
   if (num_tokens < 0 || inter_size <= 0 || inter_size % 8) return (int)hipErrorInvalidValue;
+  if (!xv_al16(x) || !xv_al16(out) || !xv_st8(x_stride) || !xv_st8(out_stride)) return (int)hipErrorInvalidValue;
   if (num_tokens == 0) return 0;
   int vpr = inter_size / 8;
   int64_t total = num_tokens * vpr;

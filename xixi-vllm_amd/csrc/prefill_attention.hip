@@ -434,6 +434,9 @@ extern "C" int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
     if (!k || !v) return (int)hipErrorInvalidValue;
     if (((uintptr_t)k | (uintptr_t)v) & 15 || (kv_stride_tok | kv_stride_head) & 7) return (int)hipErrorInvalidValue;
   }
+  // q rows are read as 16-byte vectors, out is written as 8-byte pieces
+  if ((uintptr_t)q & 15 || (q_stride_tok | q_stride_head) & 7 || (uintptr_t)out & 7 || out_stride_tok & 3)
+    return (int)hipErrorInvalidValue;
   if (batch == 0 || max_seqlen_q == 0) return 0;
   PrefillArgs a;
   a.q = (const bf16_t*)q; a.q_st = q_stride_tok; a.q_sh = q_stride_head;

@@ -6,6 +6,11 @@
 
 #define XV_INLINE __device__ __forceinline__
 
+// Host-side layout checks of the 16-byte vector paths: a 16-byte aligned base
+// (null allowed: unused operand) and strides in whole 8-element (16-byte) units.
+static inline bool xv_al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+static inline bool xv_st8(int64_t s) { return (s & 7) == 0; }
+
 typedef uint16_t bf16_t;  // raw bf16 bits as stored in HBM
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
