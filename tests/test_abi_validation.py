@@ -94,3 +94,16 @@ def test_workspace_sizes(lib):
     assert sw(0, 151936) == 256 and sw(64, 151936) % 256 == 0
     assert sw(64, 151936) >= 64 * 8192 * 8  # the per-row candidate lists
     assert sw(256, 151936) >= sw(64, 151936)
+
+
+def test_decode_workspace_never_shrinks_with_batch(lib):
+    """Decode graphs are captured largest bucket first on one shared workspace:
+    a smaller bucket must never need more (a regrown workspace would leave the
+    earlier graphs replaying onto freed memory)."""
+    for hq, hkv in ((32, 8), (16, 8), (64, 8), (8, 8)):
+        for maxb in (1, 8, 128, 256, 296, 2048, 8192):
+            prev = 0
+            for b in range(1, 300):
+                cur = lib.xv_paged_decode_workspace_size(b, hq, hkv, maxb, 16, 128)
+                assert cur >= prev, (hq, hkv, maxb, b)
+                prev = cur

@@ -531,3 +531,41 @@ def test_greedy_multi_workgroup_bitexact(dev, b, v):
         got = sample(xs.to(dev), None, all_greedy=True)
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy(), want), f"call {call}: {got.cpu().numpy()[:8]} vs {want[:8]}"
+
+
+def test_decode_graphs_largest_first_share_one_workspace(dev):
+    """Decode-attention graphs captured for buckets 256 .. 1 (largest first, as
+    the graph runner does) on the shared workspace, then replayed in mixed
+    order with eager calls between: every replay equals the eager result, and
+    no capture regrew the workspace (a regrown one would leave the earlier
+    graphs replaying onto freed memory)."""
+    import xvllm.layers.attention as A
+    from xvllm.layers.attention import paged_decode_attention
+
+    g = torch.Generator(device=dev).manual_seed(11)
+    hq, hkv, d, maxb = 32, 8, 128, 256
+    pool = 2048
+    kc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    vc = torch.randn((pool, 16, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    buckets = [256, 240, 128, 96, 64, 1]
+    ctx = torch.randint(1, 16 * 8, (256,), generator=torch.Generator().manual_seed(12)).to(torch.int32).to(dev)
+    bt = torch.randint(0, pool, (256, maxb), generator=g, device=dev).to(torch.int32)
+    q = torch.randn((256, hq * d), generator=g, device=dev).to(torch.bfloat16)
+    outs, graphs = {}, {}
+    first_ws = None
+    for bs in buckets:
+        out = torch.empty((bs, hq * d), dtype=torch.bfloat16, device=dev)
+        paged_decode_attention(q[:bs], kc, vc, bt[:bs], ctx[:bs], hq, hkv, d, out=out)  # warm-up, sizes the workspace
+        torch.cuda.synchronize()
+        ws = A._WORKSPACE[(dev.type, dev.index)]
+        first_ws = first_ws if first_ws is not None else ws.data_ptr()
+        assert ws.data_ptr() == first_ws, f"workspace regrown at bucket {bs}"
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            paged_decode_attention(q[:bs], kc, vc, bt[:bs], ctx[:bs], hq, hkv, d, out=out)
+        outs[bs], graphs[bs] = out, gr
+    for bs in [256, 1, 240, 64, 256, 96, 128, 256]:
+        want = paged_decode_attention(q[:bs], kc, vc, bt[:bs], ctx[:bs], hq, hkv, d)
+        graphs[bs].replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs[bs], want), f"replay of bucket {bs}"

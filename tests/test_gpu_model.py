@@ -158,3 +158,72 @@ def test_decode_graph_replay_matches_eager(dev):
         assert torch.equal(g_hidden, e_hidden), f"step {step}: graph replay differs from eager"
         assert torch.isfinite(g_hidden.float()).all()
     runner.destroy()
+
+
+def test_serving_loop_reads_back_the_sampled_ids(dev):
+    """A few continuous-batching steps of a 2-layer random Qwen3-shaped model
+    (prefill chunks, then decode rows with a prefill in the same step): every
+    id read back on the host equals the id sampled on the device in that step,
+    and decode steps feed them back as input.  Regression: the side-stream D2H
+    copy of the ids must be ordered after their join on the compute stream."""
+    from xvllm.batch import SeqSchedule
+    from xvllm.config import Qwen3Shape
+    from xvllm.kv_pool import KVPool
+    from xvllm.model_runner import ModelRunner
+    from xvllm.models import Qwen3ForCausalLM
+
+    V = 4096
+    cfg = Qwen3Shape(HIDDEN, HQ, HKV, D, FFN, 2, vocab_size=V, max_position_embeddings=4096)
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(dev):
+            model = Qwen3ForCausalLM(cfg).random_init_(seed=3)
+            kv = KVPool(cfg, num_blocks=512, block_size=16, device=dev, dtype=torch.bfloat16)
+    finally:
+        torch.set_default_dtype(torch.float32)
+    runner = ModelRunner(model, kv, max_num_seqs=32, max_num_batched_tokens=2048, context_len=1024, device=dev)
+    staged = {}
+    orig = runner._stage_samples
+
+    def spy(p, d):  # keep the device-side ids of the step
+        staged["p"] = None if p is None else p.clone()
+        staged["d"] = None if d is None else d.clone()
+        return orig(p, d)
+
+    runner._stage_samples = spy
+    g = gen(9)
+    free = list(range(512))
+    seqs = []
+    for i in range(12):
+        n = int(torch.randint(20, 120, (1,), generator=g))
+        seqs.append(dict(id=i, toks=torch.randint(0, V, (n,), generator=g).tolist(), cached=0, bt=[]))
+    busy = torch.randn(4096, 4096, device=dev)
+    for step in range(12):
+        decodes, prefills = [], []
+        for s in seqs:
+            if s["cached"] >= len(s["toks"]) - 1 and s["cached"] > 0:  # prompt done: decode the last token
+                if (s["cached"] + 1 + 15) // 16 > len(s["bt"]):
+                    s["bt"].append(free.pop())
+                decodes.append(SeqSchedule(s["id"], [s["toks"][-1]], s["cached"], list(s["bt"])))
+        for s in seqs[: 4 + step]:
+            if s["cached"] == 0:  # whole prompt as one prefill chunk
+                s["bt"] = [free.pop() for _ in range((len(s["toks"]) + 15) // 16)]
+                prefills.append(SeqSchedule(s["id"], s["toks"], 0, list(s["bt"])))
+        for _ in range(6):  # a busy compute stream makes a misordered copy visible
+            busy = busy @ busy * 1e-3
+        n_p, n_d = runner.run_forward(decodes, prefills)
+        p_ids, d_ids = runner.read_samples(n_p, n_d)
+        torch.cuda.synchronize()
+        want_d = [] if staged["d"] is None else staged["d"].view(-1).tolist()
+        want_p = [] if staged["p"] is None else staged["p"].view(-1).tolist()
+        assert d_ids == want_d and p_ids == want_p, f"step {step}"
+        assert all(0 <= t < V for t in d_ids + p_ids)
+        for s, t in zip(decodes, d_ids):
+            rec = seqs[s.seq_id]
+            rec["cached"] += 1
+            rec["toks"].append(t)
+        for s, t in zip(prefills, p_ids):
+            rec = seqs[s.seq_id]
+            rec["cached"] = len(rec["toks"])
+            rec["toks"].append(t)
+    runner.destroy()

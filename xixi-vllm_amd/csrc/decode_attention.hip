@@ -668,15 +668,21 @@ size_t chunk_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int m
   return counter_bytes(batch, num_kv_heads) + (size_t)batch * num_q_heads * parts * ((size_t)kD + 1) * sizeof(float);
 }
 
+// The largest one-launch workspace over every batch up to `batch` (launches
+// take at most kMaxBatch sequences).  The need of a single batch size is not
+// monotone (the partial budget lets small batches keep more partials), so the
+// query takes the maximum: the result never decreases with the batch, and a
+// workspace sized for the largest batch serves every smaller one.  Callers that
+// capture graphs for several batch sizes rely on this: their workspace is
+// allocated once, before the first (largest) capture.
 extern "C" size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int max_blocks_per_seq, int block_size, int head_dim) {
   (void)block_size;
   (void)head_dim;
   if (batch <= 0 || max_blocks_per_seq <= 0 || num_kv_heads <= 0) return 256;
-  // batches above kMaxBatch run in chunks of kMaxBatch and one remainder
-  size_t need = chunk_workspace_bytes(min(batch, kMaxBatch), num_q_heads, num_kv_heads, max_blocks_per_seq);
-  if (batch > kMaxBatch && batch % kMaxBatch)
-    need = max(need, chunk_workspace_bytes(batch % kMaxBatch, num_q_heads, num_kv_heads, max_blocks_per_seq));
+  size_t need = 256;
+  for (int b = 1; b <= min(batch, kMaxBatch); ++b)
+    need = max(need, chunk_workspace_bytes(b, num_q_heads, num_kv_heads, max_blocks_per_seq));
   return need;
 }
 
