@@ -209,6 +209,9 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  *   calls and calls of up to 128 rows spread each row over several workgroups
  *   (larger sampled batches take one workgroup per row, which fills the
  *   device); NULL selects one workgroup per row.  Both give identical ids.
+ *   The size never decreases with B, and a workspace sized for B rows serves
+ *   every later call of up to B rows, greedy or sampled, in any order (the
+ *   greedy counters sit at the bottom, the sampled path's data at the top).
  *   Calls sharing a workspace must be ordered on one stream.
  */
 #define XV_SAMPLE_ALL_GREEDY 1

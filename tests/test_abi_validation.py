@@ -107,3 +107,12 @@ def test_decode_workspace_never_shrinks_with_batch(lib):
                 cur = lib.xv_paged_decode_workspace_size(b, hq, hkv, maxb, 16, 128)
                 assert cur >= prev, (hq, hkv, maxb, b)
                 prev = cur
+
+
+def test_sampler_workspace_never_shrinks_with_batch(lib):
+    for v in (1003, 32000, 151936):
+        prev = 0
+        for b in range(1, 300):
+            cur = lib.xv_sampler_workspace_size(b, v)
+            assert cur >= prev and cur >= b * 128, (v, b)
+            prev = cur

@@ -569,3 +569,42 @@ def test_decode_graphs_largest_first_share_one_workspace(dev):
         graphs[bs].replay()
         torch.cuda.synchronize()
         assert torch.equal(outs[bs], want), f"replay of bucket {bs}"
+
+
+def test_sampler_one_workspace_sampled_and_greedy_calls_interleaved(dev):
+    """One workspace sized for 64 rows serves sampled calls (multi-workgroup
+    path, which writes the top of the workspace) and all-greedy calls (whose
+    per-row lines at the bottom must be zero) in any order and batch size:
+    greedy ids equal the argmax (lowest id on ties), sampled ids equal the
+    one-workgroup path's."""
+    from xvllm import _C
+    from xvllm._torch_glue import ptr, stream_of
+    from xvllm.sampler import sample
+
+    L = _C.lib()
+    V = 151936
+    ws = torch.zeros(L.xv_sampler_workspace_size(64, V), dtype=torch.uint8, device=dev)
+    g = gen(321)
+
+    def call(logits, flags, temps=None, tps=None, tks=None, u=None):
+        out = torch.empty(logits.shape[0], dtype=torch.int64, device=dev)
+        rc = L.xv_sample(ptr(logits), logits.stride(0), logits.shape[0], V, ptr(temps), ptr(tps), ptr(tks), None,
+                         ptr(u), flags, ptr(out), ptr(ws), ws.numel(), stream_of(logits))
+        assert rc == 0
+        return out
+
+    for bs, kind in [(8, "sampled"), (64, "greedy"), (32, "sampled"), (48, "greedy"), (64, "sampled"), (64, "greedy")]:
+        logits = _sampler_case(g, bs, V, std=1.0).to(dev)
+        if kind == "greedy":
+            got = call(logits, _C.XV_SAMPLE_ALL_GREEDY)
+            x = logits.float()
+            want = (x == x.max(dim=1, keepdim=True).values).float().argmax(dim=1)  # lowest id holding the max
+        else:
+            temps = torch.full((bs,), 0.7, device=dev)
+            tps = torch.full((bs,), 0.9, device=dev)
+            tks = torch.full((bs,), 50, dtype=torch.int32, device=dev)
+            u = torch.rand(bs, generator=g).to(dev)
+            got = call(logits, _C.XV_SAMPLE_USE_TOP_K | _C.XV_SAMPLE_USE_TOP_P, temps, tps, tks, u)
+            want = sample(logits, temps, tps, tks, None, u, use_top_k=True, use_top_p=True, multi_workgroup=False)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (bs, kind)

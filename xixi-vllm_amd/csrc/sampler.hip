@@ -1753,7 +1753,7 @@ SegLayout seg_layout(int batch, int vocab) {
   L.seg_len = ((vocab + segs - 1) / segs + 7) / 8 * 8;
   L.R = (vocab + L.seg_len - 1) / L.seg_len;
   const size_t B = (size_t)max(batch, 0), BR = B * L.R;
-  size_t o = align256(B * kGreedyLine * 8);
+  size_t o = 0;  // offsets within the sampled path's region
   L.plans = o; o = align256(o + B * sizeof(RowPlan));
   L.kmax = o;  o = align256(o + BR * 4);
   L.kmin = o;  o = align256(o + BR * 4);
@@ -1766,11 +1766,26 @@ SegLayout seg_layout(int batch, int vocab) {
   L.total = o;
   return L;
 }
+
+// The greedy path's per-row lines, which must be zero before a call.
+size_t greedy_bytes(int batch) { return align256((size_t)max(batch, 0) * kGreedyLine * 8); }
+// The largest sampled-path region of any batch up to `batch`.
+size_t seg_reserve(int batch, int vocab) {
+  size_t r = 0;
+  for (int b = 1; b <= min(batch, kSegMaxBatch); ++b) r = max(r, seg_layout(b, vocab).total);
+  return r;
+}
 }  // namespace
 
+// Workspace: the greedy lines at the bottom, the sampled path's region at the
+// top (it ends at workspace_bytes).  A workspace of this size for B rows
+// serves every call of up to B rows, greedy or sampled, in any order: the
+// greedy lines [0, Bg * 128) of a call and the region a sampled call of Bs
+// rows wrote at the top never overlap, since the size reserves both the lines
+// of Bg rows and the largest region of any Bs <= B.
 extern "C" size_t xv_sampler_workspace_size(int batch, int vocab) {
   if (batch <= 0 || vocab <= 0) return 256;
-  return seg_layout(batch, vocab).total;
+  return greedy_bytes(batch) + seg_reserve(batch, vocab);
 }
 
 extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
@@ -1800,7 +1815,7 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
   // reads each row fewer times.
   if (workspace != nullptr && batch <= kSegMaxBatch && workspace_bytes >= xv_sampler_workspace_size(batch, vocab)) {
     const SegLayout L = seg_layout(batch, vocab);
-    char* w = (char*)workspace;
+    char* w = (char*)workspace + ((workspace_bytes - L.total) & ~(size_t)255);  // region at the top
     SegArgs a;
     a.logits = (const bf16_t*)logits; a.stride = logits_stride;
     a.V = vocab; a.R = L.R; a.seg_len = L.seg_len; a.flags = flags & ~XV_SAMPLE_ALL_GREEDY;
