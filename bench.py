@@ -30,7 +30,7 @@ sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
-# 2 x 319061.4 KiB read (FETCH_SIZE counts half on this part) + 3225.3 KiB written.
+# 2 x 318995.4 KiB read (FETCH_SIZE counts half on this part) + 3225.2 KiB written.
 MEASURED_TRAFFIC_BYTES = int((2 * 318995.4 + 3225.2) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
