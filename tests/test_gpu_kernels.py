@@ -608,3 +608,41 @@ def test_sampler_one_workspace_sampled_and_greedy_calls_interleaved(dev):
             want = sample(logits, temps, tps, tks, None, u, use_top_k=True, use_top_p=True, multi_workgroup=False)
         torch.cuda.synchronize()
         assert torch.equal(got, want), (bs, kind)
+
+
+def test_sampler_randomized_configurations_bitexact(dev):
+    """40 seeded random configurations (batch 1-40, vocabularies 1003 / 4099 /
+    32000 / 151936, any mix of top-k / top-p / min-p, temperatures with some
+    greedy rows, logits from narrow to wide, coarse ties, massive ties and a
+    sprinkle of NaN): both paths equal the C oracle on every row."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    rng = np.random.default_rng(2024)
+    for case in range(40):
+        b = int(rng.integers(1, 41))
+        v = int(rng.choice([1003, 4099, 32000, 151936]))
+        flags = int(rng.choice([0, 2, 4, 8, 2 | 4, 4 | 8, 2 | 8, 2 | 4 | 8]))
+        kind = rng.choice(["narrow", "normal", "wide", "ties", "massive"])
+        std = {"narrow": 0.02, "normal": 1.0, "wide": 4.0, "ties": 1.0, "massive": 1.0}[kind]
+        x = rng.standard_normal((b, v)).astype(np.float32) * std
+        if kind == "ties":
+            x = np.round(x * 4) / 4
+        if kind == "massive":
+            x = np.round(x) / 2
+        if rng.random() < 0.2:
+            x[rng.random((b, v)) < 0.001] = np.nan
+        logits = torch.from_numpy(x).to(torch.bfloat16)
+        temps = torch.from_numpy(rng.uniform(0.3, 1.5, b).astype(np.float32))
+        temps[torch.from_numpy(rng.random(b) < 0.2)] = 0.0  # some greedy rows
+        tps = torch.from_numpy(rng.uniform(0.3, 0.99, b).astype(np.float32))
+        tks = torch.from_numpy(rng.integers(1, min(v, 3000), b).astype(np.int32))
+        mps = torch.from_numpy(rng.uniform(0.0, 0.3, b).astype(np.float32))
+        u = torch.from_numpy(rng.random(b).astype(np.float32))
+        want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                        mps.numpy(), u.numpy(), flags)
+        args = (logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev))
+        kw = dict(use_top_k=bool(flags & 2), use_top_p=bool(flags & 4), use_min_p=bool(flags & 8))
+        for mw in (True, False):
+            got = sample(*args, **kw, multi_workgroup=mw).cpu().numpy()
+            assert np.array_equal(got, want), (case, b, v, flags, kind, mw)
