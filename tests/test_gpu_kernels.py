@@ -24,7 +24,10 @@ def _close(got, want, rtol=RTOL, atol=ATOL):
     assert (err <= 0).all(), f"max excess {err.max():.4g} at {np.unravel_index(err.argmax(), err.shape)}"
 
 
-@pytest.mark.parametrize("n,hkv,d,strided", [(37, 8, 128, False), (64, 8, 128, True), (5, 2, 64, False)])
+@pytest.mark.parametrize(
+    "n,hkv,d,strided",
+    [(37, 8, 128, False), (64, 8, 128, True), (5, 2, 64, False), (7, 4, 128, False), (1, 8, 128, True)],
+)
 def test_store_kvcache_bitexact(dev, n, hkv, d, strided):
     from xvllm.kv_ops import store_kvcache
 
