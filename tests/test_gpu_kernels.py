@@ -284,6 +284,9 @@ def test_silu_and_mul(dev, t, inter):
         (32, 8, [777, 64], [777, 64], False),                   # long prompt: many tiles, odd tail
         (32, 8, [300, 129], [2100, 1129], True),                # long chunks over long cached prefixes
         (16, 8, [161], [1000], True),                           # group 2, 64-query blocks
+        (32, 8, [64, 64, 1, 64, 0, 64], [64, 64, 1, 64, 0, 64], False),  # equal work: tie order
+        (32, 8, [50, 20, 50, 20], [80, 20, 80, 50], True),      # mixed work with ties
+        (32, 8, [5, 3] * 35, [5, 3] * 35, False),               # 70 sequences: batch above 64
     ],
 )
 def test_prefill_attention(dev, hq, hkv, qlens, klens, paged):

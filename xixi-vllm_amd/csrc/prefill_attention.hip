@@ -50,7 +50,7 @@ struct PrefillArgs {
   const int32_t* bt; int64_t bt_stride;
   const int32_t* cu_q; const int32_t* cu_k;
   bf16_t* out; int64_t out_st;
-  int hq, hkv, qblocks;
+  int hq, hkv, qblocks, batch;
   float scale_log2;
 };
 
@@ -213,6 +213,31 @@ XV_INLINE bf16x8_t vt_operand(const short4_t (&t)[16], int n, int j) {
   return r;
 }
 
+// Sequence of dispatch slot j: sequences in descending causal work
+// q_len * (k_len - q_len) + q_len * (q_len + 1) / 2 (ties: lower index
+// first), so the costliest sequences' blocks are dispatched first and the
+// cheapest ones finish the grid.  Each sequence's blocks stay together in the
+// dispatch order (they share K/V tiles in L2).  Batches above 64 keep their
+// own order.
+XV_INLINE int seq_by_work(const int* cu_q, const int* cu_k, int batch, int j) {
+  if (batch > 64) return j;
+  const int lane = threadIdx.x & 63;
+  int64_t w = -1;
+  if (lane < batch) {
+    const int ql = cu_q[lane + 1] - cu_q[lane], kl = cu_k[lane + 1] - cu_k[lane];
+    w = (int64_t)ql * (kl - ql) + (int64_t)ql * (ql + 1) / 2;
+  }
+  int pos = 0;
+  for (int t = 0; t < batch; ++t) {
+    const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)w, t);
+    const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)((uint64_t)w >> 32), t);
+    const int64_t wt = (int64_t)(((uint64_t)hi << 32) | lo);
+    pos += (wt > w || (wt == w && t < lane)) ? 1 : 0;
+  }
+  const uint64_t m = __ballot(lane < batch && pos == j);
+  return __builtin_amdgcn_readfirstlane(__builtin_ctzll(m));
+}
+
 template <int G, bool PAGED>
 __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   constexpr int GW = G < 4 ? G : 4;   // query heads per workgroup
@@ -225,7 +250,8 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   // XCD-aware order: workgroups go round-robin to the 8 XCDs, so with the head
   // slot fastest every XCD serves the same kv head(s) and keeps their K/V tiles
   // in its own L2; each head carries the same work, which balances the XCDs.
-  const int hsel = blockIdx.x, rank = blockIdx.y, b = blockIdx.z;
+  const int hsel = blockIdx.x, rank = blockIdx.y;
+  const int b = seq_by_work(a.cu_q, a.cu_k, a.batch, blockIdx.z);
   // group 8: two slots per kv head (query heads 0-3 and 4-7), slot = half * Hkv
   // + kvh, so both halves of a kv head land on the same XCD
   const int kvh = G == 8 ? hsel % a.hkv : hsel;
@@ -446,7 +472,7 @@ extern "C" int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   a.bt = block_tables; a.bt_stride = bt_stride;
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k;
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
-  a.hq = num_q_heads; a.hkv = num_kv_heads;
+  a.hq = num_q_heads; a.hkv = num_kv_heads; a.batch = batch;
   a.scale_log2 = scale * 1.4426950408889634f;
   const int gw = group < 4 ? group : 4;
   const int block_q = 32 * (4 / gw);
