@@ -447,6 +447,31 @@ def test_qk_norm_rope_store_matches_separate_ops(dev, hnd):
     assert torch.equal(kc2, kc1) and torch.equal(vc2, vc1)
 
 
+def test_paged_decode_merge_ignores_stale_workspace(dev):
+    """The merge reads the first partial rows of a head speculatively; rows
+    past the head's partial count hold whatever an earlier call left, here
+    NaN bit patterns (0xFF bytes) in the whole workspace.  Batches whose
+    sequences split into 1 to 6 partials must still be finite and correct."""
+    from xvllm.layers.attention import decode_workspace, paged_decode_attention
+
+    g = gen(93)
+    for bsz, lo, hi in [(4, 2000, 4097), (16, 300, 4097), (64, 512, 4097)]:
+        ctx = torch.randint(lo, hi, (bsz,), generator=g).tolist()
+        need = sum((c + 15) // 16 for c in ctx)
+        kc, vc, bt, sl = make_paged(ctx, int(need * 1.25) + 4, 8, 128, g)
+        q = randn_bf16((bsz, 32, 128), g)
+        args = (q.view(bsz, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), 32, 8, 128)
+        paged_decode_attention(*args)  # sizes the workspace
+        decode_workspace(dev, 1).fill_(255)
+        out = paged_decode_attention(*args)
+        torch.cuda.synchronize()
+        print(f"stale workspace: B {bsz} ctx [{lo},{hi})", flush=True)
+        assert torch.isfinite(out.float()).all()
+        rows = list(range(0, bsz, max(1, bsz // 8)))
+        want = O.paged_decode_attention(f32(q)[rows], f32(kc), f32(vc), bt.numpy()[rows], sl.numpy()[rows])
+        _close(f32(out).reshape(bsz, 32, 128)[rows], want)
+
+
 def test_paged_decode_workspace_reuse_across_batches(dev):
     """Calls of different batch sizes share the per-device workspace: split
     partials of one call must never be taken for the arrival counters of the

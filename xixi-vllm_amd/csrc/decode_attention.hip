@@ -538,13 +538,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
 // Merge the partials of one (sequence, query head) with one wave.  Also
 // writes the zero output of padding rows (cache_seqlens 0).  The partial
 // count comes from the main kernel.  The count, the sequence length, the
-// first two partials (the common split, 2 dims per lane) and the
-// log2-sum-exp of partial `lane` are loaded together, so a two-way merge costs
-// one memory round trip.  More partials: lane j holds partial j's weight
+// first kFastParts partials (the common splits, 2 dims per lane) and the
+// log2-sum-exp of partial `lane` are loaded together, so a merge of up to
+// kFastParts partials costs one memory round trip.  More partials: lane j holds partial j's weight
 // (j < 64, then j - 64, j - 128 in two more registers); four groups of 16
 // lanes take every fourth partial, 8 dims per lane, eight partials per batch
 // of loads, and the groups are summed by lane swaps.
 constexpr int kMergeMaxParts = 192;
+constexpr int kFastParts = 4;  // partial counts merged from the first memory round trip
 __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int b = blockIdx.x / a.hq;
   const int h = blockIdx.x - b * a.hq;
@@ -553,10 +554,16 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
   const int ctx = a.seqlens[b];
   const int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
-  // speculative: rows 0 and 1 exist in every workspace (max_parts >= 2), rows < max_parts too
-  const float l0 = a.ws_lse[row0], l1 = a.ws_lse[row0 + 1];
-  const float2 v0 = *reinterpret_cast<const float2*>(a.ws_o + row0 * kD + d);
-  const float2 v1 = *reinterpret_cast<const float2*>(a.ws_o + (row0 + 1) * kD + d);
+  // speculative: the first kFastParts rows (clamped to max_parts - 1: rows
+  // below max_parts exist in every workspace, and max_parts >= 2)
+  float lf[kFastParts];
+  float2 vf[kFastParts];
+#pragma unroll
+  for (int r = 0; r < kFastParts; ++r) {
+    const int64_t row = row0 + min(r, a.max_parts - 1);
+    lf[r] = a.ws_lse[row];
+    vf[r] = *reinterpret_cast<const float2*>(a.ws_o + row * kD + d);
+  }
   const float lmine = lane < a.max_parts ? a.ws_lse[row0 + lane] : -INFINITY;
   bf16_t* orow = a.out + (int64_t)b * a.out_st + (int64_t)h * kD;
   if (ctx <= 0) {
@@ -564,12 +571,21 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
     return;
   }
   if (n <= 1) return;
-  if (n == 2) {
-    const float mx = fmaxf(l0, l1);
-    const float w0 = __builtin_amdgcn_exp2f(l0 - mx), w1 = __builtin_amdgcn_exp2f(l1 - mx);
-    const float inv = 1.0f / (w0 + w1);
-    *reinterpret_cast<uint32_t*>(orow + d) =
-        pack_bf16x2((w0 * v0.x + w1 * v1.x) * inv, (w0 * v0.y + w1 * v1.y) * inv);
+  if (n <= kFastParts) {
+    float mx = lf[0];
+#pragma unroll
+    for (int r = 1; r < kFastParts; ++r) mx = r < n ? fmaxf(mx, lf[r]) : mx;
+    float den = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+    for (int r = 0; r < kFastParts; ++r) {
+      if (r >= n) break;  // rows past n hold stale data (even NaN): never touched
+      const float w = __builtin_amdgcn_exp2f(lf[r] - mx);
+      den += w;
+      ox += w * vf[r].x;
+      oy += w * vf[r].y;
+    }
+    const float inv = 1.0f / den;
+    *reinterpret_cast<uint32_t*>(orow + d) = pack_bf16x2(ox * inv, oy * inv);
     return;
   }
   // weights: lane j holds partials j, 64 + j, 128 + j
