@@ -204,13 +204,12 @@ XV_INLINE void vt_wait_rest(short4_t (&t)[16]) {
                        : "memory");
 }
 // A-operand of d-tile n, key-step KS0 + j from read_vt_ks2's registers
+// (a whole-vector shuffle of the two 64-bit halves: composing it from 16-bit
+// elements leaves a no-op bit-field insert per register in front of the MFMA)
+typedef short short8_t __attribute__((ext_vector_type(8)));
 XV_INLINE bf16x8_t vt_operand(const short4_t (&t)[16], int n, int j) {
-  const short4_t& a = t[4 * n + 2 * j];
-  const short4_t& b = t[4 * n + 2 * j + 1];
-  short tmp[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  bf16x8_t r;
-  __builtin_memcpy(&r, tmp, 16);
-  return r;
+  const short8_t r = __builtin_shufflevector(t[4 * n + 2 * j], t[4 * n + 2 * j + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, r);
 }
 
 // Sequence of dispatch slot j: sequences in descending causal work
