@@ -677,3 +677,94 @@ def test_sampler_randomized_configurations_bitexact(dev):
         for mw in (True, False):
             got = sample(*args, **kw, multi_workgroup=mw).cpu().numpy()
             assert np.array_equal(got, want), (case, b, v, flags, kind, mw)
+
+
+@pytest.mark.parametrize(
+    "name,b,v,flags,top_k,kind",
+    [
+        ("k50_p0.9", 64, 151936, 2 | 4, 50, None),
+        ("k1", 8, 151936, 2, 1, None),
+        ("k64_minp", 16, 151936, 2 | 8, 64, None),
+        ("k20_all", 32, 151936, 2 | 4 | 8, 20, "ties"),
+        ("k64_massive_ties", 8, 151936, 2 | 4, 64, "massive"),
+        ("k40_flat", 8, 151936, 2 | 4, 40, "flat"),
+        ("k7_odd_vocab", 5, 1003, 2 | 4, 7, None),
+        ("k33_vocab_4099", 128, 4099, 2 | 4 | 8, 33, None),
+        ("k64_odd_vocab_b128", 128, 151935, 2 | 4, 64, None),
+    ],
+)
+def test_sampler_topk_path_bitexact(dev, name, b, v, flags, top_k, kind):
+    """The two-launch top-k path (max_top_k <= 64): per-row k in [1, top_k],
+    mixed greedy rows, NaN entries and a row of NaN only, equal to the C
+    oracle; rows outside the bound (k 0 = whole vocabulary, k above 64) are
+    still exact."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(b * 13 + v + top_k)
+    logits = _sampler_case(g, b, v, std=1.0, ties=True if kind == "ties" else (kind or False))
+    if b >= 4:
+        logits[1, ::11] = float("nan")
+        logits[2] = float("nan")
+    temps = torch.rand(b, generator=g) + 0.4
+    temps[::5] = 0.0  # greedy rows
+    tps = torch.rand(b, generator=g) * 0.6 + 0.35
+    tks = torch.randint(1, top_k + 1, (b,), generator=g, dtype=torch.int32)
+    tks[0] = top_k
+    mps = torch.rand(b, generator=g) * 0.2
+    u = torch.rand(b, generator=g)
+    u[0] = 0.0
+    kw = dict(use_top_k=True, use_top_p=bool(flags & 4), use_min_p=bool(flags & 8))
+    want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                    mps.numpy(), u.numpy(), flags)
+    got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev), **kw,
+                 max_top_k=top_k)
+    torch.cuda.synchronize()
+    print(f"top-k path {name}", flush=True)
+    assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
+    # the flag is a claim about every row: rows that break it are still sampled exactly
+    if b >= 3:
+        tks2 = tks.clone()
+        tks2[1] = 0
+        tks2[2 % b] = 100
+        want2 = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks2.numpy(),
+                         mps.numpy(), u.numpy(), flags)
+        got2 = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks2.to(dev), mps.to(dev), u.to(dev), **kw,
+                      max_top_k=top_k)
+        assert np.array_equal(got2.cpu().numpy(), want2), f"{got2.cpu().numpy()} vs {want2}"
+
+
+def test_sampler_topk_path_randomized_bitexact(dev):
+    """30 seeded random top-k configurations with every k in [1, 64]: the
+    top-k path equals the C oracle on every row."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    rng = np.random.default_rng(77)
+    for case in range(30):
+        b = int(rng.integers(1, 129))
+        v = int(rng.choice([1003, 4099, 32000, 151936]))
+        flags = 2 | int(rng.choice([0, 4, 8, 4 | 8]))
+        kind = rng.choice(["narrow", "normal", "wide", "ties", "massive"])
+        std = {"narrow": 0.02, "normal": 1.0, "wide": 4.0, "ties": 1.0, "massive": 1.0}[kind]
+        x = rng.standard_normal((b, v)).astype(np.float32) * std
+        if kind == "ties":
+            x = np.round(x * 4) / 4
+        if kind == "massive":
+            x = np.round(x) / 2
+        if rng.random() < 0.2:
+            x[rng.random((b, v)) < 0.001] = np.nan
+        logits = torch.from_numpy(x).to(torch.bfloat16)
+        temps = torch.from_numpy(rng.uniform(0.3, 1.5, b).astype(np.float32))
+        temps[torch.from_numpy(rng.random(b) < 0.2)] = 0.0
+        tps = torch.from_numpy(rng.uniform(0.3, 0.99, b).astype(np.float32))
+        kmax = int(rng.integers(1, 65))
+        tks = torch.from_numpy(rng.integers(1, kmax + 1, b).astype(np.int32))
+        mps = torch.from_numpy(rng.uniform(0.0, 0.3, b).astype(np.float32))
+        u = torch.from_numpy(rng.random(b).astype(np.float32))
+        want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                        mps.numpy(), u.numpy(), flags)
+        got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev),
+                     use_top_k=True, use_top_p=bool(flags & 4), use_min_p=bool(flags & 8),
+                     max_top_k=int(tks.max())).cpu().numpy()
+        assert np.array_equal(got, want), (case, b, v, flags, kind, kmax)

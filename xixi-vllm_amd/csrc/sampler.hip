@@ -1,9 +1,11 @@
 // Vocab-wide sampler for gfx950: greedy argmax, temperature / top-k / top-p /
-// min-p with an explicit uniform per row.  Three launch shapes share the
+// min-p with an explicit uniform per row.  Four launch shapes share the
 // arithmetic below: one 1024-thread workgroup per row (sample_kernel), the
 // all-greedy argmax over several workgroups per row (greedy_segment_kernel),
-// and the sampled path over several workgroups per row for batches of up to
-// kSegMaxBatch rows (the seg_* / row_* chain); all give the same ids.
+// the sampled path over several workgroups per row for batches of up to
+// kSegMaxBatch rows (the seg_* / row_* chain), and for calls whose every
+// top_k is at most 64 a two-launch top-k path (seg_topk / row_topk); all give
+// the same ids.
 //
 // Candidates are ordered by descending logit, ties by ascending id.  Every
 // candidate's probability mass is an exact int64
@@ -1494,15 +1496,55 @@ __global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
 }
 
 // List operations on at most 64 candidates held one per lane, by one wave
-// (no workgroup barriers).  Bitonic sort of the wave, descending; zeros
-// (padding) sort last.
+// (no workgroup barriers).
+//
+// x[lane ^ S] in registers, no LDS round trip: DPP within a 16-lane row for
+// S = 1, 2 (quad_perm), 8 (row_ror:8) and 4 (row_ror:4 for lanes with bit 2
+// set, row_ror:12 for the others: row_ror:n reads lane (i - n) mod 16), the
+// gfx950 row-swap permutes for 16 and 32 (each result holds x[lane] in one
+// half of the rows and x[lane ^ S] in the other).
+template <int CTRL>
+XV_INLINE uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+template <int S>
+XV_INLINE uint32_t xor_lane(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (S == 1) return dpp_u<0xB1>(x);
+  else if constexpr (S == 2) return dpp_u<0x4E>(x);
+  else if constexpr (S == 4) { const uint32_t a = dpp_u<0x124>(x), b = dpp_u<0x12C>(x); return (lane & 4) ? a : b; }
+  else if constexpr (S == 8) return dpp_u<0x128>(x);
+  else if constexpr (S == 16) { const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false); return (lane & 16) ? r[0] : r[1]; }
+  else { static_assert(S == 32, "xor by a power of two below 64"); const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false); return (lane & 32) ? r[0] : r[1]; }
+}
+template <int S>
+XV_INLINE unsigned long long xor_lane64(unsigned long long x) {
+  return ((unsigned long long)xor_lane<S>((uint32_t)(x >> 32)) << 32) | xor_lane<S>((uint32_t)x);
+}
+XV_INLINE unsigned long long xor_lane64(unsigned long long x, int s) {  // s a constant after unrolling
+  switch (s) {
+    case 1: return xor_lane64<1>(x);
+    case 2: return xor_lane64<2>(x);
+    case 4: return xor_lane64<4>(x);
+    case 8: return xor_lane64<8>(x);
+    case 16: return xor_lane64<16>(x);
+    default: return xor_lane64<32>(x);
+  }
+}
+// x[63 - lane]: row_mirror (lane i of a row reads lane 15 - i), then the row swaps
+XV_INLINE unsigned long long reverse_lanes64(unsigned long long x) {
+  const uint32_t lo = dpp_u<0x140>((uint32_t)x), hi = dpp_u<0x140>((uint32_t)(x >> 32));
+  return xor_lane64<32>(xor_lane64<16>(((unsigned long long)hi << 32) | lo));
+}
+
+// Bitonic sort of the wave, descending; zeros (padding) sort last.
 XV_INLINE unsigned long long wave_sort_desc(unsigned long long c) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int size = 2; size <= 64; size <<= 1)
 #pragma unroll
     for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const unsigned long long o = __shfl_xor(c, stride);
+      const unsigned long long o = xor_lane64(c, stride);
       const bool take_max = ((lane & size) == 0) == ((lane & stride) == 0);
       c = take_max ? (o > c ? o : c) : (o < c ? o : c);
     }
@@ -1645,6 +1687,261 @@ __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
     plan.M = M;
     plan.status = kPlanDraw;
   }
+}
+
+// ---------------------------------------------------------------------------
+// Top-k path, for calls whose every row has 1 <= top_k <= kTopList (the
+// caller's max_top_k; greedy rows too, since a row's argmax is its first
+// candidate).  The order of candidates (key descending, id ascending) does not
+// depend on the temperature, so a row's top kTopList candidates are the top
+// kTopList of its segments' own top kTopList lists, and they hold everything
+// a top-k row's cut and draw need: the row max (the first candidate), the
+// masses of the top-k set, the min-p key within it.  Two launches and one pass
+// over the logits:
+//   seg_topk: per segment, its top kTopList candidates, sorted, into the row's
+//             list (each wave selects from its own ids, wave 0 merges);
+//   row_topk: per row, a tree of pairwise merges of the sorted segment lists
+//             (bitonic, in registers, one wave per merge), then the argmax
+//             (greedy rows) or the cut and draw of row_cut_wave (top-k rows).
+// A row that does not meet the bound runs sample_row, so ids never depend on
+// the caller's claim.
+constexpr int kTopList = 64;
+constexpr int kTopVecs = 4;  // 8-id vectors per thread in registers: segments of up to 8192 ids
+
+// Top 64 of two lists sorted descending (lane j holds element j of each):
+// the elementwise max against the reversed second list is bitonic and holds
+// the top 64; six compare-exchange stages sort it descending.
+XV_INLINE unsigned long long merge_top64(unsigned long long x, unsigned long long y) {
+  const int lane = threadIdx.x & 63;
+  const unsigned long long yr = reverse_lanes64(y);
+  unsigned long long c = x > yr ? x : yr;
+#pragma unroll
+  for (int stride = 32; stride > 0; stride >>= 1) {
+    const unsigned long long o = xor_lane64(c, stride);
+    c = (lane & stride) ? (o < c ? o : c) : (o > c ? o : c);
+  }
+  return c;
+}
+
+XV_INLINE int wave_incl_scan_i(int x) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  return x;
+}
+
+// Each wave selects the top kTopList of its own ids (vectors v * kSegThreads
+// + 64 w + lane of the segment, ids ascending in (v, lane, k) order) with no
+// workgroup barrier: its largest key, a wave-private LDS histogram of the
+// 256 keys below it (keys further down never touch LDS), the threshold key T
+// from a scan of that histogram (a bit-by-bit count over all keys when fewer
+// than kTopList lie that close), then a ballot compaction.  Wave 0 merges the
+// four sorted wave lists into the segment's list.
+__global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
+  static_assert(kMaxSegs * kTopList <= kMaxCand, "the segment lists fit the row's list");
+  __shared__ uint32_t hist[kSegWaves][256];
+  __shared__ unsigned long long wl[kSegWaves][kTopList];
+  const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const bf16_t* row = a.logits + (int64_t)b * a.stride;
+  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
+  const int nv = ((end - beg + 7) / 8 + kSegThreads - 1) / kSegThreads;  // <= kTopVecs (checked by the host)
+  // Whole 16-byte vectors first, every load issued before any is used; then
+  // the ids of a partial vector (at most one lane) or of an unaligned row.
+  uint32_t kw[kTopVecs][4];
+#pragma unroll
+  for (int v = 0; v < kTopVecs; ++v) {
+    const int base = beg + (v * kSegThreads + t) * 8;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) kw[v][k] = 0xffffffffu;
+    if (v < nv && vec_ok && base + 8 <= end) {
+      const Vec8 y = load_vec8(row + base);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) kw[v][k] = y.w[k];
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < kTopVecs; ++v) {
+    const int base = beg + (v * kSegThreads + t) * 8;
+    if (v < nv && !(vec_ok && base + 8 <= end) && base < end) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        kw[v][k] = (base + 2 * k < end ? (uint32_t)row[base + 2 * k] : 0xffffu) |
+                   (base + 2 * k + 1 < end ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
+    }
+  }
+  uint32_t kmax = 0;
+#pragma unroll
+  for (int v = 0; v < kTopVecs; ++v)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t k0 = order_key(kw[v][k] & 0xffffu), k1 = order_key(kw[v][k] >> 16);
+      kw[v][k] = k0 | k1 << 16;
+      kmax = max(kmax, max(k0, k1));
+    }
+  auto key_at = [&](int v, int k) { return (kw[v][k >> 1] >> (16 * (k & 1))) & 0xffffu; };
+  kmax = wave_max_u(kmax);
+  // count of this wave's keys >= x (wave uniform)
+  auto count_ge = [&](uint32_t x) {
+    int c = 0;
+#pragma unroll
+    for (int v = 0; v < kTopVecs; ++v)
+      if (v < nv)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) c += __popcll(__ballot(key_at(v, k) >= x));
+    return c;
+  };
+  uint32_t T = 1;    // threshold key: every key > T is taken, and need_eq keys == T
+  int need_eq = kTopList, n_eq = 0;
+  if (kmax == 0) {
+    T = 0xffffffffu;  // nothing but NaN: an empty list
+    need_eq = 0;
+  } else {
+    // histogram of keys kmax - j, j = 0..255, in this wave's LDS row
+    const uint32_t lo = kmax > 255u ? kmax - 255u : 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hist[w][lane + 64 * j] = 0u;
+#pragma unroll
+    for (int v = 0; v < kTopVecs; ++v)
+      if (v < nv)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t key = key_at(v, k);
+          if (key && key >= lo) atomicAdd(&hist[w][kmax - key], 1u);
+        }
+    // lane l holds bins 4l .. 4l + 3 (keys kmax - 4l downwards)
+    uint32_t h[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) h[j] = hist[w][4 * lane + j];
+    const int mine = (int)(h[0] + h[1] + h[2] + h[3]);
+    const int incl = wave_incl_scan_i(mine);
+    const int total = __shfl(incl, 63);
+    if (total >= kTopList) {
+      const int l = (int)wave_first(incl >= kTopList, 63);
+      int above = __shfl(incl - mine, l);
+      const uint32_t h0 = __shfl(h[0], l), h1 = __shfl(h[1], l), h2 = __shfl(h[2], l), h3 = __shfl(h[3], l);
+      const uint32_t hh[4] = {h0, h1, h2, h3};
+      int j = 0;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        if (j == q && above + (int)hh[q] < kTopList) { above += (int)hh[q]; j = q + 1; }
+      T = kmax - (uint32_t)(4 * l + j);
+      n_eq = (int)(j == 0 ? h0 : j == 1 ? h1 : j == 2 ? h2 : h3);
+      need_eq = kTopList - above;
+    } else {
+      // fewer than kTopList keys within 256 of the largest: the largest x
+      // with count(keys >= x) >= kTopList, bit by bit (or every key)
+      const int all = count_ge(1u);
+      if (all <= kTopList) {  // every key: key > 0 selects them, no ranking
+        T = 0;
+        need_eq = 0;
+      } else {
+        uint32_t x = 0;
+        for (int bit = 15; bit >= 0; --bit) {
+          const uint32_t y = x | (1u << bit);
+          if (count_ge(y) >= kTopList) x = y;
+        }
+        T = x;
+        const int gt = count_ge(x + 1);
+        need_eq = kTopList - gt;
+        n_eq = count_ge(x) - gt;
+      }
+    }
+  }
+  // compaction: keys > T, and keys == T in id order up to need_eq of them
+  const bool rank_eq = n_eq > need_eq;
+  int filled = 0, eq_seen = 0;
+#pragma unroll
+  for (int v = 0; v < kTopVecs; ++v) {
+    if (v >= nv) break;
+    int eq_before = 0;  // keys == T of lower lanes in this vector
+    if (rank_eq) {
+      int me = 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) me += key_at(v, k) == T ? 1 : 0;
+      const int inc = wave_incl_scan_i(me);
+      eq_before = inc - me;
+      const int tot = __shfl(inc, 63);
+      eq_before += eq_seen;
+      eq_seen += tot;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t key = key_at(v, k);
+      bool take = key > T && key != 0;
+      if (key == T && key != 0) {
+        take = rank_eq ? eq_before < need_eq : true;
+        ++eq_before;
+      }
+      const unsigned long long m = __ballot(take);
+      if (take) {
+        const int slot = filled + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+        const int id = beg + (v * kSegThreads + t) * 8 + k;
+        wl[w][slot] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
+      }
+      filled += __popcll(m);
+    }
+  }
+  unsigned long long c = lane < filled ? wl[w][lane] : 0ull;
+  c = wave_sort_desc(c);
+  wl[w][lane] = c;
+  __syncthreads();
+  if (w == 0) {
+    const unsigned long long m01 = merge_top64(c, wl[1][lane]);
+    const unsigned long long m23 = merge_top64(wl[2][lane], wl[3][lane]);
+    a.cand[(int64_t)b * kMaxCand + (int64_t)r * kTopList + lane] = merge_top64(m01, m23);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
+  static_assert(kMaxSegs <= 2 * kWaves, "one merge per wave on the first level");
+  __shared__ Shared s;
+  __shared__ FastShared fs;
+  const int b = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const RowParams p = row_params(a, b);
+  if (!p.greedy && !(p.use_k && p.top_k <= kTopList)) {  // outside the bound: the one-workgroup path
+    sample_row(s, fs, b, a.logits, a.stride, a.V, a.temps, a.top_ps, a.top_ks, a.min_ps, a.uniforms,
+               a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
+    return;
+  }
+  unsigned long long* list = a.cand + (int64_t)b * kMaxCand;
+  // level 0: wave w merges segment lists 2w and 2w + 1 (missing lists are empty)
+  {
+    const unsigned long long x = 2 * w < a.R ? list[(2 * w) * kTopList + lane] : 0ull;
+    const unsigned long long y = 2 * w + 1 < a.R ? list[(2 * w + 1) * kTopList + lane] : 0ull;
+    fs.cand[w * kTopList + lane] = merge_top64(x, y);
+  }
+  __syncthreads();
+  for (int half = kWaves / 2; half >= 1; half >>= 1) {
+    unsigned long long m = 0;
+    if (w < half) m = merge_top64(fs.cand[(2 * w) * kTopList + lane], fs.cand[(2 * w + 1) * kTopList + lane]);
+    __syncthreads();
+    if (w < half) fs.cand[w * kTopList + lane] = m;
+    __syncthreads();
+  }
+  if (t >= 64) return;
+  const unsigned long long c = fs.cand[lane];
+  const int n = __popcll(__ballot(c != 0ull));
+  const unsigned long long top = __shfl(c, 0);
+  if (p.greedy || n == 0) {  // argmax; a row of NaN only: 0, as the other paths
+    if (t == 0) a.out_ids[b] = n ? cand_id(top) : 0;
+    return;
+  }
+  RowPlan pl;
+  pl.use_k = 1;
+  pl.inv_t = 1.0f / p.temp;
+  pl.zmax = bf16_to_f32(key_to_bits(cand_key(top))) * pl.inv_t;
+  uint32_t kminp = 0xffffffffu;
+  if (p.use_m && t < n) {
+    const uint32_t key = cand_key(c);
+    if (sampler_exp2(log2_ratio(key_to_bits(key), pl.inv_t, pl.zmax)) >= p.min_p) kminp = key;
+  }
+  pl.kminp = wave_min_u(kminp);
+  list[t] = c;  // row_cut_wave reads the sorted list back, each lane its own slot
+  row_cut_wave(a, pl, p, b, n);
 }
 
 XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t id_cut, float inv_t, float zmax) {
@@ -1831,6 +2128,20 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     a.seg_mass = (unsigned long long*)(w + L.mass);
     a.cand = (unsigned long long*)(w + L.cand);
     const dim3 segs((unsigned)L.R, (unsigned)batch), rows((unsigned)batch);
+    // top-k path: its own segments (about 2048 workgroups, none longer than
+    // the keys a thread holds), its lists in the rows' candidate lists
+    const int seg_cap = kTopVecs * 8 * kSegThreads;
+    const int rt = max((vocab + seg_cap - 1) / seg_cap, min(kMaxSegs, XV_SEG_TARGET / batch));
+    if ((flags & XV_SAMPLE_TOP_K_LE_64) && rt <= kMaxSegs) {
+      SegArgs at = a;
+      at.seg_len = min(seg_cap, ((vocab + rt - 1) / rt + 7) / 8 * 8);
+      at.R = (vocab + at.seg_len - 1) / at.seg_len;
+      seg_topk_kernel<<<dim3((unsigned)at.R, (unsigned)batch), kSegThreads, 0, stream>>>(at);
+      XV_CHECK_LAUNCH();
+      row_topk_kernel<<<rows, kThreads, 0, stream>>>(at);
+      XV_CHECK_LAUNCH();
+      return 0;
+    }
     seg_stats_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     seg_hist_kernel<<<segs, kSegThreads, 0, stream>>>(a);

@@ -47,6 +47,7 @@ XV_SAMPLE_ALL_GREEDY = 1
 XV_SAMPLE_USE_TOP_K = 2
 XV_SAMPLE_USE_TOP_P = 4
 XV_SAMPLE_USE_MIN_P = 8
+XV_SAMPLE_TOP_K_LE_64 = 16
 
 
 def lib_path() -> Path:

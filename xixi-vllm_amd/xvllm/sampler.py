@@ -51,12 +51,15 @@ def sample(
     use_min_p: bool = False,
     out: torch.Tensor | None = None,
     multi_workgroup: bool = True,
+    max_top_k: int = 0,
 ) -> torch.Tensor:
     """Raw entry: bf16 logits [B, V] -> int64 ids [B] (graph-capturable).
 
     With `multi_workgroup` (the default) the kernels get a workspace and split
     each row over several workgroups; without it one workgroup takes a row.
-    Both give the same ids."""
+    `max_top_k` is the largest top-k of any row, as the reference's
+    ``Batch.max_top_k``; at most 64 selects the two-launch top-k path.  All
+    of these give the same ids."""
     require_cuda(logits)
     require_bf16(logits)
     if logits.stride(-1) != 1:
@@ -71,6 +74,8 @@ def sample(
         flags |= _C.XV_SAMPLE_USE_TOP_P
     if use_min_p:
         flags |= _C.XV_SAMPLE_USE_MIN_P
+    if use_top_k and 0 < max_top_k <= 64:
+        flags |= _C.XV_SAMPLE_TOP_K_LE_64
 
     def prep(t, dt):
         if t is None:
@@ -113,13 +118,14 @@ class Sampler(nn.Module):
         max_top_k: int = 0,
         uniforms: torch.Tensor | None = None,
     ) -> torch.Tensor:
-        """Returns [batch] token ids.  ``any_greedy`` and ``max_top_k`` are accepted
-        for interface parity (the kernel checks each row's temperature and
-        top-k itself)."""
-        del any_greedy, max_top_k
+        """Returns [batch] token ids.  ``any_greedy`` is accepted for interface
+        parity (the kernel checks each row's temperature itself); ``max_top_k``
+        at most 64 selects the kernels' top-k path."""
+        del any_greedy
         if uniforms is None and not all_greedy:
             uniforms = torch.rand(logits.shape[0], generator=generator, device=logits.device)
         return sample(
             logits, temperatures, top_ps, top_ks, min_ps, uniforms,
             all_greedy=all_greedy, use_top_k=use_top_k, use_top_p=use_top_p, use_min_p=use_min_p,
+            max_top_k=max_top_k,
         )
