@@ -263,8 +263,8 @@ def kernel_suite(torch, dev) -> dict:
         # max_top_k as the serving loop passes it (the reference's Batch.max_top_k)
         rec(f"sampler_k50_p0.9_B{bsz}", _time(torch, lambda: sample(logits, temps, tps, tks, None, u, use_top_k=True,
                                                                     use_top_p=True, max_top_k=50), 20), bsz * V * 2)
-        if bsz == 64:  # the same call without the bound: the histogram chain
-            rec("sampler_k50_p0.9_B64_no_max_top_k",
+        if bsz in (64, 256):  # the same call without the bound: the histogram chain / one workgroup per row
+            rec(f"sampler_k50_p0.9_B{bsz}_no_max_top_k",
                 _time(torch, lambda: sample(logits, temps, tps, tks, None, u, use_top_k=True, use_top_p=True), 20),
                 bsz * V * 2)
     # config 5's sampling: top-p 0.95 at T 1.0 over near-flat logits (as a

@@ -219,10 +219,11 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
 #define XV_SAMPLE_USE_TOP_P  4
 #define XV_SAMPLE_USE_MIN_P  8
 /* Every row's top_k is in [1, 64] (the reference's host-side max_top_k,
- * src/compute/batch.py:251, at most 64): with a workspace, calls of up to
- * 128 rows take a two-launch top-k path that reads the logits once.  Ids are
- * the same with or without it; a row outside the bound is still sampled
- * exactly (one workgroup for that row). */
+ * src/compute/batch.py:251, at most 64): with a workspace, a two-launch
+ * top-k path that reads the logits once (batches whose B x 32 x 64 candidate
+ * lists fit the workspace's sampled region: up to 1500 rows at V 151936).
+ * Ids are the same with or without it; a row outside the bound is still
+ * sampled exactly (one workgroup for that row). */
 #define XV_SAMPLE_TOP_K_LE_64 16
 size_t xv_sampler_workspace_size(int batch, int vocab);
 int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,

@@ -691,6 +691,8 @@ def test_sampler_randomized_configurations_bitexact(dev):
         ("k7_odd_vocab", 5, 1003, 2 | 4, 7, None),
         ("k33_vocab_4099", 128, 4099, 2 | 4 | 8, 33, None),
         ("k64_odd_vocab_b128", 128, 151935, 2 | 4, 64, None),
+        ("k50_b256", 256, 151936, 2 | 4, 50, None),                # above the chain's 128 rows
+        ("k16_b300_v32000", 300, 32000, 2 | 4 | 8, 16, "ties"),
     ],
 )
 def test_sampler_topk_path_bitexact(dev, name, b, v, flags, top_k, kind):

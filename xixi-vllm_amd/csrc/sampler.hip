@@ -1086,7 +1086,8 @@ struct SegArgs {
   int64_t* seg_kept;            // [B * R]
   uint32_t* seg_cnt;            // [B * R * kBuckets]
   unsigned long long* seg_mass; // [B * R * kBuckets]
-  unsigned long long* cand;     // [B * kMaxCand]
+  unsigned long long* cand;     // [B * cand_stride]
+  int64_t cand_stride;          // candidates per row: kMaxCand, or R * kTopList on the top-k path
 };
 
 struct RowParams {
@@ -1486,7 +1487,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
   __syncthreads();
   if (mine == 0) return;
   int64_t slot = (int64_t)base_lds + incl - mine;
-  unsigned long long* dst = a.cand + (int64_t)b * kMaxCand;
+  unsigned long long* dst = a.cand + (int64_t)b * a.cand_stride;
   for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int id) {
     if (!in_plan(bits)) return;
     if (slot < kMaxCand)
@@ -1570,7 +1571,7 @@ XV_INLINE int64_t wave_first(bool pred, int64_t none) {
 XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n) {
   const int lane = threadIdx.x & 63;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
-  unsigned long long c = lane < n ? a.cand[(int64_t)b * kMaxCand + lane] : 0ull;
+  unsigned long long c = lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull;
   c = wave_sort_desc(c);
   const int64_t q = lane < n ? cand_mass(c, inv_t, zmax) : 0;
   const int64_t incl = wave_incl_scan_l(q);
@@ -1645,7 +1646,7 @@ __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
     if (t < 64) row_cut_wave(a, plan, p, b, n);
     return;
   }
-  const unsigned long long* src = a.cand + (int64_t)b * kMaxCand;
+  const unsigned long long* src = a.cand + (int64_t)b * a.cand_stride;
   for (int i = t; i < n; i += kThreads) fs.cand[i] = src[i];
   __syncthreads();
   sort_cand_desc(fs, n);
@@ -1892,7 +1893,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
   if (w == 0) {
     const unsigned long long m01 = merge_top64(c, wl[1][lane]);
     const unsigned long long m23 = merge_top64(wl[2][lane], wl[3][lane]);
-    a.cand[(int64_t)b * kMaxCand + (int64_t)r * kTopList + lane] = merge_top64(m01, m23);
+    a.cand[(int64_t)b * a.cand_stride + (int64_t)r * kTopList + lane] = merge_top64(m01, m23);
   }
 }
 
@@ -1907,7 +1908,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
                a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
     return;
   }
-  unsigned long long* list = a.cand + (int64_t)b * kMaxCand;
+  unsigned long long* list = a.cand + (int64_t)b * a.cand_stride;
   // level 0: wave w merges segment lists 2w and 2w + 1 (missing lists are empty)
   {
     const unsigned long long x = 2 * w < a.R ? list[(2 * w) * kTopList + lane] : 0ull;
@@ -2107,6 +2108,34 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     XV_CHECK_LAUNCH();
     return 0;
   }
+  // Calls whose every top_k is at most kTopList (the caller's max_top_k): the
+  // two-launch top-k path, on its own segments (about 2048 workgroups, none
+  // longer than the keys a thread holds) and a compact list region of
+  // B * R * kTopList candidates at the top of the workspace.  It stays inside
+  // the sampled region the size query reserves, so it never reaches the
+  // greedy lines; batches whose lists do not fit take the paths below.
+  if ((flags & XV_SAMPLE_TOP_K_LE_64) && workspace != nullptr && temperatures != nullptr &&
+      workspace_bytes >= xv_sampler_workspace_size(batch, vocab)) {
+    const int seg_cap = kTopVecs * 8 * kSegThreads;
+    const int rt = max((vocab + seg_cap - 1) / seg_cap, min(kMaxSegs, max(1, XV_SEG_TARGET / batch)));
+    const int seg_len = min(seg_cap, ((vocab + rt - 1) / rt + 7) / 8 * 8);
+    const int R = (vocab + seg_len - 1) / seg_len;
+    const size_t region = align256((size_t)batch * R * kTopList * 8);
+    if (R <= kMaxSegs && batch <= 65535 && region <= seg_reserve(batch, vocab)) {
+      SegArgs a = {};
+      a.logits = (const bf16_t*)logits; a.stride = logits_stride;
+      a.V = vocab; a.R = R; a.seg_len = seg_len; a.flags = flags & ~XV_SAMPLE_ALL_GREEDY;
+      a.temps = temperatures; a.top_ps = top_ps; a.top_ks = top_ks; a.min_ps = min_ps; a.uniforms = uniforms;
+      a.out_ids = out_ids;
+      a.cand = (unsigned long long*)((char*)workspace + ((workspace_bytes - region) & ~(size_t)255));
+      a.cand_stride = (int64_t)R * kTopList;
+      seg_topk_kernel<<<dim3((unsigned)R, (unsigned)batch), kSegThreads, 0, stream>>>(a);
+      XV_CHECK_LAUNCH();
+      row_topk_kernel<<<dim3((unsigned)batch), kThreads, 0, stream>>>(a);
+      XV_CHECK_LAUNCH();
+      return 0;
+    }
+  }
   // Sampled (or mixed) batches of up to kSegMaxBatch rows: several workgroups
   // per row.  Larger batches fill the device with one workgroup per row, which
   // reads each row fewer times.
@@ -2127,21 +2156,8 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     a.seg_cnt = (uint32_t*)(w + L.cnt);
     a.seg_mass = (unsigned long long*)(w + L.mass);
     a.cand = (unsigned long long*)(w + L.cand);
+    a.cand_stride = kMaxCand;
     const dim3 segs((unsigned)L.R, (unsigned)batch), rows((unsigned)batch);
-    // top-k path: its own segments (about 2048 workgroups, none longer than
-    // the keys a thread holds), its lists in the rows' candidate lists
-    const int seg_cap = kTopVecs * 8 * kSegThreads;
-    const int rt = max((vocab + seg_cap - 1) / seg_cap, min(kMaxSegs, XV_SEG_TARGET / batch));
-    if ((flags & XV_SAMPLE_TOP_K_LE_64) && rt <= kMaxSegs) {
-      SegArgs at = a;
-      at.seg_len = min(seg_cap, ((vocab + rt - 1) / rt + 7) / 8 * 8);
-      at.R = (vocab + at.seg_len - 1) / at.seg_len;
-      seg_topk_kernel<<<dim3((unsigned)at.R, (unsigned)batch), kSegThreads, 0, stream>>>(at);
-      XV_CHECK_LAUNCH();
-      row_topk_kernel<<<rows, kThreads, 0, stream>>>(at);
-      XV_CHECK_LAUNCH();
-      return 0;
-    }
     seg_stats_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     seg_hist_kernel<<<segs, kSegThreads, 0, stream>>>(a);
