@@ -187,8 +187,72 @@ XV_INLINE float wave_maxf(float x) {
   for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
   return x;
 }
+// x[lane ^ S] in registers, no LDS round trip: DPP within a 16-lane row for
+// S = 1, 2 (quad_perm), 8 (row_ror:8) and 4 (row_ror:4 for lanes with bit 2
+// set, row_ror:12 for the others: row_ror:n reads lane (i - n) mod 16), the
+// gfx950 row-swap permutes for 16 and 32 (each result holds x[lane] in one
+// half of the rows and x[lane ^ S] in the other).
+template <int CTRL>
+XV_INLINE uint32_t dpp_u(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
+}
+template <int S>
+XV_INLINE uint32_t xor_lane(uint32_t x) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (S == 1) return dpp_u<0xB1>(x);
+  else if constexpr (S == 2) return dpp_u<0x4E>(x);
+  else if constexpr (S == 4) { const uint32_t a = dpp_u<0x124>(x), b = dpp_u<0x12C>(x); return (lane & 4) ? a : b; }
+  else if constexpr (S == 8) return dpp_u<0x128>(x);
+  else if constexpr (S == 16) { const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false); return (lane & 16) ? r[0] : r[1]; }
+  else { static_assert(S == 32, "xor by a power of two below 64"); const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false); return (lane & 32) ? r[0] : r[1]; }
+}
+template <int S>
+XV_INLINE unsigned long long xor_lane64(unsigned long long x) {
+  return ((unsigned long long)xor_lane<S>((uint32_t)(x >> 32)) << 32) | xor_lane<S>((uint32_t)x);
+}
+XV_INLINE unsigned long long xor_lane64(unsigned long long x, int s) {  // s a constant after unrolling
+  switch (s) {
+    case 1: return xor_lane64<1>(x);
+    case 2: return xor_lane64<2>(x);
+    case 4: return xor_lane64<4>(x);
+    case 8: return xor_lane64<8>(x);
+    case 16: return xor_lane64<16>(x);
+    default: return xor_lane64<32>(x);
+  }
+}
+// x[63 - lane]: row_mirror (lane i of a row reads lane 15 - i), then the row swaps
+XV_INLINE unsigned long long reverse_lanes64(unsigned long long x) {
+  const uint32_t lo = dpp_u<0x140>((uint32_t)x), hi = dpp_u<0x140>((uint32_t)(x >> 32));
+  return xor_lane64<32>(xor_lane64<16>(((unsigned long long)hi << 32) | lo));
+}
+
+// x[lane - S] within the lane's 16-lane row (0 for the first S lanes of a
+// row), and the cross-row broadcasts of lane 15 (into rows 1, 3) and lane 31
+// (into rows 2, 3); other lanes get 0.
+template <int CTRL, int ROWS>
+XV_INLINE uint64_t dpp64(uint64_t x) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)x, CTRL, ROWS, 0xf, true);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(x >> 32), CTRL, ROWS, 0xf, true);
+  return ((uint64_t)hi << 32) | lo;
+}
 XV_INLINE int64_t wave_sum_l(int64_t x) {
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  x += (int64_t)xor_lane64<1>((uint64_t)x);
+  x += (int64_t)xor_lane64<2>((uint64_t)x);
+  x += (int64_t)xor_lane64<4>((uint64_t)x);
+  x += (int64_t)xor_lane64<8>((uint64_t)x);
+  x += (int64_t)xor_lane64<16>((uint64_t)x);
+  x += (int64_t)xor_lane64<32>((uint64_t)x);
+  return x;
+}
+// Inclusive prefix sum over the wave's lanes: within rows by row_shr 1, 2, 4,
+// 8, then row 1 and 3 add lane 15 of the row before, rows 2 and 3 lane 31.
+XV_INLINE int64_t wave_incl_scan_l(int64_t x) {
+  x += (int64_t)dpp64<0x111, 0xf>((uint64_t)x);
+  x += (int64_t)dpp64<0x112, 0xf>((uint64_t)x);
+  x += (int64_t)dpp64<0x114, 0xf>((uint64_t)x);
+  x += (int64_t)dpp64<0x118, 0xf>((uint64_t)x);
+  x += (int64_t)dpp64<0x142, 0xa>((uint64_t)x);
+  x += (int64_t)dpp64<0x143, 0xc>((uint64_t)x);
   return x;
 }
 
@@ -1499,45 +1563,6 @@ __global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
 // List operations on at most 64 candidates held one per lane, by one wave
 // (no workgroup barriers).
 //
-// x[lane ^ S] in registers, no LDS round trip: DPP within a 16-lane row for
-// S = 1, 2 (quad_perm), 8 (row_ror:8) and 4 (row_ror:4 for lanes with bit 2
-// set, row_ror:12 for the others: row_ror:n reads lane (i - n) mod 16), the
-// gfx950 row-swap permutes for 16 and 32 (each result holds x[lane] in one
-// half of the rows and x[lane ^ S] in the other).
-template <int CTRL>
-XV_INLINE uint32_t dpp_u(uint32_t x) {
-  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xf, 0xf, false);
-}
-template <int S>
-XV_INLINE uint32_t xor_lane(uint32_t x) {
-  const int lane = threadIdx.x & 63;
-  if constexpr (S == 1) return dpp_u<0xB1>(x);
-  else if constexpr (S == 2) return dpp_u<0x4E>(x);
-  else if constexpr (S == 4) { const uint32_t a = dpp_u<0x124>(x), b = dpp_u<0x12C>(x); return (lane & 4) ? a : b; }
-  else if constexpr (S == 8) return dpp_u<0x128>(x);
-  else if constexpr (S == 16) { const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false); return (lane & 16) ? r[0] : r[1]; }
-  else { static_assert(S == 32, "xor by a power of two below 64"); const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false); return (lane & 32) ? r[0] : r[1]; }
-}
-template <int S>
-XV_INLINE unsigned long long xor_lane64(unsigned long long x) {
-  return ((unsigned long long)xor_lane<S>((uint32_t)(x >> 32)) << 32) | xor_lane<S>((uint32_t)x);
-}
-XV_INLINE unsigned long long xor_lane64(unsigned long long x, int s) {  // s a constant after unrolling
-  switch (s) {
-    case 1: return xor_lane64<1>(x);
-    case 2: return xor_lane64<2>(x);
-    case 4: return xor_lane64<4>(x);
-    case 8: return xor_lane64<8>(x);
-    case 16: return xor_lane64<16>(x);
-    default: return xor_lane64<32>(x);
-  }
-}
-// x[63 - lane]: row_mirror (lane i of a row reads lane 15 - i), then the row swaps
-XV_INLINE unsigned long long reverse_lanes64(unsigned long long x) {
-  const uint32_t lo = dpp_u<0x140>((uint32_t)x), hi = dpp_u<0x140>((uint32_t)(x >> 32));
-  return xor_lane64<32>(xor_lane64<16>(((unsigned long long)hi << 32) | lo));
-}
-
 // Bitonic sort of the wave, descending; zeros (padding) sort last.
 XV_INLINE unsigned long long wave_sort_desc(unsigned long long c) {
   const int lane = threadIdx.x & 63;
@@ -1550,15 +1575,6 @@ XV_INLINE unsigned long long wave_sort_desc(unsigned long long c) {
       c = take_max ? (o > c ? o : c) : (o < c ? o : c);
     }
   return c;
-}
-XV_INLINE int64_t wave_incl_scan_l(int64_t x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
 }
 // First lane whose predicate holds, `none` if no lane's does.
 XV_INLINE int64_t wave_first(bool pred, int64_t none) {
@@ -1724,15 +1740,7 @@ XV_INLINE unsigned long long merge_top64(unsigned long long x, unsigned long lon
   return c;
 }
 
-XV_INLINE int wave_incl_scan_i(int x) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
-  return x;
-}
+XV_INLINE int wave_incl_scan_i(int x) { return (int)wave_incl_scan_l(x); }
 
 // Each wave selects the top kTopList of its own ids (vectors v * kSegThreads
 // + 64 w + lane of the segment, ids ascending in (v, lane, k) order) with no
