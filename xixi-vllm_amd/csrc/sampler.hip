@@ -1584,10 +1584,11 @@ XV_INLINE int64_t wave_first(bool pred, int64_t none) {
 
 // row_cut for a list of n <= 64 candidates, wave 0 alone: the same cut, kept
 // mass and draw as the workgroup list functions.
-XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n) {
+// c: this lane's candidate (0 past n), in any order.
+XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
+                                 unsigned long long c) {
   const int lane = threadIdx.x & 63;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
-  unsigned long long c = lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull;
   c = wave_sort_desc(c);
   const int64_t q = lane < n ? cand_mass(c, inv_t, zmax) : 0;
   const int64_t incl = wave_incl_scan_l(q);
@@ -1636,6 +1637,11 @@ XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p,
     plan.M = plan.m_before + m_list;
     plan.status = kPlanDraw;
   }
+}
+
+XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n) {
+  const int lane = threadIdx.x & 63;
+  row_cut_wave_list(a, plan, p, b, n, lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull);
 }
 
 __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
@@ -1949,8 +1955,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
     if (sampler_exp2(log2_ratio(key_to_bits(key), pl.inv_t, pl.zmax)) >= p.min_p) kminp = key;
   }
   pl.kminp = wave_min_u(kminp);
-  list[t] = c;  // row_cut_wave reads the sorted list back, each lane its own slot
-  row_cut_wave(a, pl, p, b, n);
+  row_cut_wave_list(a, pl, p, b, n, c);
 }
 
 XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t id_cut, float inv_t, float zmax) {
