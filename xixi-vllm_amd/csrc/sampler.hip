@@ -2122,7 +2122,7 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     return 0;
   }
   // Calls whose every top_k is at most kTopList (the caller's max_top_k): the
-  // two-launch top-k path, on its own segments (about 2048 workgroups, none
+  // two-launch top-k path, on its own segments (about 1024 workgroups, none
   // longer than the keys a thread holds) and a compact list region of
   // B * R * kTopList candidates at the top of the workspace.  It stays inside
   // the sampled region the size query reserves, so it never reaches the
@@ -2130,7 +2130,9 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
   if ((flags & XV_SAMPLE_TOP_K_LE_64) && workspace != nullptr && temperatures != nullptr &&
       workspace_bytes >= xv_sampler_workspace_size(batch, vocab)) {
     const int seg_cap = kTopVecs * 8 * kSegThreads;
-    const int rt = max((vocab + seg_cap - 1) / seg_cap, min(kMaxSegs, max(1, XV_SEG_TARGET / batch)));
+    // about 1024 workgroups: one residency round (2048, as the chain, took 1.3 rounds and
+    // 28.5 us at B 64 against 24.9 us)
+    const int rt = max((vocab + seg_cap - 1) / seg_cap, min(kMaxSegs, max(1, 1024 / batch)));
     const int seg_len = min(seg_cap, ((vocab + rt - 1) / rt + 7) / 8 * 8);
     const int R = (vocab + seg_len - 1) / seg_len;
     const size_t region = align256((size_t)batch * R * kTopList * 8);
