@@ -1872,7 +1872,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
 #pragma unroll
   for (int v = 0; v < kTopVecs; ++v) {
     if (v >= nv) break;
-    int eq_before = 0;  // keys == T of lower lanes in this vector
+    int eq_before = 0;  // keys == T at lower ids: earlier vectors, then lower lanes of this one
     if (rank_eq) {
       int me = 0;
 #pragma unroll
