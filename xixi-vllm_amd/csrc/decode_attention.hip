@@ -433,11 +433,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
     const int ctx = b < a.batch ? max(a.seqlens[b], 0) : 0;
     const int np = (ctx + kPage - 1) / kPage;
     int inc = np;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int y = __shfl_up(inc, o);
-      if (lane >= o) inc += y;
-    }
+    // inclusive scan by DPP: within 16-lane rows, then across rows
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xf, 0xf, true);  // row_shr:1
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x112, 0xf, 0xf, true);  // row_shr:2
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x114, 0xf, 0xf, true);  // row_shr:4
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x118, 0xf, 0xf, true);  // row_shr:8
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x142, 0xa, 0xf, true);  // row_bcast:15 into rows 1, 3
+    inc += __builtin_amdgcn_update_dpp(0, inc, 0x143, 0xc, 0xf, true);  // row_bcast:31 into rows 2, 3
     if (b < a.batch) {
       pref[b + 1] = carry + inc;
       sl[b] = ctx;
@@ -467,8 +469,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   Cursor ic = c0, pc = c0;  // issue and process cursors
   const __amdgpu_buffer_rsrc_t rbt =
       page_rsrc(reinterpret_cast<const bf16_t*>(a.bt), (uint32_t)((int64_t)a.batch * a.bt_stride * 4));
+  // the first window only: the second is requested once the first pages are
+  // in flight (it is read kIdWindow - NB positions later)
   load_window(idtab, a, rbt, pref, f0, 0, n, lane);
-  load_window(idtab + kIdWindow * 4, a, rbt, pref, f0, kIdWindow, n, lane);
   __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");  // nothing else in flight yet
   int issued = -1;  // last stream position issued
 
@@ -520,6 +523,8 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
 #pragma unroll
     for (int k = 0; k < NB - 1; ++k) issue(min(k, n - 1), k, ids.v[k]);
   }
+  // window 1; every page wait before its first use orders it
+  load_window(idtab + kIdWindow * 4, a, rbt, pref, f0, kIdWindow, n, lane);
   for (int x0 = 0; x0 < n; x0 += NB) {
     // ids of the NB positions issued in this round; window k+1 of the table
     // was requested when the issue side entered window k, at least
