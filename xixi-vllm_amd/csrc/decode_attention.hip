@@ -608,8 +608,9 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
   const int g = lane >> 4, i = lane & 15;  // group g: partials g, g + 4, ...; dims 8i .. 8i + 7
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < n; j0 += 32) {
-    float4 v[8][2];
+  // batches of 32 partials (8 per group), two in flight: the next batch's
+  // loads are issued before the current one is folded in
+  auto load = [&](float4 (&v)[8][2], int j0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const int j = min(j0 + 4 * k + g, n - 1);
@@ -617,6 +618,8 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
       v[k][0] = src[0];
       v[k][1] = src[1];
     }
+  };
+  auto fold = [&](const float4 (&v)[8][2], int j0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       // partial j's weight sits in lane j mod 64, in the register of its
@@ -627,6 +630,16 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
       const float w = j < n ? (j < 64 ? w_a : j < 128 ? w_b : w_c) : 0.f;
       acc[0] += w * v[k][0].x; acc[1] += w * v[k][0].y; acc[2] += w * v[k][0].z; acc[3] += w * v[k][0].w;
       acc[4] += w * v[k][1].x; acc[5] += w * v[k][1].y; acc[6] += w * v[k][1].z; acc[7] += w * v[k][1].w;
+    }
+  };
+  float4 va[8][2], vb[8][2];
+  load(va, 0);
+  for (int j0 = 0; j0 < n; j0 += 64) {
+    if (j0 + 32 < n) load(vb, j0 + 32);
+    fold(va, j0);
+    if (j0 + 32 < n) {
+      if (j0 + 64 < n) load(va, j0 + 64);
+      fold(vb, j0 + 32);
     }
   }
 #pragma unroll
