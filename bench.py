@@ -335,7 +335,8 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
 
     def step():
-        return runner._sample_logits(runner.decode_hidden(bsz), bsz)
+        runner.decode_hidden(bsz)
+        return runner.decode_sample(bsz)
 
     for _ in range(3):
         step()
@@ -405,7 +406,8 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
     runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
 
     def step():
-        return runner._sample_logits(runner.decode_hidden(bsz), bsz)
+        runner.decode_hidden(bsz)
+        return runner.decode_sample(bsz)
 
     for _ in range(2):
         step()
@@ -433,22 +435,20 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
 
 
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
-              max_num_seqs: int = 256, max_num_batched_tokens: int = 8192) -> dict:
+              max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, model=None) -> dict:
     """Config 4: Qwen3-8B (random bf16 weights ~N(0,0.02)) serving 256 requests
     with random-token prompts of U[128, 2048] tokens, each generating `gen`
     tokens (EOS ignored), under continuous batching with the reference
-    scheduler's default policy (src/control/scheduler.py:58-154: every running
-    sequence decodes one token per step, the leftover of the 8192-token budget
-    goes to prefill chunks, at most one of them partial; max 256 sequences).
-    Decode runs under hipGraph; prefill and sampling eagerly.  Sampled runs use
+    scheduler's default policy (xvllm.serving: every running sequence decodes
+    one token per step, the leftover of the 8192-token budget goes to prefill
+    chunks, at most one of them partial; max 256 sequences).  Decode and its
+    LM head + sampler run under hipGraph; prefill eagerly.  Sampled runs use
     T 0.7 / top-k 50 / top-p 0.9 with draws from a seeded generator."""
-    from collections import deque
-
-    from xvllm.batch import SeqSchedule
     from xvllm.config import QWEN3_8B
     from xvllm.kv_pool import KVPool
     from xvllm.model_runner import ModelRunner
     from xvllm.models import Qwen3ForCausalLM
+    from xvllm.serving import serve
 
     cfg = QWEN3_8B
     g = torch.Generator().manual_seed(seed + 404)
@@ -459,89 +459,30 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(dev):
-            model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+            if model is None:
+                model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
             kv = KVPool(cfg, num_blocks=pages_needed + 16, block_size=PAGE, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
+    samp = dict(temperature=0.7, top_p=0.9, top_k=50) if sampled else None
+    modes = (2 | 4 | 16,) if sampled else ()  # the sampled run's sampler graphs, recorded up front
     runner = ModelRunner(model, kv, max_num_seqs=max_num_seqs, max_num_batched_tokens=max_num_batched_tokens,
-                         context_len=max_len, device=dev)
+                         context_len=max_len, device=dev, sample_modes=modes)
     runner.generator = torch.Generator(device=dev).manual_seed(seed + 7) if sampled else None
-    free = list(range(pages_needed + 16))[::-1]
-
-    class Req:
-        __slots__ = ("rid", "prompt", "out", "bt", "cached")
-
-        def __init__(self, rid, prompt):
-            self.rid, self.prompt, self.out, self.bt, self.cached = rid, prompt, [], [], 0
-
-    samp = dict(temperature=0.7, top_p=0.9, top_k=50) if sampled else dict(temperature=0.0)
-    waiting = deque(Req(i, p) for i, p in enumerate(prompts))
-    running: deque = deque()
-    steps = decode_tokens = prefill_tokens = 0
-    host_s = 0.0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    while waiting or running:
-        h0 = time.perf_counter()
-        decodes, dreqs = [], []
-        for r in running:  # one token per running sequence (its last sampled token)
-            if len(decodes) >= max_num_seqs:
-                break
-            pos = r.cached
-            if pos // PAGE >= len(r.bt):
-                r.bt.append(free.pop())
-            decodes.append(SeqSchedule(r.rid, [r.out[-1]], pos, r.bt, **samp))
-            dreqs.append(r)
-        used = len(decodes)
-        prefills, preqs = [], []
-        for r in list(waiting):
-            if len(decodes) + len(prefills) >= max_num_seqs:
-                break
-            remaining = max_num_batched_tokens - used
-            if remaining <= 0:
-                break
-            if not r.bt:  # all of the prompt's pages at admission (the reference allocates at _try_alloc)
-                r.bt = [free.pop() for _ in range((len(r.prompt) + PAGE - 1) // PAGE)]
-            need = len(r.prompt) - r.cached
-            if remaining < need and prefills and not decodes:
-                break  # prefill-first steps take no trailing partial chunk
-            chunk = min(need, remaining)
-            done = r.cached + chunk == len(r.prompt)
-            prefills.append(SeqSchedule(r.rid, r.prompt[r.cached : r.cached + chunk], r.cached, r.bt,
-                                        need_sample=done, **samp))
-            preqs.append((r, chunk, done))
-            used += chunk
-            if not done:
-                break  # at most one partial chunk per step
-        n_p, n_d = runner.run_forward(decodes, prefills)
-        host_s += time.perf_counter() - h0
-        p_ids, d_ids = runner.read_samples(n_p, n_d)
-        steps += 1
-        decode_tokens += len(decodes)
-        for r, tok in zip(dreqs, d_ids):
-            r.cached += 1
-            r.out.append(tok)
-        for (r, chunk, done), tok in zip(preqs, p_ids):
-            r.cached += chunk
-            prefill_tokens += chunk
-            if done:
-                r.out.append(tok)
-                waiting.remove(r)
-                running.append(r)
-        for r in [r for r in running if len(r.out) >= gen]:
-            running.remove(r)
-            free.extend(r.bt)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    outs, st = serve(runner, prompts, gen, sampling=samp, max_num_seqs=max_num_seqs,
+                     max_num_batched_tokens=max_num_batched_tokens)
     runner.destroy()
-    out_tokens = n_req * gen
-    return {"requests": n_req, "prompt_tokens": sum(plens), "generated_tokens": out_tokens, "steps": steps,
-            "sampling": "T0.7/k50/p0.9" if sampled else "greedy", "wall_s": round(wall, 3),
-            "output_tok_per_s": round(out_tokens / wall, 1),
-            "total_tok_per_s": round((out_tokens + sum(plens)) / wall, 1),
-            "host_s_before_sync": round(host_s, 3),
-            "mean_decode_batch": round(decode_tokens / max(1, steps), 1),
-            "policy": "decode-first mixed, 8192-token budget, max 256 seqs, 16-token pages"}
+    del kv
+    torch.cuda.empty_cache()
+    out_tokens = sum(len(o) for o in outs)
+    assert out_tokens == n_req * gen
+    return {"requests": n_req, "prompt_tokens": sum(plens), "generated_tokens": out_tokens, "steps": st.steps,
+            "sampling": "T0.7/k50/p0.9" if sampled else "greedy", "wall_s": round(st.wall_s, 3),
+            "output_tok_per_s": round(out_tokens / st.wall_s, 1),
+            "total_tok_per_s": round((out_tokens + sum(plens)) / st.wall_s, 1),
+            "host_s_before_sync": round(st.host_s, 3),
+            "mean_decode_batch": round(st.decode_tokens / max(1, st.steps), 1),
+            "policy": "decode-first mixed, 8192-token budget, max 256 seqs, 16-token pages"}, model
 
 
 def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
@@ -648,7 +589,7 @@ def main() -> int:
     ap.add_argument("--e2e-only", action="store_true", help="only the Qwen3-8B decode step (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the prefill attention cases (for profiling)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill attention cases")
-    ap.add_argument("--serve", action="store_true", help="also run config 4 (256 requests, greedy and sampled)")
+    ap.add_argument("--no-serve", action="store_true", help="skip config 4 (256 requests, greedy and sampled)")
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
     ap.add_argument("--config5", action="store_true", help="also run config 5 (Qwen3-32B-shaped long-context decode)")
     ap.add_argument("--config5-only", action="store_true", help="only config 5 (for profiling)")
@@ -683,8 +624,9 @@ def main() -> int:
         print(json.dumps(decode_config5(torch, dev)))
         return 0
     if args.serve_only:
-        print(json.dumps({"serve_greedy": serve_e2e(torch, dev, sampled=False),
-                          "serve_sampled": serve_e2e(torch, dev, sampled=True)}))
+        greedy, model = serve_e2e(torch, dev, sampled=False)
+        sampled, model = serve_e2e(torch, dev, sampled=True, model=model)
+        print(json.dumps({"serve_greedy": greedy, "serve_sampled": sampled}))
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_suite(torch, dev, iters=args.steps)))
@@ -752,10 +694,12 @@ def main() -> int:
     if args.config5:
         torch.cuda.empty_cache()
         line["config5"] = decode_config5(torch, dev)
-    if args.serve:
+    if not args.no_serve:
         torch.cuda.empty_cache()
-        line["serve_greedy"] = serve_e2e(torch, dev, sampled=False)
-        line["serve_sampled"] = serve_e2e(torch, dev, sampled=True)
+        line["serve_greedy"], model = serve_e2e(torch, dev, sampled=False)
+        line["serve_sampled"], model = serve_e2e(torch, dev, sampled=True, model=model)
+        del model
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(ctx)
         line["cpu_baseline_rows"] = cpu_baseline_rows()

@@ -63,7 +63,11 @@ int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
  *              second kernel.  No initial contents are required.  Calls
  *              sharing a workspace must be ordered on one stream.
  * Query head h reads kv head h / (Hq / Hkv).  scale multiplies q.k (1/sqrt(D) in the reference).
- * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 (batches above
+ * block_size is the tokens per cache block, any multiple of 16 (the
+ * reference's default kvcache_block_size is 256, src/config.py:66-67): token t
+ * of a sequence is row t % block_size of block block_tables[b][t / block_size],
+ * max_blocks_per_seq counts blocks.
+ * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8} (batches above
  * 256 run as consecutive launches of 256 sequences on the same workspace),
  * head rows of 256 contiguous bytes with head_stride*(Hkv-1) + D <= tok_stride
  * or tok_stride == D (the reference's [page][token][head][d] pool, or a
@@ -97,7 +101,7 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
  *   dense (block_tables == NULL): key token j of sequence b is row cu_k[b]+j of k/v,
  *         element (row, kvh, d) at row*kv_stride_tok + kvh*kv_stride_head + d.
  *   out : element (tok, h, d) at tok*out_stride_tok + h*D + d.
- * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size == 16 when paged.
+ * Supported: D == 128, Hq/Hkv in {1, 2, 4, 8}, block_size a multiple of 16 when paged.
  * Rows move by 16-byte LDS-DMA: q, k, v, k_cache and v_cache 16-byte aligned,
  * every input stride a multiple of 8 elements; out 8-byte aligned with
  * out_stride_tok a multiple of 4 (hipErrorInvalidValue otherwise).

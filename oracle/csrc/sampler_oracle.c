@@ -59,11 +59,14 @@ static int cmp_rank(const void *pa, const void *pb) {
 int64_t oracle_sample_row(const uint16_t *logits, int V, float temperature, float top_p, int top_k, float min_p,
                           float u, int flags) {
   if ((flags & FLAG_ALL_GREEDY) || temperature <= 1e-5f) {
-    /* argmax, lowest index on ties (torch argmax / max) */
+    /* torch.argmax (the reference's greedy, sampler.py:48,61,91 and
+     * vocab_parallel.py:180-216): a NaN is the maximum, so the lowest NaN
+     * index wins if there is one; otherwise the largest value, lowest index
+     * on ties (-0 equals +0). */
     int best = -1;
     float bv = 0.f;
     for (int i = 0; i < V; ++i) {
-      if (is_nan16(logits[i])) continue;
+      if (is_nan16(logits[i])) return i;
       float v = bf16f(logits[i]);
       if (best < 0 || v > bv) { best = i; bv = v; }
     }
@@ -141,7 +144,7 @@ int64_t oracle_sample_row(const uint16_t *logits, int V, float temperature, floa
 void oracle_sample(const uint16_t *logits, int64_t stride, int B, int V, const float *temps, const float *top_ps,
                    const int32_t *top_ks, const float *min_ps, const float *uniforms, int flags, int64_t *out) {
   for (int b = 0; b < B; ++b)
-    out[b] = oracle_sample_row(logits + b * stride, V, temps[b], top_ps ? top_ps[b] : 1.0f,
+    out[b] = oracle_sample_row(logits + b * stride, V, temps ? temps[b] : 1.0f, top_ps ? top_ps[b] : 1.0f,
                                top_ks ? top_ks[b] : V, min_ps ? min_ps[b] : 0.0f, uniforms ? uniforms[b] : 0.5f,
                                flags);
 }

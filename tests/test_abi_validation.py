@@ -31,7 +31,7 @@ def _decode(lib, **kw):
 
 
 def test_decode_rejects_bad_layouts(lib):
-    for kw in (dict(D=64), dict(BS=32), dict(Hq=12), dict(Hq=128), dict(q=U), dict(kc=U), dict(qst=4100),
+    for kw in (dict(D=64), dict(BS=24), dict(BS=0), dict(BS=8), dict(Hq=12), dict(Hq=128), dict(q=U), dict(kc=U), dict(qst=4100),
                dict(ts=1028), dict(out=A + 2), dict(ost=4097), dict(ws=None), dict(wsb=1024), dict(maxb=0)):
         assert _decode(lib, **kw) == INVALID, kw
     assert _decode(lib, B=0) == 0  # nothing to do
@@ -49,7 +49,7 @@ def _prefill(lib, **kw):
 
 def test_prefill_rejects_bad_layouts(lib):
     for kw in (dict(D=64), dict(Hq=24), dict(k=None), dict(k=U), dict(kvst=1020), dict(q=U), dict(qsh=130),
-               dict(out=A + 4), dict(ost=4098), dict(bt=A, kc=A, vc=A, BS=32), dict(bt=A, kc=None, vc=A),
+               dict(out=A + 4), dict(ost=4098), dict(bt=A, kc=A, vc=A, BS=40), dict(bt=A, kc=None, vc=A),
                dict(bt=A, kc=U, vc=A, BS=16), dict(maxq=32 * 65536)):
         assert _prefill(lib, **kw) == INVALID, kw
     assert _prefill(lib, B=0) == 0 and _prefill(lib, maxq=0) == 0

@@ -136,3 +136,40 @@ def test_graph_buckets_and_padding():
             p = r._pad_bs(n)
             assert p >= n and p in bs and not any(n <= b < p for b in bs)
     assert HipGraphRunner.make_bs_list(256)[:6] == [1, 2, 4, 8, 16, 32]
+
+
+def test_staging_rejects_bad_pages_positions_and_ids():
+    """With the pool size known, a page id outside the pool, a position past
+    the block table or an input id outside the vocabulary raises on the host
+    before anything is staged for a kernel; padding rows are staged greedy."""
+    import pytest
+
+    from xvllm.batch import Batch, SeqSchedule
+
+    def mk():
+        return Batch(max_bs=16, max_tokens=2048, max_blocks=32, vocab_size=V, device=CPU, block_size=16,
+                     num_blocks=100)
+
+    ok = SeqSchedule(1, [5], 20, [3, 4])
+    mk().build_decode([ok], pad_to=2)
+    for bad in (SeqSchedule(1, [5], 20, [3, 100]),       # page past the pool
+                SeqSchedule(1, [5], 20, [-1, 4]),        # negative page
+                SeqSchedule(1, [5], 32, [3, 4]),         # position 32 has no page
+                SeqSchedule(1, [V], 20, [3, 4]),         # id outside the vocabulary
+                SeqSchedule(1, [5], 20, list(range(33)))):  # more blocks than a row holds
+        with pytest.raises(ValueError):
+            mk().build_decode([bad])
+    with pytest.raises(ValueError):
+        mk().build_prefill([SeqSchedule(1, list(range(40)), 0, [3, 4])])   # 40 tokens, 2 pages
+    with pytest.raises(ValueError):
+        mk().build_prefill([SeqSchedule(1, [1, 2, 3], 0, [150])])
+    # an appended page is checked too
+    b = mk()
+    b.build_decode([SeqSchedule(7, [5], 31, [3, 4])])
+    with pytest.raises(ValueError):
+        b.build_decode([SeqSchedule(7, [5], 32, [3, 4, 999])])
+    # padding rows sample greedily
+    b = mk()
+    b.temperatures.fill_(0.7)
+    b.build_decode([SeqSchedule(1, [5], 20, [3, 4], temperature=0.9)], pad_to=4)
+    assert b.temperatures[:4].tolist() == pytest.approx([0.9, 0.0, 0.0, 0.0])

@@ -385,15 +385,18 @@ def test_sampler_nan_rows_paths_agree(dev):
     logits[2] = 0.25
     logits[3, :100] = float("nan")
     logits[3, 5000] = float("inf")
+    logits[4, 70001] = logits[4, 90001] = float("nan")  # greedy row: torch.argmax takes NaN id 70001
     temps = torch.tensor([1.0, 0.8, 1.0, 0.7, 0.0, 1.3])
     tps = torch.full((b,), 0.9)
     tks = torch.full((b,), 40, dtype=torch.int32)
     u = torch.rand(b, generator=g)
-    for kw in (dict(use_top_p=True), dict(use_top_k=True, use_top_p=True), {}):
+    for kw in (dict(use_top_p=True), dict(use_top_k=True, use_top_p=True),
+               dict(use_top_k=True, use_top_p=True, max_top_k=40), {}):
         args = (logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), None, u.to(dev))
         got = sample(*args, **kw)
         want = sample(*args, **kw, multi_workgroup=False)
         assert torch.equal(got, want), (kw, got, want)
+        assert int(got[4]) == 70001, kw
 
 
 def test_sampler_many_draws_bitexact(dev):
@@ -540,8 +543,9 @@ def test_config3_elementwise_full_size(dev):
 @pytest.mark.parametrize("b,v", [(1, 151936), (7, 4099), (64, 151936), (300, 32000)])
 def test_greedy_multi_workgroup_bitexact(dev, b, v):
     """All-greedy batches spread each row over several workgroups (one 64-bit
-    atomic max per wave).  Against the C oracle: ties at the maximum (lowest id
-    wins), -0 vs +0 (equal), NaN entries skipped, an all-NaN row (id 0); and a
+    atomic max per wave).  Against the C oracle and torch.argmax (the
+    reference's greedy): ties at the maximum (lowest id wins), -0 vs +0
+    (equal), NaN entries (the lowest NaN id wins), an all-NaN row (id 0); and a
     second call on the same workspace (its slots must have been cleared)."""
     import oracle.sampler as S
     from xvllm.sampler import sample
@@ -555,6 +559,8 @@ def test_greedy_multi_workgroup_bitexact(dev, b, v):
         bits[2, :] = torch.tensor(-32768, dtype=torch.int16)  # all -0.0 ...
         bits[2, 5:9] = 0                                      # ... a few +0.0 after the first ids
         bits[3, ::5] = torch.tensor(0x7FC0, dtype=torch.int16)  # NaNs among values
+        bits[4, v - 3] = torch.tensor(0x7FC0, dtype=torch.int16)  # one NaN near the end
+        bits[5, v // 2 :: 97] = torch.tensor(-64, dtype=torch.int16)  # 0xFFC0: negative-sign NaNs
     for call in range(2):
         xs = x if call == 0 else x.flip(1).contiguous()
         want = S.sample(xs.view(torch.int16).numpy().view(np.uint16), np.zeros(b, np.float32), None, None, None,
@@ -562,6 +568,7 @@ def test_greedy_multi_workgroup_bitexact(dev, b, v):
         got = sample(xs.to(dev), None, all_greedy=True)
         torch.cuda.synchronize()
         assert np.array_equal(got.cpu().numpy(), want), f"call {call}: {got.cpu().numpy()[:8]} vs {want[:8]}"
+        assert np.array_equal(want, xs.argmax(-1).numpy())
 
 
 def test_decode_graphs_largest_first_share_one_workspace(dev):

@@ -259,3 +259,27 @@ def test_sampler_draw_frequencies_chi_square():
     p = S.probs(bits[0], 0.8, 0.9, 20, 0.0, 2 | 4)
     freq = np.bincount(ids, minlength=v) / n
     np.testing.assert_allclose(freq, p, atol=2.0 / n + 1e-12)
+
+
+def test_sampler_greedy_is_torch_argmax():
+    """The reference's greedy id is ``logits.argmax(-1)`` on the bf16 logits
+    (src/compute/sampler.py:48,61,91): the lowest index on ties, -0 equal to
+    +0, and a NaN counts as the maximum (the lowest NaN index wins)."""
+    import torch
+
+    v = 777
+    x = rng.standard_normal((10, v)).astype(np.float32)
+    x[0, 5] = x[0, 600] = np.nan                  # NaN among values: the first NaN
+    x[1, :] = np.nan                              # all NaN: 0
+    x[2, :] = 0.0
+    x[2, 3] = -0.0                                # zeros of both signs: 0
+    x[3, :] = -np.inf                             # all -inf: 0
+    x[4, 100] = np.inf
+    x[4, 700] = np.nan                            # NaN beats +inf
+    x[5, 9] = x[5, 20] = 50.0                     # ties: the lower id
+    x[6, v - 1] = np.nan                          # NaN in the last slot
+    bits = f32_to_bf16_bits(x)
+    want = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).argmax(-1).numpy()
+    for flags, temps in ((1, None), (0, np.zeros(10, np.float32))):
+        got = S.sample(bits, temps, None, None, None, np.full(10, 0.5, np.float32), flags)
+        np.testing.assert_array_equal(got, want)

@@ -48,6 +48,7 @@ struct DecodeArgs {
   float* ws_o; float* ws_lse;
   int* ws_nparts;  // partials per (sequence, kv head), written by the wave holding the segment's last page
   int batch, hq, hkv, group;
+  int nsub;       // 16-token pages per cache block (block_size / 16)
   int lmin;       // minimum pages per wave range
   int max_parts;  // partial slots per (sequence, head) in the workspace
   int nwaves;     // workgroups of the main kernel (the range count)
@@ -114,9 +115,11 @@ XV_INLINE LaneOffsets lane_offsets(int64_t tok_stride, int lane) {
   return o;
 }
 
-XV_INLINE void issue_page(char* buf, const DecodeArgs& a, int page, int kvh, int valid_rows,
+// One 16-token page: tokens 16*sub .. 16*sub + 15 of cache block `page`.
+XV_INLINE void issue_page(char* buf, const DecodeArgs& a, int page, int sub, int kvh, int valid_rows,
                           const LaneOffsets& lo) {
-  const int64_t base = (int64_t)page * a.page_stride + (int64_t)kvh * a.head_stride;
+  const int64_t base =
+      (int64_t)page * a.page_stride + (int64_t)sub * kPage * a.tok_stride + (int64_t)kvh * a.head_stride;
   const uint32_t bytes = (uint32_t)(((int64_t)(valid_rows - 1) * a.tok_stride + kD) * 2);
   const __amdgpu_buffer_rsrc_t rk = page_rsrc(a.kc + base, bytes);
   const __amdgpu_buffer_rsrc_t rv = page_rsrc(a.vc + base, bytes);
@@ -234,16 +237,21 @@ constexpr int kIdWindow = 128;
 
 // Uniform position of a page in the flat (sequence, kv head, page) space.
 struct Cursor {
-  int b, kvh, pg;  // sequence, kv head, page within the sequence
+  int b, kvh, pg;  // sequence, kv head, 16-token page within the sequence
+  int sub;         // pg modulo the 16-token pages of a cache block
   int npb, ctx;    // pages and tokens of sequence b
 };
 
 // The next page of the flat space.  Sequences without pages (cache_seqlens
 // 0) hold no flat positions and are stepped over; the caller only advances
 // while a next page exists, and the loop is bounded by the batch regardless.
-XV_INLINE void advance(Cursor& c, const int* pref, const int* sl, int hkv, int batch) {
-  if (++c.pg < c.npb) return;
+XV_INLINE void advance(Cursor& c, const int* pref, const int* sl, int hkv, int batch, int nsub) {
+  if (++c.pg < c.npb) {
+    if (++c.sub == nsub) c.sub = 0;
+    return;
+  }
   c.pg = 0;
+  c.sub = 0;
   if (++c.kvh < hkv) return;
   c.kvh = 0;
   do {
@@ -364,7 +372,7 @@ XV_INLINE void load_window(char* half, const DecodeArgs& a, __amdgpu_buffer_rsrc
       const int npb = pref[b + 1] - pref[b];
       const int r = (int)(f - (int64_t)a.hkv * pref[b]);
       const int kvh = r / npb;
-      off = (int)(((int64_t)b * a.bt_stride + (r - kvh * npb)) * 4);
+      off = (int)(((int64_t)b * a.bt_stride + (r - kvh * npb) / a.nsub) * 4);  // the page's cache block
     }
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rbt, (lds_void*)(half + 256 * j), 4, off, 0, 0, 0);
   }
@@ -465,6 +473,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
     const int r = (int)(f0 - (int64_t)a.hkv * pref[c0.b]);
     c0.kvh = __builtin_amdgcn_readfirstlane(r / c0.npb);
     c0.pg = __builtin_amdgcn_readfirstlane(r - c0.kvh * c0.npb);
+    c0.sub = __builtin_amdgcn_readfirstlane(c0.pg % a.nsub);
   }
   Cursor ic = c0, pc = c0;  // issue and process cursors
   const __amdgpu_buffer_rsrc_t rbt =
@@ -482,13 +491,13 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   auto issue = [&](int y, int slot, int page_id) {
     char* buf = lds + slot * BUF;
     if (y > issued) {
-      const bool newseg = issued < 0 || (advance(ic, pref, sl, a.hkv, a.batch), ic.pg == 0);
+      const bool newseg = issued < 0 || (advance(ic, pref, sl, a.hkv, a.batch, a.nsub), ic.pg == 0);
       issued = y;
       if (y % kIdWindow == 0 && y > 0)  // entering window k: request window k+1
         load_window(idtab + ((y / kIdWindow + 1) & 1) * (kIdWindow * 4), a, rbt, pref, f0, y + kIdWindow, n, lane);
       if (newseg) issue_q<G>(buf + kPageLds, a, ic.b, ic.kvh, lane);
     }
-    issue_page(buf, a, page_id, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
+    issue_page(buf, a, page_id, ic.sub, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
   };
 
   SplitState st;
@@ -505,7 +514,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
     const char* buf = lds + slot * BUF;
     if (x > 0) {
       const Cursor prev = pc;
-      advance(pc, pref, sl, a.hkv, a.batch);
+      advance(pc, pref, sl, a.hkv, a.batch, a.nsub);
       if (pc.pg == 0) {
         finish(prev);
         reset(st);
@@ -695,11 +704,17 @@ int waves_for(int group) {
 // Workspace layout: [partial counts int32, B*Hkv, padded to 256 B][partial outputs fp32][partial log2-sum-exp fp32]
 size_t counter_bytes(int batch, int num_kv_heads) { return ((size_t)batch * num_kv_heads * 4 + 255) / 256 * 256; }
 
-// Workspace of one launch of `batch` <= kMaxBatch sequences.
-size_t chunk_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_blocks_per_seq) {
-  const int lmin = min_range_pages(batch, num_q_heads, max_blocks_per_seq);
-  const int parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
+// Workspace of one launch of `batch` <= kMaxBatch sequences; max_pages counts
+// 16-token pages per sequence.
+size_t chunk_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int max_pages) {
+  const int lmin = min_range_pages(batch, num_q_heads, max_pages);
+  const int parts = (max_pages + lmin - 1) / lmin + 1;
   return counter_bytes(batch, num_kv_heads) + (size_t)batch * num_q_heads * parts * ((size_t)kD + 1) * sizeof(float);
+}
+
+// 16-token pages per sequence for a block table of max_blocks cache blocks.
+int64_t pages_per_seq(int max_blocks_per_seq, int block_size) {
+  return (int64_t)max_blocks_per_seq * (block_size > 0 && block_size % kPage == 0 ? block_size / kPage : 1);
 }
 
 // The largest one-launch workspace over every batch up to `batch` (launches
@@ -711,66 +726,41 @@ size_t chunk_workspace_bytes(int batch, int num_q_heads, int num_kv_heads, int m
 // allocated once, before the first (largest) capture.
 extern "C" size_t xv_paged_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
                                                  int max_blocks_per_seq, int block_size, int head_dim) {
-  (void)block_size;
   (void)head_dim;
-  if (batch <= 0 || max_blocks_per_seq <= 0 || num_kv_heads <= 0) return 256;
+  const int64_t pages = pages_per_seq(max_blocks_per_seq, block_size);
+  if (batch <= 0 || pages <= 0 || pages > INT32_MAX || num_kv_heads <= 0) return 256;
   size_t need = 256;
   for (int b = 1; b <= min(batch, kMaxBatch); ++b)
-    need = max(need, chunk_workspace_bytes(b, num_q_heads, num_kv_heads, max_blocks_per_seq));
+    need = max(need, chunk_workspace_bytes(b, num_q_heads, num_kv_heads, (int)pages));
   return need;
 }
 
-extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                                         const void* k_cache, const void* v_cache,
-                                         int64_t page_stride, int64_t tok_stride, int64_t head_stride,
-                                         const int32_t* block_tables, int64_t bt_stride,
-                                         const int32_t* cache_seqlens,
-                                         void* out, int64_t out_stride_tok,
-                                         void* workspace, size_t workspace_bytes,
-                                         int batch, int num_q_heads, int num_kv_heads, int head_dim,
-                                         int block_size, int max_blocks_per_seq, float scale,
-                                         hipStream_t stream) {
-  if (head_dim != kD || block_size != kPage || batch < 0 || num_kv_heads <= 0 ||
-      num_q_heads % num_kv_heads || max_blocks_per_seq <= 0)
-    return (int)hipErrorInvalidValue;
-  const int group = num_q_heads / num_kv_heads;
-  if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
-  if (batch == 0) return 0;
-  if (batch > kMaxBatch) {
-    // chunks of kMaxBatch sequences, in stream order on the same workspace
-    // (every call leaves its counters zero)
-    for (int c0 = 0; c0 < batch; c0 += kMaxBatch) {
-      const int rc = xv_paged_decode_attention(
-          (const bf16_t*)q + (int64_t)c0 * q_stride_tok, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride,
-          tok_stride, head_stride, block_tables + (int64_t)c0 * bt_stride, bt_stride, cache_seqlens + c0,
-          (bf16_t*)out + (int64_t)c0 * out_stride_tok, out_stride_tok, workspace, workspace_bytes,
-          min(kMaxBatch, batch - c0), num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale,
-          stream);
-      if (rc) return rc;
-    }
-    return 0;
-  }
-  // rows move by 16-byte LDS-DMA: aligned bases, strides in whole 16-byte units
-  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
-      (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
-    return (int)hipErrorInvalidValue;
-  if ((uintptr_t)out & 3 || out_stride_tok & 1) return (int)hipErrorInvalidValue;  // bf16 pairs stored as 4 bytes
-  const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_blocks_per_seq);
+namespace {
+
+// One launch pair (main kernel + merge) over batch <= kMaxBatch sequences,
+// arguments already validated.
+int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                 const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                 const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+                 int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+                 int num_kv_heads, int nsub, int max_pages, float scale, hipStream_t stream) {
+  const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_pages);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
+  const int group = num_q_heads / num_kv_heads;
   DecodeArgs a;
   a.q = (const bf16_t*)q; a.q_st = q_stride_tok; a.q_sh = q_stride_head;
   a.kc = (const bf16_t*)k_cache; a.vc = (const bf16_t*)v_cache;
   a.page_stride = page_stride; a.tok_stride = tok_stride; a.head_stride = head_stride;
   a.bt = block_tables; a.bt_stride = bt_stride; a.seqlens = cache_seqlens;
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
-  const int lmin = min_range_pages(batch, num_q_heads, max_blocks_per_seq);
-  a.max_parts = (max_blocks_per_seq + lmin - 1) / lmin + 1;
+  const int lmin = min_range_pages(batch, num_q_heads, max_pages);
+  a.max_parts = (max_pages + lmin - 1) / lmin + 1;
   a.ws_nparts = (int*)workspace;
   a.ws_o = (float*)((char*)workspace + counter_bytes(batch, num_kv_heads));
   a.ws_lse = a.ws_o + (size_t)batch * num_q_heads * a.max_parts * kD;
-  a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin;
+  a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin; a.nsub = nsub;
   // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
-  const int64_t max_total = (int64_t)batch * num_kv_heads * max_blocks_per_seq;
+  const int64_t max_total = (int64_t)batch * num_kv_heads * max_pages;
   a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
   switch (group) {
@@ -783,4 +773,53 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   merge_parts_kernel<<<dim3((unsigned)(batch * num_q_heads)), 64, 0, stream>>>(a);
   XV_CHECK_LAUNCH();
   return 0;
+}
+
+// Argument checks shared by both entry points, then the launches in chunks of
+// kMaxBatch sequences, in stream order on the same workspace.
+int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+               const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+               const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+               int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+               int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, float scale,
+               hipStream_t stream) {
+  if (head_dim != kD || block_size <= 0 || block_size % kPage || batch < 0 || num_kv_heads <= 0 ||
+      num_q_heads % num_kv_heads || max_blocks_per_seq <= 0)
+    return (int)hipErrorInvalidValue;
+  const int group = num_q_heads / num_kv_heads;
+  if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
+  const int64_t max_pages = pages_per_seq(max_blocks_per_seq, block_size);
+  if (max_pages > (1 << 24)) return (int)hipErrorInvalidValue;  // 256M tokens per sequence
+  // rows move by 16-byte LDS-DMA: aligned bases, strides in whole 16-byte units
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
+      (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
+    return (int)hipErrorInvalidValue;
+  if ((uintptr_t)out & 3 || out_stride_tok & 1) return (int)hipErrorInvalidValue;  // bf16 pairs stored as 4 bytes
+  if (batch == 0) return 0;
+  for (int c0 = 0; c0 < batch; c0 += kMaxBatch) {
+    const int rc = decode_chunk(
+        (const bf16_t*)q + (int64_t)c0 * q_stride_tok, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride,
+        tok_stride, head_stride, block_tables + (int64_t)c0 * bt_stride, bt_stride, cache_seqlens + c0,
+        (bf16_t*)out + (int64_t)c0 * out_stride_tok, out_stride_tok, workspace, workspace_bytes,
+        min(kMaxBatch, batch - c0), num_q_heads, num_kv_heads, block_size / kPage, (int)max_pages, scale, stream);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                         const void* k_cache, const void* v_cache,
+                                         int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                         const int32_t* block_tables, int64_t bt_stride,
+                                         const int32_t* cache_seqlens,
+                                         void* out, int64_t out_stride_tok,
+                                         void* workspace, size_t workspace_bytes,
+                                         int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                         int block_size, int max_blocks_per_seq, float scale,
+                                         hipStream_t stream) {
+  return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
+                    block_tables, bt_stride, cache_seqlens, out, out_stride_tok, workspace, workspace_bytes, batch,
+                    num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream);
 }

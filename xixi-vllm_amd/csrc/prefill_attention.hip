@@ -47,7 +47,7 @@ struct PrefillArgs {
   const bf16_t* q; int64_t q_st, q_sh;
   const bf16_t* k; const bf16_t* v; int64_t kv_st, kv_sh;
   const bf16_t* kc; const bf16_t* vc; int64_t page_stride, tok_stride, head_stride;
-  const int32_t* bt; int64_t bt_stride;
+  const int32_t* bt; int64_t bt_stride; int block_size;
   const int32_t* cu_q; const int32_t* cu_k;
   bf16_t* out; int64_t out_st;
   int hq, hkv, qblocks, batch;
@@ -70,14 +70,14 @@ XV_INLINE __amdgpu_buffer_rsrc_t rsrc(const bf16_t* base, uint32_t bytes) {
 // Wave w moves keys key0+16w .. +15 of the tile (one cache page when paged):
 // 4 LDS-DMA instructions for K and/or 4 for V, each 4 whole rows.
 template <bool PAGED, bool DO_K, bool DO_V>
-XV_INLINE void load_rows(char* buf, const PrefillArgs& a, int b, int kvh, int key0, int k0, int k_len, int page,
-                         int wave, int lane) {
+XV_INLINE void load_rows(char* buf, const PrefillArgs& a, int b, int kvh, int key0, int k0, int k_len,
+                         int64_t page_off, int wave, int lane) {
   const int j0 = key0 + 16 * wave;
   const int valid = min(16, k_len - j0);
   const bf16_t *kb, *vb;
   int64_t rs;  // row stride (elements)
   if (PAGED) {
-    const int64_t off = (int64_t)page * a.page_stride + (int64_t)kvh * a.head_stride;
+    const int64_t off = page_off + (int64_t)kvh * a.head_stride;
     kb = a.kc + off; vb = a.vc + off; rs = a.tok_stride;
   } else {
     const int64_t off = (int64_t)(k0 + j0) * a.kv_st + (int64_t)kvh * a.kv_sh;
@@ -289,10 +289,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
     for (int r = 0; r < 16; ++r) o[n][r] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  auto page_of = [&](int t) {
+  // element offset of the 16 keys j .. j + 15 (a 16-aligned run inside one
+  // cache block of block_size tokens): block bt[j / BS], token j % BS
+  auto page_of = [&](int t) -> int64_t {
     if (!PAGED) return 0;
     const int j = t * kKeys + 16 * wave;
-    return j < k_len ? __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.bt_stride + j / 16]) : 0;
+    if (j >= k_len) return 0;
+    const int blk = j / a.block_size;
+    const int64_t page = __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.bt_stride + blk]);
+    return page * a.page_stride + (int64_t)(j - blk * a.block_size) * a.tok_stride;
   };
   const LdsAddr ad = lds_addr(lds, lane);
   // S^T of one tile from K buffer PAR
@@ -382,7 +387,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(PrefillArgs a) {
   // therefore runs a tile ahead of V: iteration t loads K(t+2) into the K
   // buffer S(t) used and V(t+1) into the V buffer P(t-1) V(t-1) used, both
   // freed by the barrier at its top.
-  int pv_page = ntiles > 1 ? page_of(1) : 0, pk_page = ntiles > 2 ? page_of(2) : 0;
+  int64_t pv_page = ntiles > 1 ? page_of(1) : 0, pk_page = ntiles > 2 ? page_of(2) : 0;
   if (ntiles > 0) load_rows<PAGED, true, true>(lds, a, b, kvh, 0, k0, k_len, page_of(0), wave, lane);
   if (ntiles > 1) load_rows<PAGED, true, false>(lds + kBuf, a, b, kvh, kKeys, k0, k_len, pv_page, wave, lane);
   __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
@@ -451,7 +456,7 @@ extern "C" int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   const int group = num_q_heads / num_kv_heads;
   if (group != 1 && group != 2 && group != 4 && group != 8) return (int)hipErrorInvalidValue;
   if (block_tables) {
-    if (!k_cache || !v_cache || block_size != 16) return (int)hipErrorInvalidValue;
+    if (!k_cache || !v_cache || block_size <= 0 || block_size % 16) return (int)hipErrorInvalidValue;
     // K/V rows move by 16-byte LDS-DMA
     if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 15 || (page_stride | tok_stride | head_stride) & 7)
       return (int)hipErrorInvalidValue;
@@ -468,7 +473,7 @@ extern "C" int xv_prefill_attention(const void* q, int64_t q_stride_tok, int64_t
   a.k = (const bf16_t*)k; a.v = (const bf16_t*)v; a.kv_st = kv_stride_tok; a.kv_sh = kv_stride_head;
   a.kc = (const bf16_t*)k_cache; a.vc = (const bf16_t*)v_cache;
   a.page_stride = page_stride; a.tok_stride = tok_stride; a.head_stride = head_stride;
-  a.bt = block_tables; a.bt_stride = bt_stride;
+  a.bt = block_tables; a.bt_stride = bt_stride; a.block_size = block_size;
   a.cu_q = cu_seqlens_q; a.cu_k = cu_seqlens_k;
   a.out = (bf16_t*)out; a.out_st = out_stride_tok;
   a.hq = num_q_heads; a.hkv = num_kv_heads; a.batch = batch;

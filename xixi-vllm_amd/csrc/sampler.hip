@@ -7,6 +7,9 @@
 // top_k is at most 64 a two-launch top-k path (seg_topk / row_topk); all give
 // the same ids.
 //
+// Greedy rows follow torch.argmax, the reference's greedy: the lowest NaN id
+// if the row holds a NaN, else the largest logit at its lowest id.  Sampled
+// rows drop NaN logits (the reference's softmax would turn the whole row NaN).
 // Candidates are ordered by descending logit, ties by ascending id.  Every
 // candidate's probability mass is an exact int64
 //   q = trunc(2^40 * 2^d),  d = (l * (1/T) - x_max) * log2 e  (<= 0)
@@ -894,18 +897,24 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   const float temp = temps ? temps[b] : 1.0f;
   const bool greedy = (flags & XV_SAMPLE_ALL_GREEDY) || temp <= 1e-5f;
 
-  // ---- greedy: max value, then the lowest index holding it ----
+  // ---- greedy (torch.argmax): the lowest NaN id if the row holds a NaN,
+  // else the max value and the lowest index holding it ----
   if (greedy) {
-    // one pass: the lane's max and its lowest id, then the block's
+    // one pass: the lane's max, its lowest id and its lowest NaN id, then the block's
     float fm = -INFINITY;
-    uint32_t best = 0xffffffffu;
+    uint32_t best = 0xffffffffu, nan_id = 0xffffffffu;
     for_each_strided(row, V, vec_ok, [&](uint32_t bits, int id) {
-      if (!order_key(bits)) return;
+      if (!order_key(bits)) {
+        if (id < V) nan_id = min(nan_id, (uint32_t)id);  // ids past V are padding
+        return;
+      }
       const float v = bf16_to_f32(bits);
       if (v > fm) { fm = v; best = (uint32_t)id; }  // ids ascend within a lane: keeps the lowest
     });
+    nan_id = block_min_u(s, nan_id);
     const float gm = block_maxf(s, fm);
     best = block_min_u(s, fm == gm ? best : 0xffffffffu);
+    if (nan_id != 0xffffffffu) best = nan_id;
     if (t == 0) out_ids[b] = best == 0xffffffffu ? 0 : (int64_t)best;
     return;
   }
@@ -1003,15 +1012,27 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
 // All-greedy batches over several workgroups per row (a small batch would
 // leave most CUs idle with one workgroup per row).  A lane keeps the largest
 // logit of its ids and the lowest id holding it (float compares: -0 equals
-// +0, NaN never wins), as the one-workgroup path does.  Each workgroup then
-// folds its best into the row's 64-bit slot with one atomic max of
-//   order key << 32 | (2^32 - 1 - id)
-// (the largest logit wins, among equal logits the lowest id) and counts
+// +0), and its lowest NaN id, as the one-workgroup path does.  Each workgroup
+// then folds its best into the row's 64-bit slot with one atomic max of
+//   order key << 32 | (2^32 - 1 - id)      (greedy_word: NaN above every value)
+// (as torch.argmax: a NaN wins, then the largest logit, among equals the lowest id) and counts
 // itself in the row's arrival counter; the last workgroup of the row writes the id
 // and clears both words for the next call.  Every atomic is awaited before
 // the next one is issued, so the count is only bumped after the workgroup's
 // max has been performed.  Atomics on one cache line serialise, so each row
 // has its own line and is cut into at most 32 segments.
+// A lane's greedy candidate as one word that an integer max orders like
+// torch.argmax: key << 32 | (2^32 - 1 - id).  A NaN (nid >= 0, the lane's
+// lowest NaN id) takes key 0xffff, above every value's order key (at most
+// 0xff80, +inf); otherwise the lane's max value fm at its lowest id bid.  0
+// means no candidate.
+XV_INLINE unsigned long long greedy_word(float fm, int bid, int nid) {
+  if (nid >= 0) return (0xffffull << 32) | (0xffffffffu - (uint32_t)nid);
+  if (bid < 0) return 0ull;
+  const uint32_t fb = __float_as_uint(fm) >> 16;
+  return ((unsigned long long)order_key(fb == 0x8000u ? 0u : fb) << 32) | (0xffffffffu - (uint32_t)bid);
+}
+
 constexpr int kGreedyThreads = 256;
 constexpr int kGreedyUnroll = 8;
 constexpr int kGreedyLine = 16;  // u64 words per row: its slot, then its arrival counter, one 128-byte line
@@ -1026,7 +1047,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
   const int beg = blockIdx.x * seg_len, end = min(V, beg + seg_len);
   float fm = -INFINITY;
-  int bid = -1;
+  int bid = -1, nid = -1;
   constexpr int step = kGreedyThreads * 8;
   for (int i0 = beg + threadIdx.x * 8; i0 < end; i0 += kGreedyUnroll * step) {
     uint32_t bits[kGreedyUnroll][8];
@@ -1043,14 +1064,11 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
         const bool better = v > fm && i + k < end;  // ids ascend within a lane: keeps the lowest
         fm = better ? v : fm;
         bid = better ? i + k : bid;
+        nid = (nid < 0 && i + k < end && !order_key(bits[u][k])) ? i + k : nid;
       }
     }
   }
-  unsigned long long best = 0;
-  if (bid >= 0) {
-    const uint32_t fb = __float_as_uint(fm) >> 16;
-    best = ((unsigned long long)order_key(fb == 0x8000u ? 0u : fb) << 32) | (0xffffffffu - (uint32_t)bid);
-  }
+  unsigned long long best = greedy_word(fm, bid, nid);
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
     const unsigned long long y = __shfl_xor(best, o);
@@ -1074,7 +1092,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
     const unsigned int n = __hip_atomic_fetch_add(arrival, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (n == waves - 1) {
       const unsigned long long c = __hip_atomic_fetch_max(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out_ids[b] = c ? (int64_t)(0xffffffffu - (uint32_t)c) : 0;  // all-NaN row: 0, as the one-workgroup path
+      out_ids[b] = c ? (int64_t)(0xffffffffu - (uint32_t)c) : 0;  // (a row always has a candidate)
       __hip_atomic_store(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(arrival, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -1295,20 +1313,17 @@ __global__ __launch_bounds__(kSegThreads) void seg_stats_kernel(SegArgs a) {
   const bf16_t* row = a.logits + (int64_t)b * a.stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
   const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
-  if (a.temps[b] <= 1e-5f) {  // greedy row: the segment's best (value, then lowest id)
+  if (a.temps[b] <= 1e-5f) {  // greedy row: the segment's best (torch.argmax: NaN, else value; lowest id)
     float fm = -INFINITY;
-    int bid = -1;
+    int bid = -1, nid = -1;
     for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int id) {
       const float v = bf16_to_f32(bits);  // NaN (and padding) never compares greater
       const bool better = v > fm;         // ids ascend within a lane: keeps the lowest
       fm = better ? v : fm;
       bid = better ? id : bid;
+      nid = (nid < 0 && id < end && !order_key(bits)) ? id : nid;
     });
-    unsigned long long best = 0;
-    if (bid >= 0) {
-      const uint32_t fb = __float_as_uint(fm) >> 16;
-      best = ((unsigned long long)order_key(fb == 0x8000u ? 0u : fb) << 32) | (0xffffffffu - (uint32_t)bid);
-    }
+    unsigned long long best = greedy_word(fm, bid, nid);
     best = seg_max_ull(red, best);
     if (threadIdx.x == 0) a.seg_best[b * a.R + r] = best;
     return;
@@ -1788,12 +1803,21 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
                    (base + 2 * k + 1 < end ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
     }
   }
+  // A greedy row is torch.argmax: its NaNs (real ids only) take key 0xffff,
+  // above every value (at most 0xff80, +inf), so the list's first entry is
+  // the lowest NaN id when there is one.  Other rows drop NaN (key 0).
+  const bool greedy = a.temps[b] <= 1e-5f;
   uint32_t kmax = 0;
 #pragma unroll
   for (int v = 0; v < kTopVecs; ++v)
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t k0 = order_key(kw[v][k] & 0xffffu), k1 = order_key(kw[v][k] >> 16);
+      uint32_t k0 = order_key(kw[v][k] & 0xffffu), k1 = order_key(kw[v][k] >> 16);
+      if (greedy) {
+        const int id0 = beg + (v * kSegThreads + t) * 8 + 2 * k;
+        if (!k0 && v < nv && id0 < end) k0 = 0xffffu;
+        if (!k1 && v < nv && id0 + 1 < end) k1 = 0xffffu;
+      }
       kw[v][k] = k0 | k1 << 16;
       kmax = max(kmax, max(k0, k1));
     }
@@ -1941,7 +1965,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
   const unsigned long long c = fs.cand[lane];
   const int n = __popcll(__ballot(c != 0ull));
   const unsigned long long top = __shfl(c, 0);
-  if (p.greedy || n == 0) {  // argmax; a row of NaN only: 0, as the other paths
+  if (p.greedy || n == 0) {  // argmax (NaN first for greedy rows); a sampled row of NaN only: 0
     if (t == 0) a.out_ids[b] = n ? cand_id(top) : 0;
     return;
   }

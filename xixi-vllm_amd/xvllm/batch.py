@@ -6,7 +6,8 @@ H2D without blocking, so that graph replays read them in place.
 Decode metadata per sequence (batch.py:119-124): input id = last token,
 position = num_cached_tokens, slot = bt[pos // BS] * BS + pos % BS,
 cache_seqlens = pos + 1.  Rows padded up to a graph bucket get slot -1,
-seqlen 0 and block table -1 (batch.py:133-136).
+seqlen 0 and block table -1 (batch.py:133-136), and temperature 0, so that a
+sampler graph recorded for the bucket treats them as greedy rows.
 """
 from __future__ import annotations
 
@@ -47,7 +48,11 @@ def _pinned(shape, dtype, fill=None, pin=True):
 
 class Batch:
     def __init__(self, *, max_bs: int, max_tokens: int, max_blocks: int, vocab_size: int,
-                 device: torch.device, block_size: int) -> None:
+                 device: torch.device, block_size: int, num_blocks: int | None = None) -> None:
+        """`num_blocks`: pages in the KV pool; when given, every page id and
+        slot staged for the device is checked against it on the host (a bad
+        one raises ValueError instead of reaching a kernel)."""
+        self.num_blocks = num_blocks
         self.max_bs, self.max_tokens, self.max_blocks = max_bs, max_tokens, max_blocks
         self.vocab_size, self.device, self.block_size = vocab_size, device, block_size
         gpu = lambda shape, dt, fill=0: torch.full(shape, fill, dtype=dt, device=device)
@@ -107,16 +112,24 @@ class Batch:
             k = len(s.block_table)
             if self._row_sid[i] == s.seq_id and self._row_len[i] == k:
                 continue
+            if k > self.max_blocks:
+                raise ValueError(f"sequence {s.seq_id}: {k} blocks, the batch holds at most {self.max_blocks}")
             if self._row_sid[i] == s.seq_id and self._row_len[i] == k - 1 and k > 0:
                 bt[i, k - 1] = s.block_table[-1]
+                self._check_pages(s.seq_id, bt[i, k - 1 : k])
             else:
                 bt[i, :k] = s.block_table
                 bt[i, k:] = -1
+                self._check_pages(s.seq_id, bt[i, :k])
             self._row_sid[i], self._row_len[i] = s.seq_id, k
             dirty = True
         if dirty:
             n = len(seqs)
             self.block_tables[:n].copy_(self._h_bt[:n], non_blocking=True)
+
+    def _check_pages(self, seq_id: int, pages: np.ndarray) -> None:
+        if self.num_blocks is not None and pages.size and (pages.min() < 0 or pages.max() >= self.num_blocks):
+            raise ValueError(f"sequence {seq_id}: page id outside [0, {self.num_blocks}) in its block table")
 
     def _sync_sampling(self, seqs: list[SeqSchedule]) -> None:
         key = tuple((s.seq_id, s.temperature, s.top_p, s.top_k, s.min_p) for s in seqs)
@@ -150,6 +163,12 @@ class Batch:
         self._sync_block_tables(seqs)
         pos = np.fromiter((s.num_cached_tokens for s in seqs), np.int64, n)
         ids = np.fromiter((s.token_ids[-1] for s in seqs), np.int64, n)
+        short = pos // self.block_size >= self._row_len[:n]
+        if short.any() or (pos < 0).any():
+            i = int(np.argmax(short | (pos < 0)))
+            raise ValueError(f"sequence {seqs[i].seq_id}: position {int(pos[i])} has no page in its block table")
+        if ((ids < 0) | (ids >= self.vocab_size)).any():
+            raise ValueError(f"decode input id outside [0, {self.vocab_size})")
         rows = np.arange(n)
         slot = self._bt_np[rows, pos // self.block_size].astype(np.int64) * self.block_size + pos % self.block_size
         self._h_ids.numpy()[:n] = ids
@@ -165,6 +184,7 @@ class Batch:
             self.slot_mapping[n:pad_to].fill_(-1)
             self.cache_seqlens[n:pad_to].zero_()
             self.block_tables[n:pad_to].fill_(-1)
+            self.temperatures[n:pad_to].zero_()  # padding rows sample greedily (cheapest path)
             self._row_sid[n:pad_to] = -1
             self._row_len[n:pad_to] = -1
         self._staged()
@@ -181,11 +201,16 @@ class Batch:
             end = start + n
             ids[nt : nt + n] = s.token_ids
             pos[nt : nt + n] = np.arange(start, end)
+            if (end + self.block_size - 1) // self.block_size > len(s.block_table):
+                raise ValueError(f"sequence {s.seq_id}: positions up to {end} need more pages than its block table")
             slot[nt : nt + n] = slots_for_range(s.block_table, start, end, self.block_size)
+            self._check_pages(s.seq_id, np.asarray(s.block_table[: (end + self.block_size - 1) // self.block_size]))
             cuq[i + 1], cuk[i + 1] = cuq[i] + n, cuk[i] + end
             max_q, max_k = max(max_q, n), max(max_k, end)
             nt += n
         bs = len(seqs)
+        if nt and ((ids[:nt] < 0) | (ids[:nt] >= self.vocab_size)).any():
+            raise ValueError(f"prefill input id outside [0, {self.vocab_size})")
         self.input_ids[:nt].copy_(self._h_ids[:nt], non_blocking=True)
         self.positions[:nt].copy_(self._h_pos[:nt], non_blocking=True)
         self.slot_mapping[:nt].copy_(self._h_slot[:nt], non_blocking=True)

@@ -16,18 +16,26 @@ def store_kvcache(
 ) -> None:
     """k_cache[slot[i]] = key[i]; v_cache[slot[i]] = value[i]; slot -1 is skipped.
 
-    key/value: [N, Hkv, D] (any row strides with a unit last stride; the
-    reference makes them contiguous first, kv_ops.py:42-45 -- here the kernel
-    reads the strided view directly).  k_cache/v_cache: paged [NB, BS, Hkv, D]
-    views of the pool (any strides, written in place) or flat [num_slots, Hkv, D].
+    key/value: [N, Hkv, D].  The kernel reads strided views directly when
+    every head row starts 16-byte aligned with a unit last stride (the q/k/v
+    views of a fused qkv GEMM output); any other layout is first copied to a
+    fresh contiguous tensor, as the reference does for every input
+    (kv_ops.py:42-45).  k_cache/v_cache: paged [NB, BS, Hkv, D] views of the
+    pool (any strides, written in place) or flat [num_slots, Hkv, D].
     """
     require_cuda(key, value, k_cache, v_cache, slot_mapping)
     require_bf16(key, value, k_cache, v_cache)
     n, num_heads, head_dim = key.shape
     assert slot_mapping.numel() == n
-    for t in (key, value):
+    if head_dim % 8:
+        raise ValueError(f"head_dim must be a multiple of 8 (16-byte rows), got {head_dim}")
+
+    def readable(t):
         if t.stride(-1) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or not aligned16(t):
-            raise ValueError("key/value need a unit last stride and 16-byte aligned head rows")
+            return t.clone(memory_format=torch.contiguous_format)  # fresh, aligned allocation
+        return t
+
+    key, value = readable(key), readable(value)
     kc, vc = k_cache, v_cache
     if kc.stride() != vc.stride() or kc.shape != vc.shape:
         raise ValueError("k_cache and v_cache must share one layout")

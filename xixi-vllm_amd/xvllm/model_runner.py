@@ -1,21 +1,55 @@
 """Per-step driver on one GPU (reference src/compute/model_runner.py:23-312):
 decode (hipGraph replay per batch bucket, or eager) then prefill, sampling,
-and an asynchronous D2H copy of the sampled ids on a side stream."""
+and an asynchronous D2H copy of the sampled ids on a side stream.
+
+Unlike the reference, whose sampler runs eagerly after the decode graph
+(model_runner.py:206), the LM head and the sampler of a decode step replay
+as a second graph per (batch bucket, sampling mode): the mode is the set of
+kernel switches the batch's parameters select (all greedy, top-k / top-p /
+min-p in use, every top-k at most 64), so a graph is only replayed for
+batches it was recorded for.  Sampling parameters and the uniform draws are
+static buffers written before the replay."""
 from __future__ import annotations
 
 import torch
 
+from . import _C
 from .batch import Batch, SeqSchedule
 from .cuda_graph import HipGraphRunner
 from .kv_pool import KVPool
 from .layers.attention import AttnInputs, AttnMetadata, attention_context
-from .sampler import Sampler
+from .sampler import Sampler, reserve_workspace, sample
+
+
+class SampledIdOutOfRange(RuntimeError):
+    """A sampled id read back on the host lies outside [0, vocab): fed back as
+    the next step's input it would index past the embedding table."""
+
+
+def sample_mode(batch: Batch) -> int:
+    """The xv_sample flag set the staged batch selects (the reference's
+    host-side switches, batch.py:217-251)."""
+    if batch.all_greedy:
+        return _C.XV_SAMPLE_ALL_GREEDY
+    f = 0
+    if batch.use_top_k:
+        f |= _C.XV_SAMPLE_USE_TOP_K
+        if 0 < batch.max_top_k <= 64:
+            f |= _C.XV_SAMPLE_TOP_K_LE_64
+    if batch.use_top_p:
+        f |= _C.XV_SAMPLE_USE_TOP_P
+    if batch.use_min_p:
+        f |= _C.XV_SAMPLE_USE_MIN_P
+    return f
 
 
 class ModelRunner:
     def __init__(self, model, kv: KVPool, sampler: Sampler | None = None, *, max_num_seqs: int = 256,
                  max_num_batched_tokens: int = 8192, context_len: int = 4096, device=None,
-                 enforce_eager: bool = False) -> None:
+                 enforce_eager: bool = False, sample_modes: tuple[int, ...] = ()) -> None:
+        """`sample_modes`: sampling modes (see `sample_mode`) whose decode
+        sampler graphs are recorded up front besides the all-greedy one;
+        other modes are recorded at their first use."""
         self.model = model
         self.kv = kv
         self.sampler = sampler or Sampler()
@@ -33,16 +67,25 @@ class ModelRunner:
         max_blocks = (context_len + self.block_size - 1) // self.block_size
         self.batch = Batch(max_bs=self.max_bs, max_tokens=max(max_num_batched_tokens, self.max_bs),
                            max_blocks=max_blocks, vocab_size=cfg.vocab_size, device=self.device,
-                           block_size=self.block_size)
+                           block_size=self.block_size, num_blocks=kv.num_blocks)
+        self.vocab_size = cfg.vocab_size
         self._decode_out = torch.zeros(self.max_bs, self.hidden_size, dtype=kv.dtype, device=self.device)
+        self._decode_ids = torch.zeros(self.max_bs, dtype=torch.int64, device=self.device)
+        self._uniforms = torch.zeros(self.max_bs, dtype=torch.float32, device=self.device)
         self._copy_stream = torch.cuda.Stream(device=self.device)
         self._copy_event = torch.cuda.Event()
         self._sample_cpu = torch.empty(self.max_bs * 2, dtype=torch.int64, pin_memory=True)
         self.graph_runner: HipGraphRunner | None = None
+        self._sample_graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         if not enforce_eager:
+            # every workspace a graph will hold is allocated before the first capture
+            reserve_workspace(self.device, self.max_bs, cfg.vocab_size)
             self.graph_runner = HipGraphRunner(HipGraphRunner.make_bs_list(self.max_bs), self.device)
             with torch.inference_mode():
                 self.graph_runner.capture(self._decode_body)
+                for mode in dict.fromkeys((_C.XV_SAMPLE_ALL_GREEDY, *sample_modes)):
+                    for bs in reversed(self.graph_runner.bs_list):
+                        self._sample_graph(bs, mode)
 
     # ------------------------------------------------------------ decode
     def _decode_attn(self, bs: int) -> AttnInputs:
@@ -67,7 +110,52 @@ class ModelRunner:
         bs = len(seqs)
         pad_to = self.graph_runner._pad_bs(bs) if self.graph_runner is not None and bs <= self.max_bs else None
         self.batch.build_decode(seqs, pad_to=pad_to)
-        return self._sample_logits(self.decode_hidden(bs), bs)
+        if pad_to is None:
+            return self._sample_logits(self.decode_hidden(bs), bs)
+        self.decode_hidden(bs)
+        return self.decode_sample(bs)
+
+    # ------------------------------------------------------------ decode sampling graphs
+    def _sample_body(self, bs: int, mode: int) -> None:
+        """LM head + sampler over the first bs rows of the decode output into
+        the static id buffer, with the staged parameters and uniforms."""
+        logits = self.model.compute_logits(self._decode_out[:bs])
+        b = self.batch
+        greedy = bool(mode & _C.XV_SAMPLE_ALL_GREEDY)
+        sample(logits, None if greedy else b.temperatures[:bs], b.top_ps[:bs], b.top_ks[:bs], b.min_ps[:bs],
+               None if greedy else self._uniforms[:bs], all_greedy=greedy,
+               use_top_k=bool(mode & _C.XV_SAMPLE_USE_TOP_K), use_top_p=bool(mode & _C.XV_SAMPLE_USE_TOP_P),
+               use_min_p=bool(mode & _C.XV_SAMPLE_USE_MIN_P),
+               max_top_k=64 if mode & _C.XV_SAMPLE_TOP_K_LE_64 else 0, out=self._decode_ids[:bs])
+
+    def _sample_graph(self, bs: int, mode: int) -> torch.cuda.CUDAGraph:
+        """The sampler graph of bucket bs in `mode`, recorded on first use
+        (after one eager run that sizes the GEMM's library workspace; the
+        sampler workspace was reserved for max_bs rows beforehand)."""
+        key = (bs, mode)
+        graph = self._sample_graphs.get(key)
+        if graph is None:
+            torch.cuda.synchronize(self.device)
+            self._sample_body(bs, mode)
+            torch.cuda.synchronize(self.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, pool=self.graph_runner._mempool):
+                self._sample_body(bs, mode)
+            torch.cuda.synchronize(self.device)
+            self._sample_graphs[key] = graph
+        return graph
+
+    @torch.inference_mode()
+    def decode_sample(self, bs: int) -> torch.Tensor:
+        """Ids [bs] of the decode rows whose hidden states are in the decode
+        output, by the sampler graph of bs's bucket and the staged mode.  Rows
+        past bs up to the bucket are padding, staged greedy by build_decode."""
+        size = self.graph_runner.bucket(bs)
+        mode = sample_mode(self.batch)
+        if not mode & _C.XV_SAMPLE_ALL_GREEDY:  # rows past bs are greedy padding: no draw
+            self._uniforms[:bs].uniform_(generator=self.generator)
+        self._sample_graph(size, mode).replay()
+        return self._decode_ids[:bs]
 
     # ------------------------------------------------------------ prefill
     def _run_prefill(self, seqs: list[SeqSchedule]) -> torch.Tensor | None:
@@ -90,11 +178,14 @@ class ModelRunner:
             return self.model.argmax(hidden)
         logits = self.model.compute_logits(hidden)
         b = self.batch
+        # drawn like the graph path's (uniform_ from the same generator), into a
+        # buffer of its own: a decode sampler graph may still read _uniforms
+        u = torch.empty(bs, dtype=torch.float32, device=self.device).uniform_(generator=self.generator)
         return self.sampler(logits, b.temperatures[:bs], top_ps=b.top_ps[:bs], top_ks=b.top_ks[:bs],
                             min_ps=b.min_ps[:bs], generator=self.generator, all_greedy=b.all_greedy,
                             any_greedy=b.any_greedy,
                             use_top_k=b.use_top_k, use_top_p=b.use_top_p, use_min_p=b.use_min_p,
-                            max_top_k=b.max_top_k)
+                            max_top_k=b.max_top_k, uniforms=u)
 
     @torch.inference_mode()
     def run_forward(self, decodes: list[SeqSchedule], prefills: list[SeqSchedule]) -> tuple[int, int]:
@@ -125,12 +216,20 @@ class ModelRunner:
         return n_p, n_d
 
     def read_samples(self, n_p: int, n_d: int) -> tuple[list[int], list[int]]:
-        """(prefill ids, decode ids) of the step staged last."""
+        """(prefill ids, decode ids) of the step staged last.  Every id is
+        checked against [0, vocab) on the host before it is returned, so a
+        wrong id raises here instead of faulting the next step's embedding
+        gather when it is fed back."""
         self._copy_event.synchronize()
         ids = self._sample_cpu[: n_d + n_p].tolist()
+        bad = [(i, t) for i, t in enumerate(ids) if not 0 <= t < self.vocab_size]
+        if bad:
+            raise SampledIdOutOfRange(f"{len(bad)} sampled ids outside [0, {self.vocab_size}): "
+                                      f"first (row, id) {bad[:4]} of {n_d} decode + {n_p} prefill rows")
         return ids[n_d:], ids[:n_d]
 
     def destroy(self) -> None:
+        self._sample_graphs.clear()
         if self.graph_runner is not None:
             self.graph_runner.destroy()
             self.graph_runner = None

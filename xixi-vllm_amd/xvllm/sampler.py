@@ -3,7 +3,9 @@
 radix-select sampling kernel (one workgroup per row).
 
 Semantics follow the reference: temperature <= 1e-5 rows (or ``all_greedy``)
-take the argmax of the logits (lowest id on ties, as ``argmax``); otherwise
+take ``torch.argmax`` of the logits (a NaN counts as the maximum, so the
+lowest NaN id wins; otherwise the lowest id on ties).  Sampled rows drop NaN
+logits, where the reference's softmax would make the whole row NaN; otherwise
 the logits are scaled by 1/temperature and filtered by top-k, then top-p
 and min-p over the renormalised top-k set, keeping at least the best token.
 The reference draws with ``torch.multinomial`` / exponential noise; here the
@@ -24,17 +26,31 @@ from ._torch_glue import ptr, require_bf16, require_cuda, stream_of
 
 _WORKSPACE: dict[tuple[str, int | None], torch.Tensor] = {}
 
+# Workspaces replaced by a larger one stay allocated until the process ends:
+# a hipGraph captured on an earlier one keeps its pointer and replays onto it.
+_RETIRED: list[torch.Tensor] = []
+
 
 def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     """Per-device sampler workspace, zero-filled once and grown on demand (the
-    kernels leave it zero after every call).  Calls on one device share it and
-    must be ordered on one stream."""
+    kernels leave it zero after every call).  Growing must happen outside
+    graph capture: callers that capture size it first with `reserve_workspace`
+    for their largest batch (the size query never decreases with the batch).
+    Calls on one device share it and must be ordered on one stream."""
     key = (device.type, device.index)
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws
+
+
+def reserve_workspace(device: torch.device, max_batch: int, vocab: int) -> torch.Tensor:
+    """Allocate the sampler workspace for every call of up to `max_batch`
+    rows over `vocab` ids, before any graph that samples is captured."""
+    return _workspace(torch.device(device), _C.lib().xv_sampler_workspace_size(max_batch, vocab))
 
 
 def sample(
