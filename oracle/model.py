@@ -38,11 +38,18 @@ def decode_layer(w: dict, hidden, residual, positions, k_cache, v_cache, block_t
     O.store_kvcache(k, v, k_cache, v_cache, slots)
     attn = round_bf16(O.paged_decode_attention(q, k_cache, v_cache, block_tables, seqlens).astype(np.float32))
     attn = attn.reshape(t, hq * d)
+    h, residual = post_attention(w, attn, residual, eps)
+    return {"attn": attn, "hidden": h, "residual": residual}
+
+
+def post_attention(w: dict, attn, residual, eps: float):
+    """The rest of a decoder layer after attention (qwen3.py:66-72, 143-153):
+    o_proj, fused add + post-attention RMSNorm, gate_up, SiLU-and-mul, down.
+    Returns (layer output, residual stream)."""
     h = linear(attn, w["o_proj"])
     h, residual = O.fused_add_rmsnorm(h, residual, w["post_attention_layernorm"], eps)
     gu = linear(h, w["gate_up_proj"])
-    h = linear(O.silu_and_mul(gu), w["down_proj"])
-    return {"attn": attn, "hidden": h, "residual": residual}
+    return linear(O.silu_and_mul(gu), w["down_proj"]), residual
 
 
 def final_logits(hidden, residual, norm_w, lm_head, eps):

@@ -775,14 +775,11 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   return 0;
 }
 
-// Argument checks shared by both entry points, then the launches in chunks of
-// kMaxBatch sequences, in stream order on the same workspace.
-int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
-               const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
-               const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
-               int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
-               int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, float scale,
-               hipStream_t stream) {
+// Argument checks shared by both entry points (host only, no device call).
+int decode_check(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                 const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride, void* out,
+                 int64_t out_stride_tok, int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+                 int max_blocks_per_seq) {
   if (head_dim != kD || block_size <= 0 || block_size % kPage || batch < 0 || num_kv_heads <= 0 ||
       num_q_heads % num_kv_heads || max_blocks_per_seq <= 0)
     return (int)hipErrorInvalidValue;
@@ -795,7 +792,22 @@ int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const
       (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)out & 3 || out_stride_tok & 1) return (int)hipErrorInvalidValue;  // bf16 pairs stored as 4 bytes
-  if (batch == 0) return 0;
+  return 0;
+}
+
+// Checks, then the launches in chunks of kMaxBatch sequences, in stream order
+// on the same workspace.
+int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+               const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+               const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
+               int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
+               int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, float scale,
+               hipStream_t stream) {
+  const int rc0 = decode_check(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride,
+                               head_stride, out, out_stride_tok, batch, num_q_heads, num_kv_heads, head_dim,
+                               block_size, max_blocks_per_seq);
+  if (rc0 || batch == 0) return rc0;
+  const int64_t max_pages = pages_per_seq(max_blocks_per_seq, block_size);
   for (int c0 = 0; c0 < batch; c0 += kMaxBatch) {
     const int rc = decode_chunk(
         (const bf16_t*)q + (int64_t)c0 * q_stride_tok, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride,
