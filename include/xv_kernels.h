@@ -89,6 +89,29 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
                               hipStream_t stream);
 
 /*
+ * xv_paged_decode_attention without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture that must not
+ * call hipMalloc, tight serving loops, harnesses that forbid allocation).  It
+ * has no counterpart in the reference.  The workspace is a static device
+ * array of 48 MiB that each GPU the library runs on holds until the process
+ * ends; a call whose xv_paged_decode_workspace_size(batch, ...) exceeds it
+ * returns hipErrorInvalidValue before touching the device.  Nothing is
+ * allocated, freed or cleared (the kernels need no initial workspace
+ * contents).  Every call on one GPU shares that GPU's array: calls that
+ * overlap on one GPU (several streams or threads) race; order them on one
+ * stream.  Arguments and results are those of xv_paged_decode_attention.
+ */
+int xv_paged_decode_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                      const void* k_cache, const void* v_cache,
+                                      int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                      const int32_t* block_tables, int64_t bt_stride,
+                                      const int32_t* cache_seqlens,
+                                      void* out, int64_t out_stride_tok,
+                                      int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                      int block_size, int max_blocks_per_seq, float scale,
+                                      hipStream_t stream);
+
+/*
  * Varlen causal prefill attention, optionally reading K/V through the paged
  * cache (chunked prefill / cached prefix).  Causal masking is bottom-right
  * aligned: query i of sequence b (of q_len_b queries) sees keys

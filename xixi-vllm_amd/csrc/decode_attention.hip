@@ -25,6 +25,7 @@
 #include "xv_kernels.h"
 #include <math.h>
 #include <stdlib.h>
+#include <mutex>
 
 namespace {
 
@@ -833,5 +834,67 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
                                          hipStream_t stream) {
   return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
                     block_tables, bt_stride, cache_seqlens, out, out_stride_tok, workspace, workspace_bytes, batch,
+                    num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant: the workspace is `scratch`, a file-scope device
+// array of kScratchBytes that every GPU the library runs on holds until the
+// process ends.  Host code never uses the array's name as an address (on the
+// host it is only a stand-in): the device address is looked up once per
+// device with hipGetSymbolAddress, with that device current, and kept per
+// device.  The decode kernels need no initial workspace contents (counts and
+// partials are written before they are read), so nothing is cleared.  All
+// calls on one device share its array: calls that overlap on one GPU (other
+// streams, other threads) race.
+constexpr size_t kScratchBytes = (size_t)48 << 20;
+__device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+void* g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+hipError_t scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return hipSuccess;
+}
+}  // namespace
+
+extern "C" int xv_paged_decode_attention_noalloc(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                                 const void* k_cache, const void* v_cache,
+                                                 int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                                 const int32_t* block_tables, int64_t bt_stride,
+                                                 const int32_t* cache_seqlens,
+                                                 void* out, int64_t out_stride_tok,
+                                                 int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                                 int block_size, int max_blocks_per_seq, float scale,
+                                                 hipStream_t stream) {
+  // arguments and the workspace this call needs, checked before the device is touched
+  const int rc0 = decode_check(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride,
+                               head_stride, out, out_stride_tok, batch, num_q_heads, num_kv_heads, head_dim,
+                               block_size, max_blocks_per_seq);
+  if (rc0 || batch == 0) return rc0;
+  if (xv_paged_decode_workspace_size(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size, head_dim) >
+      kScratchBytes)
+    return (int)hipErrorInvalidValue;
+  void* ws = nullptr;
+  const hipError_t e = scratch_ptr(&ws);
+  if (e != hipSuccess) return (int)e;
+  return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
+                    block_tables, bt_stride, cache_seqlens, out, out_stride_tok, ws, kScratchBytes, batch,
                     num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream);
 }

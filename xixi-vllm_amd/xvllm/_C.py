@@ -23,6 +23,11 @@ SIGNATURES: dict[str, tuple] = {
         [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, i64, vp, sz,
          i32, i32, i32, i32, i32, i32, f32, vp],
     ),
+    "xv_paged_decode_attention_noalloc": (
+        i32,
+        [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, i64,
+         i32, i32, i32, i32, i32, i32, f32, vp],
+    ),
     "xv_prefill_attention": (
         i32,
         [vp, i64, i64, vp, vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, i64,
