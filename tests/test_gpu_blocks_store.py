@@ -143,3 +143,26 @@ def test_paged_decode_merge_partial_count_boundaries(dev, parts):
     if math.ceil(total / 4) <= 1024:  # ranges of exactly 4 pages while they fit the resident waves
         assert counts == [parts] * hkv, counts
     _close(f32(out).reshape(1, hq, d), want)
+
+
+def test_store_kvcache_multi_unit_waves_with_padding(dev):
+    """2049 tokens (4098 64-chunk units: the two-units-per-wave path, with an
+    odd unit count so the last wave has one) and padding slots (-1)."""
+    from xvllm.kv_ops import store_kvcache
+
+    g = gen(2049)
+    t, hkv, d, nb = 2049, 8, 128, 200
+    key, val = randn_bf16((t, hkv, d), g), randn_bf16((t, hkv, d), g)
+    slots = torch.randperm(nb * 16, generator=g)[:t].to(torch.int32)
+    slots[::5] = -1
+    slots[-1] = -1
+    kc, vc = randn_bf16((nb, 16, hkv, d), g), randn_bf16((nb, 16, hkv, d), g)
+    kr, vr = kc.clone(), vc.clone()
+    keep = slots >= 0
+    kr.view(-1, hkv, d)[slots[keep].long()] = key[keep]
+    vr.view(-1, hkv, d)[slots[keep].long()] = val[keep]
+    kg, vg = kc.to(dev), vc.to(dev)
+    store_kvcache(key.to(dev), val.to(dev), kg, vg, slots.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(kg.cpu().view(torch.int16), kr.view(torch.int16))
+    assert torch.equal(vg.cpu().view(torch.int16), vr.view(torch.int16))
