@@ -359,11 +359,16 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
             "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}
 
 
-def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
+def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bool = True, model=None):
     """Config 5: Qwen3-32B-shaped decode (64 layers, hidden 5120, 64 q / 8 kv
     heads, FFN 25600, random bf16 weights ~N(0,0.02)), batch 32 at context
-    32768; 16 requests share an 8192-token prefix mapped to the same KV pages,
-    16 are independent; top-p 0.95 over the 151936 vocab with seeded draws.
+    32768; 16 requests share an 8192-token prefix, 16 are independent; top-p
+    0.95 over the 151936 vocab with seeded draws.  The requests' pages come
+    from a radix prefix cache (xvllm.prefix_cache): the first shared request
+    publishes its blocks, the other 15 match the 512 prefix blocks and reuse
+    their pages.  With `cascade` the decode reads those pages once per kv head
+    (shared-prefix pass + per-row suffix, merged by log-sum-exp); without it
+    every row streams its whole table.
     The 64 layers' KV (275 GB per sequence, 243 GB of unique pages) does not
     fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
     layer i reads pool layer i % pool_layers: every layer streams the same
@@ -374,36 +379,45 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
     from xvllm.kv_pool import KVPool
     from xvllm.model_runner import ModelRunner
     from xvllm.models import Qwen3ForCausalLM
+    from xvllm.prefix_cache import RadixPrefixCache
 
     cfg = QWEN3_32B
     bsz, ctx, prefix, shared = 32, 32768, 8192, 16
     npg, ppg = ctx // PAGE, prefix // PAGE
     unique = ppg + shared * (npg - ppg) + (bsz - shared) * npg
+    g = torch.Generator().manual_seed(55)
+    pre_toks = torch.randint(0, cfg.vocab_size, (prefix,), generator=g).tolist()
+    cache = RadixPrefixCache(PAGE)
+    free = torch.randperm(unique, generator=g).tolist()
+    tables, hits = [], 0
+    for i in range(bsz):
+        own = torch.randint(0, cfg.vocab_size, (ctx - (prefix if i < shared else 0),), generator=g).tolist()
+        toks = (pre_toks + own) if i < shared else own
+        hit = cache.match(toks)
+        hits += len(hit)
+        bt = hit + [free.pop() for _ in range(npg - len(hit))]
+        held, _ = cache.insert(toks, bt)
+        assert held == bt[: len(held)]
+        tables.append((bt, toks[-1]))
+    assert hits == (shared - 1) * ppg and not free
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(dev):
-            model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+            if model is None:
+                model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
             kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
                         num_layers=pool_layers)
     finally:
         torch.set_default_dtype(torch.float32)
     kv.kv_cache.normal_()
-    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx, device=dev)
+    casc = dict(cascade_groups=2, cascade_max_prefix_blocks=ppg, cascade_min_blocks=64) if cascade else {}
+    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx, device=dev, **casc)
     runner.generator = torch.Generator(device=dev).manual_seed(5)
-    g = torch.Generator().manual_seed(55)
-    perm = torch.randperm(unique, generator=g).tolist()
-    prefix_pages, o = perm[:ppg], ppg
-    seqs = []
-    for i in range(bsz):
-        if i < shared:
-            bt = prefix_pages + perm[o : o + npg - ppg]
-            o += npg - ppg
-        else:
-            bt = perm[o : o + npg]
-            o += npg
-        seqs.append(SeqSchedule(seq_id=i, token_ids=[int(torch.randint(0, cfg.vocab_size, (1,), generator=g))],
-                                num_cached_tokens=ctx - 1, block_table=bt, temperature=1.0, top_p=0.95))
+    seqs = [SeqSchedule(seq_id=i, token_ids=[tok], num_cached_tokens=ctx - 1, block_table=bt, temperature=1.0,
+                        top_p=0.95) for i, (bt, tok) in enumerate(tables)]
     runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
+    if cascade:
+        assert runner.batch.cascade_rows == shared
 
     def step():
         runner.decode_hidden(bsz)
@@ -423,15 +437,20 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8) -> dict:
     per_tok_layer = cfg.num_key_value_heads * 128 * 2 * 2
     kv_seq = bsz * ctx * cfg.num_hidden_layers * per_tok_layer
     kv_unique = unique * PAGE * cfg.num_hidden_layers * per_tok_layer
-    roof_ms = (wbytes + kv_seq) / (HBM_PEAK_GBS * 1e9) * 1e3
+    kv_read = kv_unique if cascade else kv_seq  # per-step KV bytes the decode streams
+    roof_ms = (wbytes + kv_read) / (HBM_PEAK_GBS * 1e9) * 1e3
     runner.destroy()
     assert ids.shape[0] == bsz
+    del kv
+    torch.cuda.empty_cache()
     return {"model": "Qwen3-32B-shaped (64 layers, 64q/8kv, FFN 25600)", "batch": bsz, "context": ctx,
-            "shared_prefix": f"{shared} requests x {prefix} tokens", "sampling": "top-p 0.95 (T 1.0)",
-            "kv_pool_layers": pool_layers, "ms_per_step": round(ms, 3), "tok_per_s": round(bsz / (ms * 1e-3), 1),
-            "weight_bytes": wbytes, "kv_bytes_per_seq": kv_seq, "kv_bytes_unique_pages": kv_unique,
+            "shared_prefix": f"{shared} requests x {prefix} tokens (radix prefix cache)",
+            "attention": "cascade (shared blocks read once per kv head)" if cascade else "plain paged decode",
+            "sampling": "top-p 0.95 (T 1.0)", "kv_pool_layers": pool_layers, "ms_per_step": round(ms, 3),
+            "tok_per_s": round(bsz / (ms * 1e-3), 1), "weight_bytes": wbytes, "kv_bytes_per_seq": kv_seq,
+            "kv_bytes_unique_pages": kv_unique, "kv_bytes_read_per_step": kv_read,
             "roofline_ms": round(roof_ms, 3), "frac_of_roofline": round(roof_ms / ms, 4),
-            "achieved_GB/s_per_seq_bytes": round((wbytes + kv_seq) / (ms * 1e-3) / 1e9, 1)}
+            "achieved_GB/s": round((wbytes + kv_read) / (ms * 1e-3) / 1e9, 1)}, model
 
 
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
@@ -621,7 +640,9 @@ def main() -> int:
         print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
         return 0
     if args.config5_only:
-        print(json.dumps(decode_config5(torch, dev)))
+        c5, model = decode_config5(torch, dev, cascade=True)
+        c5p, model = decode_config5(torch, dev, cascade=False, model=model)
+        print(json.dumps({"config5": c5, "config5_plain": c5p}))
         return 0
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)
@@ -693,7 +714,10 @@ def main() -> int:
         line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
     if args.config5:
         torch.cuda.empty_cache()
-        line["config5"] = decode_config5(torch, dev)
+        line["config5"], model = decode_config5(torch, dev, cascade=True)
+        line["config5_plain"], model = decode_config5(torch, dev, cascade=False, model=model)
+        del model
+        torch.cuda.empty_cache()
     if not args.no_serve:
         torch.cuda.empty_cache()
         line["serve_greedy"], model = serve_e2e(torch, dev, sampled=False)

@@ -89,6 +89,49 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
                               hipStream_t stream);
 
 /*
+ * Shared-prefix (cascade) decode attention: xv_paged_decode_attention for a
+ * batch whose rows may share their first tokens' cache blocks, as a radix
+ * prefix cache maps them (the reference's prefix index,
+ * src/data/prefix/radix_index.py:20-129 with src/data/kv.py:40-119, shares
+ * the blocks; its decode, attention.py:91-99, still reads them once per row).
+ * Here each group's shared blocks are read once per kv head: a prefix pass
+ * attends all of the group's query rows to them (MFMA, 16 rows per tile),
+ * the per-row suffix runs through the decode kernels, and the merge combines
+ * both by log-sum-exp.  Outputs equal xv_paged_decode_attention's up to
+ * fp32 summation order.
+ *   prefix_tokens[b]: tokens of row b covered by its group's prefix pass, a
+ *     multiple of block_size (0: the row has no shared prefix); every row
+ *     with prefix_tokens > 0 belongs to exactly one group, whose rows all have
+ *     the same prefix_tokens and the same first prefix_tokens / block_size
+ *     block ids; prefix_tokens[b] <= cache_seqlens[b] and
+ *     <= max_prefix_blocks * block_size.
+ *   group_info: int32 [num_groups][4], 16-byte aligned; group g's record is
+ *     {first index into group_rows, number of rows, its first batch row,
+ *     prefix_tokens of its rows}: the batch rows of group g are
+ *     group_rows[info.x .. info.x + info.y), at most 128 / (Hq / Hkv) of
+ *     them (further rows are not attended by the prefix pass: split larger
+ *     groups), info.z == group_rows[info.x].  Empty groups (info.y == 0) are
+ *     allowed, so a caller recording a graph can pass a fixed num_groups.
+ *   workspace: xv_cascade_decode_workspace_size(batch, ...) bytes, 256-byte
+ *     aligned; no initial contents.  batch <= 256.
+ * Other arguments, supported shapes and errors as xv_paged_decode_attention.
+ */
+size_t xv_cascade_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                        int max_blocks_per_seq, int block_size, int head_dim);
+int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                const void* k_cache, const void* v_cache,
+                                int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                const int32_t* block_tables, int64_t bt_stride,
+                                const int32_t* cache_seqlens, const int32_t* prefix_tokens,
+                                const int32_t* group_info, const int32_t* group_rows,
+                                int num_groups, int max_prefix_blocks,
+                                void* out, int64_t out_stride_tok,
+                                void* workspace, size_t workspace_bytes,
+                                int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                int block_size, int max_blocks_per_seq, float scale,
+                                hipStream_t stream);
+
+/*
  * xv_paged_decode_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture that must not
  * call hipMalloc, tight serving loops, harnesses that forbid allocation).  It

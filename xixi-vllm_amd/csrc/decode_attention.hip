@@ -26,6 +26,7 @@
 #include <math.h>
 #include <stdlib.h>
 #include <mutex>
+#include <type_traits>
 
 namespace {
 
@@ -54,6 +55,14 @@ struct DecodeArgs {
   int max_parts;  // partial slots per (sequence, head) in the workspace
   int nwaves;     // workgroups of the main kernel (the range count)
   float scale_log2;
+  // Cascade (shared-prefix) decode; pre_tokens == nullptr otherwise.  Row b's
+  // first pre_tokens[b] tokens were attended by the prefix pass, whose
+  // partials (normalised output, log2-sum-exp) sit at pre_o / pre_lse slot
+  // (chunk * batch + b) * hq + h; bt and seqlens then describe the
+  // suffix only, and every suffix segment of such a row leaves a partial.
+  const int32_t* pre_tokens;
+  int pre_chunk_pages;  // prefix pages per prefix-pass chunk
+  const bf16_t* pre_o; const float* pre_lse;  // prefix outputs in bf16 (halves the pass's store traffic)
 };
 
 // Both K and V of a page travel HBM -> LDS by LDS-DMA (buffer_load ... lds:
@@ -117,7 +126,9 @@ XV_INLINE LaneOffsets lane_offsets(int64_t tok_stride, int lane) {
 }
 
 // One 16-token page: tokens 16*sub .. 16*sub + 15 of cache block `page`.
-XV_INLINE void issue_page(char* buf, const DecodeArgs& a, int page, int sub, int kvh, int valid_rows,
+// (A is any argument record with the cache fields kc, vc and strides.)
+template <typename A>
+XV_INLINE void issue_page(char* buf, const A& a, int page, int sub, int kvh, int valid_rows,
                           const LaneOffsets& lo) {
   const int64_t base =
       (int64_t)page * a.page_stride + (int64_t)sub * kPage * a.tok_stride + (int64_t)kvh * a.head_stride;
@@ -150,9 +161,12 @@ constexpr float kLazy = 8.0f;
 
 // Value of head (4g+RR)%G -- the head of O row 4g+RR -- for a per-head value
 // that is equal across the four 16-lane rows: lane (4g+RR)%G of this row.
+// G == 16 is the cascade prefix pass: 16 distinct query rows per tile, so
+// row 4g+RR's value sits in lane 4g+RR of the 16-lane row, which depends on g.
 template <int G, int RR>
 XV_INLINE float head_of_row(float x, int g) {
-  if constexpr (G == 8) return (g & 1) ? row_bcast<(4 + RR) % 8>(x) : row_bcast<RR % 8>(x);
+  if constexpr (G == 16) return __shfl(x, 20 * g + RR);
+  else if constexpr (G == 8) return (g & 1) ? row_bcast<(4 + RR) % 8>(x) : row_bcast<RR % 8>(x);
   else return row_bcast<RR % G>(x);
 }
 
@@ -164,39 +178,56 @@ XV_INLINE void rescale_row(SplitState& st, float alpha, int g) {
   for (int n = 0; n < 8; ++n) st.o[n][RR] *= ar;
 }
 
-template <int G, int NB>
-XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
-                            int page_tok0, int ctx, float scale_log2, int lane) {
-  const int g = lane >> 4;
-  // The page arrived by LDS-DMA; the 8 VMEM operations of each of the
-  // NB-1 pages issued after it may still be in flight: vmcnt(8*(NB-1))
-  // waits exactly for this page.  Waits and reads are one asm block so that
-  // the compiler, which cannot tell the LDS buffers apart, adds no wait of
-  // its own on the loads in flight.
-  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+// K (A operands of S^T) and transposed V (B operands of O) of one page from
+// its LDS image.  VM >= 0: first wait until at most VM vector-memory
+// operations are outstanding (the page's LDS-DMA); the wait and the reads are
+// one asm block so that the compiler, which cannot tell the LDS buffers apart,
+// adds no wait of its own on the loads in flight.  VM < 0: no vmcnt wait (the
+// caller already waited and synchronised the workgroup).
+struct PageRegs {
   bf16x8_t kr[4];
   short4_t vt[8];
-  __asm__ __volatile__(
-      "s_waitcnt vmcnt(%24)\n\t"
-      "ds_read_b128 %0, %12\n\t"
-      "ds_read_b128 %1, %13\n\t"
-      "ds_read_b128 %2, %14\n\t"
-      "ds_read_b128 %3, %15\n\t"
-      "ds_read_b64_tr_b16 %4, %16\n\t"
-      "ds_read_b64_tr_b16 %5, %17\n\t"
-      "ds_read_b64_tr_b16 %6, %18\n\t"
-      "ds_read_b64_tr_b16 %7, %19\n\t"
-      "ds_read_b64_tr_b16 %8, %20\n\t"
-      "ds_read_b64_tr_b16 %9, %21\n\t"
-      "ds_read_b64_tr_b16 %10, %22\n\t"
-      "ds_read_b64_tr_b16 %11, %23\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(kr[0]), "=&v"(kr[1]), "=&v"(kr[2]), "=&v"(kr[3]), "=&v"(vt[0]), "=&v"(vt[1]), "=&v"(vt[2]),
-        "=&v"(vt[3]), "=&v"(vt[4]), "=&v"(vt[5]), "=&v"(vt[6]), "=&v"(vt[7])
-      : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),
-        "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),
-        "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7]), "n"(8 * (NB - 1))
-      : "memory");
+};
+template <int VM>
+XV_INLINE void read_page(PageRegs& pr, const char* buf, const LaneOffsets& lo) {
+  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+#define XV_PAGE_READS                                                                                   \
+  "ds_read_b128 %0, %12\n\t"                                                                            \
+  "ds_read_b128 %1, %13\n\t"                                                                            \
+  "ds_read_b128 %2, %14\n\t"                                                                            \
+  "ds_read_b128 %3, %15\n\t"                                                                            \
+  "ds_read_b64_tr_b16 %4, %16\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %5, %17\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %6, %18\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %7, %19\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %8, %20\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %9, %21\n\t"                                                                      \
+  "ds_read_b64_tr_b16 %10, %22\n\t"                                                                     \
+  "ds_read_b64_tr_b16 %11, %23\n\t"                                                                     \
+  "s_waitcnt lgkmcnt(0)"
+#define XV_PAGE_OPERANDS                                                                                \
+  : "=&v"(pr.kr[0]), "=&v"(pr.kr[1]), "=&v"(pr.kr[2]), "=&v"(pr.kr[3]), "=&v"(pr.vt[0]), "=&v"(pr.vt[1]), \
+    "=&v"(pr.vt[2]), "=&v"(pr.vt[3]), "=&v"(pr.vt[4]), "=&v"(pr.vt[5]), "=&v"(pr.vt[6]), "=&v"(pr.vt[7])  \
+  : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),       \
+    "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),       \
+    "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7])
+  if constexpr (VM >= 0) {
+    __asm__ __volatile__("s_waitcnt vmcnt(%24)\n\t" XV_PAGE_READS XV_PAGE_OPERANDS, "n"(VM) : "memory");
+  } else {
+    __asm__ __volatile__(XV_PAGE_READS XV_PAGE_OPERANDS : "memory");
+  }
+#undef XV_PAGE_READS
+#undef XV_PAGE_OPERANDS
+}
+
+// S^T = K Q^T, the online softmax update and O += P V for one page already
+// in registers.  Tokens at page_tok0 + t >= ctx are masked.
+template <int G>
+XV_INLINE void page_math(SplitState& st, const PageRegs& pr, const bf16x8_t (&qb)[4], int page_tok0, int ctx,
+                         float scale_log2, int lane) {
+  const int g = lane >> 4;
+  const bf16x8_t (&kr)[4] = pr.kr;
+  const short4_t (&vt)[8] = pr.vt;
   // ---- S^T = K Q^T ----
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -231,6 +262,17 @@ XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& 
   // ---- O += P V ----
 #pragma unroll
   for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
+}
+
+template <int G, int NB>
+XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
+                            int page_tok0, int ctx, float scale_log2, int lane) {
+  // The page arrived by LDS-DMA; the 8 VMEM operations of each of the
+  // NB-1 pages issued after it may still be in flight: vmcnt(8*(NB-1))
+  // waits exactly for this page.
+  PageRegs pr;
+  read_page<8 * (NB - 1)>(pr, buf, lo);
+  page_math<G>(st, pr, qb, page_tok0, ctx, scale_log2, lane);
 }
 
 // Stream positions per half of the page-id table.
@@ -506,7 +548,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   bf16x8_t qb[4];
   auto finish = [&](const Cursor& c) {
     const int64_t seg0 = (int64_t)a.hkv * pref[c.b] + (int64_t)c.kvh * c.npb;
-    const bool full = seg0 >= f0 && seg0 + c.npb <= f0 + n;
+    // a row with a shared prefix always leaves a partial: the merge combines it with the prefix pass's
+    const bool pre = a.pre_tokens != nullptr && __builtin_amdgcn_readfirstlane(a.pre_tokens[c.b]) > 0;
+    const bool full = seg0 >= f0 && seg0 + c.npb <= f0 + n && !pre;
     const int part = (int)(blockIdx.x - seg0 / L);
     finish_segment<G>(a, st, c.b, c.kvh, full, part, lane);
     if (lane == 0 && seg0 + c.npb <= f0 + n) a.ws_nparts[c.b * a.hkv + c.kvh] = full ? 1 : part + 1;
@@ -550,63 +594,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
   XV_DECODE_TIMESTAMP(2);
 }
 
-// Merge the partials of one (sequence, query head) with one wave.  Also
-// writes the zero output of padding rows (cache_seqlens 0).  The partial
-// count comes from the main kernel.  The count, the sequence length, the
-// first kFastParts partials (the common splits, 2 dims per lane) and the
-// log2-sum-exp of partial `lane` are loaded together, so a merge of up to
-// kFastParts partials costs one memory round trip.  More partials: lane j holds partial j's weight
-// (j < 64, then j - 64, j - 128 in two more registers); four groups of 16
-// lanes take every fourth partial, 8 dims per lane, eight partials per batch
-// of loads, and the groups are summed by lane swaps.
+// Cascade decode: prefix-pass partials per (sequence, query head).
+constexpr int kCascMaxChunks = 32;
+
+// Weighted merge of n partials of one (sequence, query head) by one wave:
+// lane j holds partial j's weight (j < 64, then j - 64, j - 128 in two more
+// registers); four groups of 16 lanes take every fourth partial, 8 dims per
+// lane, 32 partials per batch of loads with two batches in flight, and the
+// groups are summed by lane swaps.  part_vals(j, i, lo, hi) loads values
+// 8i .. 8i + 7 of partial j, part_lse(j) is its log2-sum-exp; n <= kMergeMaxParts.
 constexpr int kMergeMaxParts = 192;
-constexpr int kFastParts = 4;  // partial counts merged from the first memory round trip
-__global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
-  const int b = blockIdx.x / a.hq;
-  const int h = blockIdx.x - b * a.hq;
-  const int lane = threadIdx.x;
-  const int d = lane * 2;
-  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
-  const int ctx = a.seqlens[b];
-  const int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
-  // speculative: the first kFastParts rows (clamped to max_parts - 1: rows
-  // below max_parts exist in every workspace, and max_parts >= 2)
-  float lf[kFastParts];
-  float2 vf[kFastParts];
-#pragma unroll
-  for (int r = 0; r < kFastParts; ++r) {
-    const int64_t row = row0 + min(r, a.max_parts - 1);
-    lf[r] = a.ws_lse[row];
-    vf[r] = *reinterpret_cast<const float2*>(a.ws_o + row * kD + d);
-  }
-  const float lmine = lane < a.max_parts ? a.ws_lse[row0 + lane] : -INFINITY;
-  bf16_t* orow = a.out + (int64_t)b * a.out_st + (int64_t)h * kD;
-  if (ctx <= 0) {
-    *reinterpret_cast<uint32_t*>(orow + d) = 0u;
-    return;
-  }
-  if (n <= 1) return;
-  if (n <= kFastParts) {
-    float mx = lf[0];
-#pragma unroll
-    for (int r = 1; r < kFastParts; ++r) mx = r < n ? fmaxf(mx, lf[r]) : mx;
-    float den = 0.f, ox = 0.f, oy = 0.f;
-#pragma unroll
-    for (int r = 0; r < kFastParts; ++r) {
-      if (r >= n) break;  // rows past n hold stale data (even NaN): never touched
-      const float w = __builtin_amdgcn_exp2f(lf[r] - mx);
-      den += w;
-      ox += w * vf[r].x;
-      oy += w * vf[r].y;
-    }
-    const float inv = 1.0f / den;
-    *reinterpret_cast<uint32_t*>(orow + d) = pack_bf16x2(ox * inv, oy * inv);
-    return;
-  }
-  // weights: lane j holds partials j, 64 + j, 128 + j
-  const float la = lane < n ? lmine : -INFINITY;
-  const float lb = 64 + lane < n ? a.ws_lse[row0 + 64 + lane] : -INFINITY;
-  const float lc = 128 + lane < n ? a.ws_lse[row0 + 128 + lane] : -INFINITY;
+// lse_lane: partial `lane`'s log2-sum-exp when the caller loaded it already
+// (HAVE_LANE), so that it need not wait for a load after learning n.
+template <bool HAVE_LANE, typename PV, typename PL>
+XV_INLINE void merge_general(int n, PV part_vals, PL part_lse, float lse_lane, bf16_t* orow, int lane) {
+  const float la = lane < n ? (HAVE_LANE ? lse_lane : part_lse(lane)) : -INFINITY;
+  const float lb = 64 + lane < n ? part_lse(64 + lane) : -INFINITY;
+  const float lc = 128 + lane < n ? part_lse(128 + lane) : -INFINITY;
   float mx = fmaxf(la, fmaxf(lb, lc));
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -618,15 +622,10 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
   const int g = lane >> 4, i = lane & 15;  // group g: partials g, g + 4, ...; dims 8i .. 8i + 7
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  // batches of 32 partials (8 per group), two in flight: the next batch's
-  // loads are issued before the current one is folded in
   auto load = [&](float4 (&v)[8][2], int j0) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      const int j = min(j0 + 4 * k + g, n - 1);
-      const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
-      v[k][0] = src[0];
-      v[k][1] = src[1];
+      part_vals(min(j0 + 4 * k + g, n - 1), i, v[k][0], v[k][1]);
     }
   };
   auto fold = [&](const float4 (&v)[8][2], int j0) {
@@ -665,6 +664,93 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   }
 }
 
+// Merge the partials of one (sequence, query head) with one wave.  Also
+// writes the zero output of padding rows (cache_seqlens 0).  The partial
+// count comes from the main kernel.  The count, the sequence length, the
+// first kFastParts partials (the common splits, 2 dims per lane) and the
+// log2-sum-exp of partial `lane` are loaded together, so a merge of up to
+// kFastParts partials costs one memory round trip.  More partials take
+// merge_general.  Cascade rows (a shared prefix) merge the suffix partials
+// with the prefix pass's chunk partials.
+constexpr int kFastParts = 4;  // partial counts merged from the first memory round trip
+__global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
+  const int b = blockIdx.x / a.hq;
+  const int h = blockIdx.x - b * a.hq;
+  const int lane = threadIdx.x;
+  const int d = lane * 2;
+  const int64_t row0 = ((int64_t)b * a.hq + h) * a.max_parts;
+  const int ctx = a.seqlens[b];
+  int n = a.ws_nparts[b * a.hkv + h / a.group];  // stale when ctx <= 0: not used then
+  bf16_t* orow = a.out + (int64_t)b * a.out_st + (int64_t)h * kD;
+  if (a.pre_tokens != nullptr) {
+    const int pre_pages = a.pre_tokens[b] / kPage;
+    if (pre_pages > 0) {
+      n = ctx > 0 ? n : 0;
+      const int npre = (pre_pages + a.pre_chunk_pages - 1) / a.pre_chunk_pages;
+      // partial j >= n: prefix chunk j - n, rows chunk-major
+      const int64_t cstride = (int64_t)a.batch * a.hq, prow = (int64_t)b * a.hq + h;
+      merge_general<false>(
+          n + npre,
+          [&](int j, int i, float4& lo, float4& hi) {
+            if (j < n) {
+              const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
+              lo = src[0];
+              hi = src[1];
+            } else {  // prefix chunk partials are bf16
+              float f[8];
+              unpack8(load_vec8(a.pre_o + ((j - n) * cstride + prow) * kD + 8 * i), f);
+              lo = make_float4(f[0], f[1], f[2], f[3]);
+              hi = make_float4(f[4], f[5], f[6], f[7]);
+            }
+          },
+          [&](int j) { return j < n ? a.ws_lse[row0 + j] : a.pre_lse[(j - n) * cstride + prow]; }, 0.f, orow,
+          lane);
+      return;
+    }
+  }
+  // speculative: the first kFastParts rows (clamped to max_parts - 1: rows
+  // below max_parts exist in every workspace, and max_parts >= 2)
+  float lf[kFastParts];
+  float2 vf[kFastParts];
+#pragma unroll
+  for (int r = 0; r < kFastParts; ++r) {
+    const int64_t row = row0 + min(r, a.max_parts - 1);
+    lf[r] = a.ws_lse[row];
+    vf[r] = *reinterpret_cast<const float2*>(a.ws_o + row * kD + d);
+  }
+  const float lmine = lane < a.max_parts ? a.ws_lse[row0 + lane] : -INFINITY;
+  if (ctx <= 0) {
+    *reinterpret_cast<uint32_t*>(orow + d) = 0u;
+    return;
+  }
+  if (n <= 1) return;
+  if (n <= kFastParts) {
+    float mx = lf[0];
+#pragma unroll
+    for (int r = 1; r < kFastParts; ++r) mx = r < n ? fmaxf(mx, lf[r]) : mx;
+    float den = 0.f, ox = 0.f, oy = 0.f;
+#pragma unroll
+    for (int r = 0; r < kFastParts; ++r) {
+      if (r >= n) break;  // rows past n hold stale data (even NaN): never touched
+      const float w = __builtin_amdgcn_exp2f(lf[r] - mx);
+      den += w;
+      ox += w * vf[r].x;
+      oy += w * vf[r].y;
+    }
+    const float inv = 1.0f / den;
+    *reinterpret_cast<uint32_t*>(orow + d) = pack_bf16x2(ox * inv, oy * inv);
+    return;
+  }
+  merge_general<true>(
+      n,
+      [&](int j, int i, float4& lo, float4& hi) {
+        const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
+        lo = src[0];
+        hi = src[1];
+      },
+      [&](int j) { return a.ws_lse[row0 + j]; }, lmine, orow, lane);
+}
+
 // Minimum pages per wave range.  It bounds the partials per (sequence, head),
 // parts = ceil(max_blocks / lmin) + 1, by P: at most 129, and fewer when the
 // workspace for batch x q heads x P partials would pass kPartBudget.  Small
@@ -677,6 +763,192 @@ int min_range_pages(int batch, int num_q_heads, int max_blocks_per_seq) {
   const size_t per_part = (size_t)max(batch, 1) * max(num_q_heads, 1) * (kD + 1) * sizeof(float);
   const int P = (int)max((size_t)3, min((size_t)kMaxParts, kPartBudget / per_part));
   return max(4, (max_blocks_per_seq + P - 2) / (P - 1));
+}
+
+// ---------------------------------------------------------------------------
+// Cascade (shared-prefix) decode, prefix pass.  The sequences of a group share
+// their first P tokens: the same cache blocks, as a prefix cache maps them.
+// Instead of every member streaming those pages, one workgroup per (prefix
+// chunk, kv head, group) reads the chunk's pages once and attends the whole
+// group's query rows to them: R = members x G rows (at most kCascRows), in
+// 16-row tiles on the MFMA columns (each column its own row, G = 16 in the
+// page math), one tile per wave.  Pages arrive in sub-chunks of up to
+// kCascSub pages by LDS-DMA, all of a sub-chunk's loads issued at once (its
+// page ids fetched first), so each workgroup has up to 128 KB in flight; the
+// waves then run their tiles over the sub-chunk.  Each row's normalised
+// chunk output and its log2-sum-exp go to the prefix partial slots, which the merge
+// combines with the row's suffix partials.  The launch's last workgroups
+// write the suffix view of every row instead (block-table rows shifted past
+// the prefix blocks, suffix lengths) for the suffix decode.
+constexpr int kCascRows = 128;
+constexpr int kCascWaves = kCascRows / 16;  // one 16-row tile per wave
+constexpr int kCascSub = 16;                // pages per sub-chunk (128 KB of LDS)
+constexpr int kCascUnits = 2 * kCascSub / kCascWaves;  // (page, K or V) units each wave moves per sub-chunk
+
+struct CascadeArgs {
+  const bf16_t* q; int64_t q_st, q_sh;
+  const bf16_t* kc; const bf16_t* vc;
+  int64_t page_stride, tok_stride, head_stride;
+  const int32_t* bt; int64_t bt_stride;
+  const int32_t* seqlens;
+  int nsub, block_size, batch, max_blocks;
+  const int4* grp_info;     // per group: first index into grp_rows, rows, first row, prefix tokens
+  const int32_t* grp_rows;  // batch rows of each group
+  const int32_t* pre_tokens;
+  int num_groups, hq, hkv, chunk_pages, num_chunks, num_view;
+  bf16_t* pre_o; float* pre_lse;
+  int32_t* sbt; int32_t* ssl;  // suffix view: [batch, max_blocks] block table, [batch] lengths
+  float scale_log2;
+};
+
+XV_INLINE void cascade_suffix_view(const CascadeArgs& a, int v, int nview) {
+  for (int b = v; b < a.batch; b += nview) {
+    const int pre = max(a.pre_tokens[b], 0);
+    const int skip = pre / a.block_size;
+    for (int j = threadIdx.x; j < a.max_blocks; j += blockDim.x)
+      a.sbt[(int64_t)b * a.max_blocks + j] = j + skip < a.max_blocks ? a.bt[(int64_t)b * a.bt_stride + j + skip] : -1;
+    if (threadIdx.x == 0) a.ssl[b] = max(a.seqlens[b] - pre, 0);
+  }
+}
+
+template <int G>
+__global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(CascadeArgs a) {
+  __shared__ __attribute__((aligned(16))) char lds[kCascSub * kPageLds];
+  // the first num_view workgroups write the suffix view; then (chunk, group,
+  // kv head), chunk fastest: the workgroups of empty groups (a graph records a
+  // fixed group count) are interleaved with working ones instead of forming a
+  // tail of their own
+  const int w = (int)blockIdx.x - a.num_view;
+  if (w < 0) {
+    cascade_suffix_view(a, blockIdx.x, a.num_view);
+    return;
+  }
+  const int c = w % a.num_chunks, grp = (w / a.num_chunks) % a.num_groups,
+            kvh = w / (a.num_chunks * a.num_groups);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // one record gives everything the page loads need: the page ids are one
+  // round trip away, the q rows two (their batch rows first)
+  const int4 info = a.grp_info[grp];
+  const int r0 = __builtin_amdgcn_readfirstlane(info.x);
+  const int nm = __builtin_amdgcn_readfirstlane(min(info.y, kCascRows / G));
+  if (nm <= 0) return;
+  const int b0 = __builtin_amdgcn_readfirstlane(info.z);
+  const int npages = __builtin_amdgcn_readfirstlane(info.w) / kPage;
+  const int p0 = c * a.chunk_pages, p1 = min(npages, p0 + a.chunk_pages);
+  if (p0 >= p1) return;
+  const int R = nm * G;
+  const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
+  const int i = lane & 15, g = lane >> 4;
+  const bool active = wave * 16 < R;  // this wave's tile holds rows
+  const uint32_t bytes = (uint32_t)(((int64_t)(kPage - 1) * a.tok_stride + kD) * 2);
+  // unit u = wave + kCascWaves * j of a sub-chunk: page u / 2, its K rows (u even) or V rows (u odd)
+  auto issue_sub = [&](int s0, int n) {
+    int page[kCascUnits];
+#pragma unroll
+    for (int j = 0; j < kCascUnits; ++j) {  // the ids first: one wait for all of them
+      const int p = s0 + min((wave + kCascWaves * j) >> 1, n - 1);
+      page[j] = __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b0 * a.bt_stride + p / a.nsub]);
+    }
+#pragma unroll
+    for (int j = 0; j < kCascUnits; ++j) {
+      const int u = wave + kCascWaves * j;
+      const int k = min(u >> 1, n - 1);  // past the sub-chunk: its last page again (never read)
+      const int p = s0 + k;
+      const int64_t base = (int64_t)page[j] * a.page_stride + (int64_t)(p % a.nsub) * kPage * a.tok_stride +
+                           (int64_t)kvh * a.head_stride;
+      const __amdgpu_buffer_rsrc_t r = page_rsrc(((u & 1) ? a.vc : a.kc) + base, bytes);
+      char* dst = lds + (u >> 1) * kPageLds + ((u & 1) ? kVPageBytes : 0);
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g[s], 0, 0, kNontemporal);
+    }
+  };
+  // Q^T B operand of the wave's tile: column i = row 16 w + i, k = d-chunk 4s + g
+  bf16x8_t qb[4];
+  {
+    const int row = wave * 16 + i;
+    if (row < R) {
+      const int b = a.grp_rows[r0 + row / G];
+      const bf16_t* qr = a.q + (int64_t)b * a.q_st + (int64_t)(kvh * G + row % G) * a.q_sh;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const Vec8 v = load_vec8(qr + (4 * s + g) * 8);
+        __builtin_memcpy(&qb[s], &v, 16);
+      }
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qb[s] = bf16x8_t{};
+    }
+  }
+  SplitState st;
+  reset(st);
+  static_assert(kCascUnits == 4 && kCascWaves == 8, "the waits below count 4 LDS-DMA instructions per unit");
+  static_assert(kCascUnits * kCascWaves == 2 * kCascSub, "every (page, K or V) unit of a sub-chunk has one wave");
+  // A wave's units go out in order j = 0 .. kCascUnits - 1, unit j of every
+  // wave carrying pages 4j .. 4j + 3: once every wave has seen its first
+  // j + 1 units land (vmcnt), those pages are complete, so the tiles run over
+  // them while the later pages still stream in.
+  for (int s0 = p0; s0 < p1; s0 += kCascSub) {
+    const int n = min(kCascSub, p1 - s0);
+    issue_sub(s0, n);
+#pragma unroll
+    for (int j = 0; j < kCascUnits; ++j) {
+      if (j == 0) __asm__ __volatile__("s_waitcnt vmcnt(12)" ::: "memory");
+      else if (j == 1) __asm__ __volatile__("s_waitcnt vmcnt(8)" ::: "memory");
+      else if (j == 2) __asm__ __volatile__("s_waitcnt vmcnt(4)" ::: "memory");
+      else __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (active) {
+        for (int k = 4 * j; k < min(n, 4 * j + 4); ++k) {
+          PageRegs pr;
+          read_page<-1>(pr, lds + k * kPageLds, offs);
+          page_math<16>(st, pr, qb, 0, kPage, a.scale_log2, lane);
+        }
+      }
+    }
+    __syncthreads();  // the next sub-chunk overwrites the buffers
+  }
+  if (!active) return;
+  // Rows 16 w + 4 g + RR of O, normalised, go through LDS (the page buffers
+  // are free now) so that each row's 512 bytes leave as whole 16-byte pieces:
+  // the wave's 16 x 128 fp32 tile at w * 16 * kORow floats, rows padded to
+  // kORow floats to spread the banks.
+  constexpr int kORow = kD + 4;
+  float* tile = reinterpret_cast<float*>(lds) + wave * 16 * kORow;
+  const float lsum = xor32_sum(xor16_sum(st.l));
+  auto put = [&](auto rr_tag) {
+    constexpr int RR = decltype(rr_tag)::value;
+    const float lh = head_of_row<16, RR>(lsum, g);
+    const float mh = head_of_row<16, RR>(st.m, g);
+    const float inv = 1.0f / lh;
+    float* o = tile + (4 * g + RR) * kORow + i;
+#pragma unroll
+    for (int nn = 0; nn < 8; ++nn) o[16 * nn] = st.o[nn][RR] * inv;
+    const int row = wave * 16 + 4 * g + RR;
+    if (i == 0 && row < R) {
+      const int b = a.grp_rows[r0 + row / G];
+      a.pre_lse[((int64_t)c * a.batch + b) * a.hq + kvh * G + row % G] = mh + __log2f(lh);
+    }
+  };
+  put(std::integral_constant<int, 0>{});
+  put(std::integral_constant<int, 1>{});
+  put(std::integral_constant<int, 2>{});
+  put(std::integral_constant<int, 3>{});
+  // wave-private region: the wave's own LDS writes precede its reads
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_wave_barrier();
+  // lane l: rows 4k + l / 16, values 8 (l % 16) .. +7, stored as 8 bf16
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int rt = 4 * k + (lane >> 4);
+    const int row = wave * 16 + rt;
+    if (row >= R) break;
+    const int b = a.grp_rows[r0 + row / G];
+    const float* src = tile + rt * kORow + 8 * (lane & 15);
+    const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
+    const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+    store_vec8(a.pre_o + (((int64_t)c * a.batch + b) * a.hq + kvh * G + row % G) * kD + 8 * (lane & 15), pack8(f));
+  }
 }
 
 int waves_for(int group) {
@@ -740,11 +1012,19 @@ namespace {
 
 // One launch pair (main kernel + merge) over batch <= kMaxBatch sequences,
 // arguments already validated.
+struct CascadeParts {  // the prefix pass's partials for the merge (pre_tokens == nullptr: none)
+  const int32_t* pre_tokens = nullptr;
+  int chunk_pages = 1;
+  const bf16_t* pre_o = nullptr;
+  const float* pre_lse = nullptr;
+};
+
 int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                  const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
                  const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
                  int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
-                 int num_kv_heads, int nsub, int max_pages, float scale, hipStream_t stream) {
+                 int num_kv_heads, int nsub, int max_pages, float scale, hipStream_t stream,
+                 const CascadeParts& cp = CascadeParts()) {
   const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_pages);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
   const int group = num_q_heads / num_kv_heads;
@@ -764,6 +1044,7 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_pages;
   a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.pre_tokens = cp.pre_tokens; a.pre_chunk_pages = cp.chunk_pages; a.pre_o = cp.pre_o; a.pre_lse = cp.pre_lse;
   switch (group) {
     case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;
     case 2: paged_decode_kernel<2><<<a.nwaves, 64, 0, stream>>>(a); break;
@@ -835,6 +1116,104 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
                     block_tables, bt_stride, cache_seqlens, out, out_stride_tok, workspace, workspace_bytes, batch,
                     num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Cascade (shared-prefix) decode entry point.
+namespace {
+size_t al256(size_t x) { return (x + 255) / 256 * 256; }
+struct CascadeLayout {
+  size_t sbt, ssl, lse, o, dec, total;
+};
+CascadeLayout cascade_layout(int batch, int num_q_heads, int num_kv_heads, int max_blocks_per_seq, int block_size) {
+  CascadeLayout L;
+  L.sbt = 0;
+  L.ssl = al256((size_t)batch * max_blocks_per_seq * 4);
+  L.lse = L.ssl + al256((size_t)batch * 4);
+  L.o = L.lse + al256((size_t)batch * num_q_heads * kCascMaxChunks * 4);
+  L.dec = L.o + al256((size_t)batch * num_q_heads * kCascMaxChunks * kD * 2);
+  L.total = L.dec + chunk_workspace_bytes(batch, num_q_heads, num_kv_heads,
+                                          (int)pages_per_seq(max_blocks_per_seq, block_size));
+  return L;
+}
+}  // namespace
+
+extern "C" size_t xv_cascade_decode_workspace_size(int batch, int num_q_heads, int num_kv_heads,
+                                                   int max_blocks_per_seq, int block_size, int head_dim) {
+  (void)head_dim;
+  const int64_t pages = pages_per_seq(max_blocks_per_seq, block_size);
+  if (batch <= 0 || pages <= 0 || pages > INT32_MAX || num_kv_heads <= 0 || num_q_heads <= 0) return 256;
+  size_t need = 256;
+  for (int b = 1; b <= min(batch, kMaxBatch); ++b)  // never decreases with the batch
+    need = max(need, cascade_layout(b, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size).total);
+  return need;
+}
+
+extern "C" int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                           const void* k_cache, const void* v_cache,
+                                           int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                           const int32_t* block_tables, int64_t bt_stride,
+                                           const int32_t* cache_seqlens, const int32_t* prefix_tokens,
+                                           const int32_t* group_info, const int32_t* group_rows,
+                                           int num_groups, int max_prefix_blocks,
+                                           void* out, int64_t out_stride_tok,
+                                           void* workspace, size_t workspace_bytes,
+                                           int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                           int block_size, int max_blocks_per_seq, float scale,
+                                           hipStream_t stream) {
+  const int rc0 = decode_check(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride,
+                               head_stride, out, out_stride_tok, batch, num_q_heads, num_kv_heads, head_dim,
+                               block_size, max_blocks_per_seq);
+  if (rc0) return rc0;
+  if (batch > kMaxBatch || num_groups < 0 || num_groups > 65535 || max_prefix_blocks < 0 ||
+      max_prefix_blocks > max_blocks_per_seq || !prefix_tokens || (num_groups > 0 && (!group_info || !group_rows)) ||
+      ((uintptr_t)group_info & 15))
+    return (int)hipErrorInvalidValue;
+  if (batch == 0) return 0;
+  const CascadeLayout Lw = cascade_layout(batch, num_q_heads, num_kv_heads, max_blocks_per_seq, block_size);
+  if (workspace == nullptr || workspace_bytes < Lw.total || (uintptr_t)workspace & 255)
+    return (int)hipErrorInvalidValue;
+  char* ws = (char*)workspace;
+  int32_t* sbt = (int32_t*)(ws + Lw.sbt);
+  int32_t* ssl = (int32_t*)(ws + Lw.ssl);
+  float* pre_lse = (float*)(ws + Lw.lse);
+  bf16_t* pre_o = (bf16_t*)(ws + Lw.o);
+  const int nsub = block_size / kPage;
+  const int group = num_q_heads / num_kv_heads;
+  // 1. the prefix pass (at most kCascMaxChunks chunks of the longest prefix),
+  //    and in the launch's last z slice the suffix view of every row
+  const int max_pre_pages = max_prefix_blocks * nsub;
+  const int chunk_pages = max(4, (max_pre_pages + kCascMaxChunks - 1) / kCascMaxChunks);
+  {
+    CascadeArgs c;
+    c.q = (const bf16_t*)q; c.q_st = q_stride_tok; c.q_sh = q_stride_head;
+    c.kc = (const bf16_t*)k_cache; c.vc = (const bf16_t*)v_cache;
+    c.page_stride = page_stride; c.tok_stride = tok_stride; c.head_stride = head_stride;
+    c.bt = block_tables; c.bt_stride = bt_stride; c.seqlens = cache_seqlens;
+    c.nsub = nsub; c.block_size = block_size; c.batch = batch; c.max_blocks = max_blocks_per_seq;
+    c.grp_info = (const int4*)group_info; c.grp_rows = group_rows; c.pre_tokens = prefix_tokens;
+    c.num_groups = max_pre_pages > 0 ? num_groups : 0;
+    c.hq = num_q_heads; c.hkv = num_kv_heads; c.chunk_pages = chunk_pages;
+    c.pre_o = pre_o; c.pre_lse = pre_lse; c.sbt = sbt; c.ssl = ssl;
+    c.scale_log2 = scale * 1.4426950408889634f;
+    c.num_chunks = max(1, (max_pre_pages + chunk_pages - 1) / chunk_pages);
+    c.num_view = min(batch, 64);
+    const dim3 grid((unsigned)(c.num_groups * c.num_chunks * num_kv_heads + c.num_view));
+    switch (group) {
+      case 1: cascade_prefix_kernel<1><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+      case 2: cascade_prefix_kernel<2><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+      case 4: cascade_prefix_kernel<4><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+      default: cascade_prefix_kernel<8><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+    }
+    XV_CHECK_LAUNCH();
+  }
+  // 3. the suffix decode and the merge of suffix and prefix partials
+  CascadeParts cp;
+  cp.pre_tokens = prefix_tokens; cp.chunk_pages = chunk_pages; cp.pre_o = pre_o; cp.pre_lse = pre_lse;
+  return decode_chunk(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride, sbt,
+                      max_blocks_per_seq, ssl, out, out_stride_tok, ws + Lw.dec, Lw.total - Lw.dec, batch,
+                      num_q_heads, num_kv_heads, nsub, (int)pages_per_seq(max_blocks_per_seq, block_size), scale,
+                      stream, cp);
 }
 
 // ---------------------------------------------------------------------------

@@ -48,10 +48,16 @@ def _pinned(shape, dtype, fill=None, pin=True):
 
 class Batch:
     def __init__(self, *, max_bs: int, max_tokens: int, max_blocks: int, vocab_size: int,
-                 device: torch.device, block_size: int, num_blocks: int | None = None) -> None:
+                 device: torch.device, block_size: int, num_blocks: int | None = None,
+                 cascade_groups: int = 0, cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16,
+                 cascade_max_rows: int = 16) -> None:
         """`num_blocks`: pages in the KV pool; when given, every page id and
         slot staged for the device is checked against it on the host (a bad
-        one raises ValueError instead of reaching a kernel)."""
+        one raises ValueError instead of reaching a kernel).
+        `cascade_groups` > 0: decode builds also stage the batch's
+        shared-prefix groups (at most that many, of at most cascade_max_rows
+        rows, prefixes of cascade_min_blocks .. cascade_max_prefix_blocks
+        blocks) for the cascade decode."""
         self.num_blocks = num_blocks
         self.max_bs, self.max_tokens, self.max_blocks = max_bs, max_tokens, max_blocks
         self.vocab_size, self.device, self.block_size = vocab_size, device, block_size
@@ -91,6 +97,17 @@ class Batch:
         # step that runs decode and prefill stages both into the same buffers)
         self._h2d_done = torch.cuda.Event() if torch.device(device).type == "cuda" else None
         self._h2d_pending = False
+        # shared-prefix groups of the decode batch (static buffers a graph can hold)
+        self.cascade = None
+        self._casc_cfg = (cascade_groups, cascade_max_prefix_blocks or max_blocks, cascade_min_blocks,
+                          cascade_max_rows)
+        if cascade_groups > 0:
+            from .layers.attention import CascadePlan
+
+            self.cascade = CascadePlan(gpu((max_bs,), torch.int32), gpu((cascade_groups, 4), torch.int32),
+                                       gpu((max_bs,), torch.int32), cascade_groups, self._casc_cfg[1])
+            self._h_casc = _pinned((2 * max_bs + 4 * cascade_groups,), torch.int32, pin=pin)
+            self.cascade_rows = 0  # rows in shared-prefix groups in the last decode build
 
     def _wait_staging(self) -> None:
         if self._h2d_pending:
@@ -180,6 +197,8 @@ class Batch:
         self.slot_mapping[:n].copy_(self._h_slot[:n], non_blocking=True)
         self.cache_seqlens[:n].copy_(self._h_csl[:n], non_blocking=True)
         self._sync_sampling(seqs)
+        if self.cascade is not None:
+            self._stage_cascade(n, pos + 1, pad_to or n)
         if pad_to is not None and pad_to > n:
             self.slot_mapping[n:pad_to].fill_(-1)
             self.cache_seqlens[n:pad_to].zero_()
@@ -188,6 +207,25 @@ class Batch:
             self._row_sid[n:pad_to] = -1
             self._row_len[n:pad_to] = -1
         self._staged()
+
+    def _stage_cascade(self, n: int, seqlens: np.ndarray, rows: int) -> None:
+        from .prefix_cache import cascade_groups
+
+        groups, max_pre, min_blocks, max_rows = self._casc_cfg
+        pre, info, grp_rows = cascade_groups(self._bt_np[:n], seqlens, self.block_size, max_rows=max_rows,
+                                             min_blocks=min_blocks, max_groups=groups, max_prefix_blocks=max_pre)
+        h = self._h_casc.numpy()
+        mb, ng = self.max_bs, len(grp_rows)
+        h[:rows] = 0
+        h[:n] = pre
+        h[mb : mb + 4 * groups] = info.reshape(-1)
+        h[mb + 4 * groups : mb + 4 * groups + ng] = grp_rows
+        self.cascade_rows = ng
+        c = self.cascade
+        c.prefix_tokens[:rows].copy_(self._h_casc[:rows], non_blocking=True)
+        c.group_info.view(-1).copy_(self._h_casc[mb : mb + 4 * groups], non_blocking=True)
+        if ng:
+            c.group_rows[:ng].copy_(self._h_casc[mb + 4 * groups : mb + 4 * groups + ng], non_blocking=True)
 
     # ------------------------------------------------------------ prefill
     def build_prefill(self, seqs: list[SeqSchedule]) -> tuple[int, int, int, bool]:

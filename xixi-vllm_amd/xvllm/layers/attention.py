@@ -19,6 +19,20 @@ from .._torch_glue import aligned16, ptr, require_bf16, require_cuda, stream_of
 from ..kv_ops import store_kvcache
 
 
+@dataclass
+class CascadePlan:
+    """Shared-prefix groups of a decode batch (device int32 tensors): row b's
+    first prefix_tokens[b] tokens are its group's shared blocks; group g's
+    record group_info[g] is (first index into group_rows, rows, first batch
+    row, prefix tokens).  num_groups and max_prefix_blocks fix the prefix
+    pass's grid (empty groups allowed)."""
+    prefix_tokens: torch.Tensor
+    group_info: torch.Tensor
+    group_rows: torch.Tensor
+    num_groups: int
+    max_prefix_blocks: int
+
+
 class AttnInputs(NamedTuple):
     slot_mapping: torch.Tensor
     is_prefill: bool
@@ -28,6 +42,7 @@ class AttnInputs(NamedTuple):
     max_seqlen_k: int = 0
     block_tables: Optional[torch.Tensor] = None
     cache_seqlens: Optional[torch.Tensor] = None
+    cascade: Optional[CascadePlan] = None  # decode only: shared-prefix groups (no reference counterpart)
 
 
 @dataclass
@@ -130,6 +145,60 @@ def paged_decode_attention(
             bsz, num_qo_heads, num_kv_heads, head_dim, page, max_blocks, float(scale), stream_of(q),
         ),
         "xv_paged_decode_attention",
+    )
+    return out
+
+
+_CASCADE_WS: dict[tuple[str, int | None], torch.Tensor] = {}
+
+
+def cascade_decode_attention(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    plan: CascadePlan,
+    num_qo_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    softmax_scale: float | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """paged_decode_attention with the shared prefixes of `plan` read once per
+    group (xv_cascade_decode_attention).  Same output as the plain decode up
+    to fp32 summation order."""
+    require_cuda(q, k_cache, v_cache, block_tables, cache_seqlens, plan.prefix_tokens)
+    require_bf16(q, k_cache, v_cache)
+    q3, qs0, qs1 = _q_view(q, num_qo_heads, head_dim)
+    bsz = q3.shape[0]
+    nb, page, hkv, d = k_cache.shape
+    assert hkv == num_kv_heads and d == head_dim and v_cache.stride() == k_cache.stride()
+    bt = block_tables if block_tables.dtype == torch.int32 else block_tables.to(torch.int32)
+    if bt.stride(-1) != 1:
+        bt = bt.contiguous()
+    sl = cache_seqlens.to(torch.int32).contiguous()
+    if out is None:
+        out = torch.empty((bsz, num_qo_heads * head_dim), dtype=q.dtype, device=q.device)
+    L = _C.lib()
+    max_blocks = bt.shape[1]
+    nbytes = L.xv_cascade_decode_workspace_size(bsz, num_qo_heads, num_kv_heads, max_blocks, page, head_dim)
+    key = (q.device.type, q.device.index)
+    ws = _CASCADE_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)  # a recorded graph may still hold it
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=q.device)
+        _CASCADE_WS[key] = ws
+    scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
+    _C.check(
+        L.xv_cascade_decode_attention(
+            ptr(q3), qs0, qs1, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+            ptr(bt), bt.stride(0), ptr(sl), ptr(plan.prefix_tokens), ptr(plan.group_info), ptr(plan.group_rows),
+            plan.num_groups, min(plan.max_prefix_blocks, max_blocks), ptr(out), out.stride(0), ptr(ws), ws.numel(),
+            bsz, num_qo_heads, num_kv_heads, head_dim, page, max_blocks, float(scale), stream_of(q),
+        ),
+        "xv_cascade_decode_attention",
     )
     return out
 
@@ -253,6 +322,14 @@ class Attention(nn.Module):
         self.layer_id = layer_id
 
     def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, attn: AttnInputs) -> torch.Tensor:
+        if attn.cascade is not None and not attn.is_prefill:
+            # shared-prefix decode: the plan does not fit the vllm::attention schema
+            k_cache, v_cache = _layer_caches(self.layer_id)
+            if attn.slot_mapping is not None:
+                store_kvcache(k.view(-1, self.num_kv_heads, self.head_dim), v.view(-1, self.num_kv_heads, self.head_dim),
+                              k_cache, v_cache, attn.slot_mapping)
+            return cascade_decode_attention(q, k_cache, v_cache, attn.block_tables, attn.cache_seqlens, attn.cascade,
+                                            self.num_heads, self.num_kv_heads, self.head_dim)
         return torch.ops.vllm.attention(
             q, k, v, attn.slot_mapping, attn.is_prefill, attn.cu_seqlens_q, attn.cu_seqlens_k,
             attn.max_seqlen_q, attn.max_seqlen_k, attn.block_tables, attn.cache_seqlens,

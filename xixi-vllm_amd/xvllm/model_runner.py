@@ -46,10 +46,16 @@ def sample_mode(batch: Batch) -> int:
 class ModelRunner:
     def __init__(self, model, kv: KVPool, sampler: Sampler | None = None, *, max_num_seqs: int = 256,
                  max_num_batched_tokens: int = 8192, context_len: int = 4096, device=None,
-                 enforce_eager: bool = False, sample_modes: tuple[int, ...] = ()) -> None:
+                 enforce_eager: bool = False, sample_modes: tuple[int, ...] = (), cascade_groups: int = 0,
+                 cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16) -> None:
         """`sample_modes`: sampling modes (see `sample_mode`) whose decode
         sampler graphs are recorded up front besides the all-greedy one;
-        other modes are recorded at their first use."""
+        other modes are recorded at their first use.
+        `cascade_groups` > 0: decode steps find up to that many groups of rows
+        whose block tables share leading pages (a prefix cache's shared
+        blocks) and read those pages once per group (cascade decode);
+        cascade_max_prefix_blocks bounds the shared blocks per group (default:
+        the whole table) and sizes the prefix pass."""
         self.model = model
         self.kv = kv
         self.sampler = sampler or Sampler()
@@ -67,7 +73,9 @@ class ModelRunner:
         max_blocks = (context_len + self.block_size - 1) // self.block_size
         self.batch = Batch(max_bs=self.max_bs, max_tokens=max(max_num_batched_tokens, self.max_bs),
                            max_blocks=max_blocks, vocab_size=cfg.vocab_size, device=self.device,
-                           block_size=self.block_size, num_blocks=kv.num_blocks)
+                           block_size=self.block_size, num_blocks=kv.num_blocks, cascade_groups=cascade_groups,
+                           cascade_max_prefix_blocks=cascade_max_prefix_blocks, cascade_min_blocks=cascade_min_blocks,
+                           cascade_max_rows=max(1, 128 // (cfg.num_attention_heads // cfg.num_key_value_heads)))
         self.vocab_size = cfg.vocab_size
         self._decode_out = torch.zeros(self.max_bs, self.hidden_size, dtype=kv.dtype, device=self.device)
         self._decode_ids = torch.zeros(self.max_bs, dtype=torch.int64, device=self.device)
@@ -90,7 +98,8 @@ class ModelRunner:
     # ------------------------------------------------------------ decode
     def _decode_attn(self, bs: int) -> AttnInputs:
         return AttnInputs(slot_mapping=self.batch.slot_mapping[:bs], is_prefill=False,
-                          cache_seqlens=self.batch.cache_seqlens[:bs], block_tables=self.batch.block_tables[:bs])
+                          cache_seqlens=self.batch.cache_seqlens[:bs], block_tables=self.batch.block_tables[:bs],
+                          cascade=self.batch.cascade)
 
     def _decode_body(self, bs: int) -> torch.Tensor:
         with attention_context(self._meta):
