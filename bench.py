@@ -4,7 +4,9 @@
 Workload: paged GQA decode attention at the Qwen3-8B
 attention shape -- 32 q heads / 8 kv heads, head_dim 128, bf16, batch 64,
 context lengths U[512, 4096], 16-token pages, block tables a random
-permutation of a pool 1.25x the pages needed.  One "step" is one decode
+permutation of a pool 1.25x the pages needed, in KVPool's default page
+memory order ([page][kv head][token][d]; the reference's order is timed
+beside it in `sweep`).  One "step" is one decode
 attention call over the batch (split-KV kernel + split merge).  Four layers'
 worth of KV pools are cycled so that a step never finds its KV in the 256 MB
 MALL, as in a real multi-layer decode step.
@@ -45,10 +47,11 @@ def algo_bytes(ctx: list[int], hq=HQ, hkv=HKV, d=D) -> int:
     return kv + qo + bt + 4 * len(ctx)
 
 
-def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = "nhd"):
-    """Per layer: q, K pool, V pool, block tables, seqlens.  layout "nhd" is
-    the reference's [NB, BS, Hkv, D] page; "hnd" stores [NB, Hkv, BS, D] and
-    passes the transposed view (same logical shape)."""
+def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = "hnd"):
+    """Per layer: q, K pool, V pool, block tables, seqlens.  layout "hnd" (the
+    default KVPool order) stores [NB, Hkv, BS, D] and passes the transposed
+    view with the reference's logical shape [NB, BS, Hkv, D]; "nhd" is the
+    reference's memory order."""
     g = torch.Generator().manual_seed(seed)
     need = [(c + PAGE - 1) // PAGE for c in ctx]
     pool = math.ceil(1.25 * sum(need))
@@ -615,6 +618,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--layout", choices=("hnd", "nhd"), default="hnd",
+                    help="KV page memory order of the headline (hnd: KVPool's default; nhd: the reference's)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); run with --gpus 1"}))
@@ -652,7 +657,7 @@ def main() -> int:
     if args.prefill_only:
         print(json.dumps(prefill_suite(torch, dev, iters=args.steps)))
         return 0
-    cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1)
+    cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=args.layout)
     ms, wall, eager_ms = time_decode(torch, cases, args.steps, args.warmup)
     nbytes = algo_bytes(ctx)
     gbs = nbytes / (ms * 1e-3) / 1e9
@@ -667,6 +672,15 @@ def main() -> int:
             sweep[f"B{bsz}_ctx{clen}"] = {"us": round(m2 * 1e3, 2), "GB/s": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9, 1),
                                           "frac": round(algo_bytes(c2) / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
             del cs
+        torch.cuda.empty_cache()
+        # the KV pool's memory order: config 2 in the other page layout, timed
+        # the same way as the headline (one graph of K calls)
+        other = "nhd" if args.layout == "hnd" else "hnd"
+        cs = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=other)
+        m2, _, _ = time_decode(torch, cs, args.steps, 20)
+        sweep[f"config2_{other}_pages"] = {"us": round(m2 * 1e3, 2), "GB/s": round(nbytes / (m2 * 1e-3) / 1e9, 1),
+                                           "frac": round(nbytes / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del cs
         torch.cuda.empty_cache()
 
     line = {
@@ -687,6 +701,9 @@ def main() -> int:
             "batch": 64,
             "total_ctx_tokens": sum(ctx),
             "kv_pools_cycled": 4,
+            "kv_page_layout": args.layout + (" (KVPool default: [page][kv head][token][d] in memory, the reference's"
+                                             " logical [page][token][kv head][d] view)" if args.layout == "hnd"
+                                             else " (the reference's memory order)"),
         },
         "roofline": {
             "bound": "hbm",
