@@ -34,8 +34,8 @@ sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
-# 2 x 318995.4 KiB read (FETCH_SIZE counts half on this part) + 3225.2 KiB written.
-MEASURED_TRAFFIC_BYTES = int((2 * 318995.4 + 3225.2) * 1024)
+# 2 x 319336.1 KiB read (FETCH_SIZE counts half on this part) + 3226.4 KiB written.
+MEASURED_TRAFFIC_BYTES = int((2 * 319336.1 + 3226.4) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
@@ -645,9 +645,9 @@ def main() -> int:
         print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
         return 0
     if args.config5_only:
-        c5, model = decode_config5(torch, dev, cascade=True)
-        c5p, model = decode_config5(torch, dev, cascade=False, model=model)
-        print(json.dumps({"config5": c5, "config5_plain": c5p}))
+        c5, model = decode_config5(torch, dev, cascade=False)
+        c5c, model = decode_config5(torch, dev, cascade=True, model=model)
+        print(json.dumps({"config5": c5, "config5_cascade": c5c}))
         return 0
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)
@@ -731,8 +731,8 @@ def main() -> int:
         line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
     if args.config5:
         torch.cuda.empty_cache()
-        line["config5"], model = decode_config5(torch, dev, cascade=True)
-        line["config5_plain"], model = decode_config5(torch, dev, cascade=False, model=model)
+        line["config5"], model = decode_config5(torch, dev, cascade=False)
+        line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
         del model
         torch.cuda.empty_cache()
     if not args.no_serve:
