@@ -537,7 +537,17 @@ def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
         "kind": "port",
         "sample": f"numpy oracle (fp32), the full config-2 batch ({len(ctx_all)} sequences, {sum(ctx_all)} tokens) "
                   f"x {reps} repetitions, {t_used:.1f} s timed (input generation excluded)",
+        # the host the baseline ran on (the port uses one thread of it)
+        "host_cpus": os.cpu_count(),
+        "host_cpus_usable": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+        "torch_threads": _torch_threads(),
     }
+
+
+def _torch_threads():
+    import torch
+
+    return torch.get_num_threads()
 
 
 def cpu_baseline_rows(budget_s: float = 1.0) -> dict:
