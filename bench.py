@@ -319,7 +319,7 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(dev):
-            model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+            model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
             kv = KVPool(cfg, num_blocks=pool, block_size=PAGE, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
@@ -407,7 +407,7 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     try:
         with torch.device(dev):
             if model is None:
-                model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+                model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
             kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
                         num_layers=pool_layers)
     finally:
@@ -482,7 +482,7 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
     try:
         with torch.device(dev):
             if model is None:
-                model = Qwen3ForCausalLM(cfg).random_init_(seed=0)
+                model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
             kv = KVPool(cfg, num_blocks=pages_needed + 16, block_size=PAGE, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
@@ -609,6 +609,10 @@ def cpu_baseline_rows(budget_s: float = 1.0) -> dict:
     return out
 
 
+# split-K o_proj / down_proj at decode batch sizes (xvllm.layers.linear); --no-split-k turns it off
+SPLIT_K = True
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -628,9 +632,12 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-split-k", action="store_true", help="plain o_proj / down_proj GEMMs in the model runs")
     ap.add_argument("--layout", choices=("hnd", "nhd"), default="hnd",
                     help="KV page memory order of the headline (hnd: KVPool's default; nhd: the reference's)")
     args = ap.parse_args()
+    global SPLIT_K
+    SPLIT_K = not args.no_split_k
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one GPU only (no multi-GPU path); run with --gpus 1"}))
         return 2

@@ -205,6 +205,21 @@ int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, int64_t resi
                          hipStream_t stream);
 
 /*
+ * fused_add_rmsnorm whose x is the fp32 partial sums of a split-K GEMM.
+ * Same contract as vllm::fused_add_rmsnorm (src/compute/layers/ops.py:72-79)
+ * applied to x = bf16(sum_p parts[p]), the output of the unsplit GEMM that
+ * feeds it (o_proj / down_proj, src/compute/models/qwen3.py:64,115, into the norms
+ * of :150,:152 and the final norm); the normalised rows go to `out` instead of over x.
+ *   part p of row r at parts + p*part_stride + r*row_stride (floats, both
+ *   multiples of 4);  1 <= num_parts <= 8.
+ *   s = bf16(sum parts) + residual (fp32);  residual <- bf16(s);
+ *   out <- bf16(s * rsqrt(mean(s^2)+eps) * w)
+ */
+int xv_fused_add_rmsnorm_parts(const float* parts, int64_t part_stride, int64_t row_stride, int num_parts,
+                               void* out, int64_t out_stride, void* residual, int64_t residual_stride,
+                               const void* weight, int64_t rows, int hidden, float eps, hipStream_t stream);
+
+/*
  * NeoX rotary embedding from an fp32 cos||sin table [max_pos, D] into new buffers.
  * Replaces vllm::rotary_embedding, src/compute/layers/ops.py:31-51
  * (flashinfer apply_rope_with_cos_sin_cache, is_neox=True) with the table of

@@ -67,6 +67,12 @@ def test_elementwise_entry_points_reject_bad_layouts(lib):
     assert lib.xv_rmsnorm(U, 4096, 0, A, A, 4, 1, 4096, C.c_float(1e-6), s) == INVALID
     assert lib.xv_fused_add_rmsnorm(A, 4100, A, 4096, A, 4, 4096, C.c_float(1e-6), s) == INVALID
     assert lib.xv_fused_add_rmsnorm(A, 4096, U, 4096, A, 4, 4096, C.c_float(1e-6), s) == INVALID
+    # split-K parts norm: 0 or 9 parts, a part stride not in 16-byte units, misaligned residual
+    f = C.c_float(1e-6)
+    assert lib.xv_fused_add_rmsnorm_parts(A, 16384, 4096, 0, A, 4096, A, 4096, A, 4, 4096, f, s) == INVALID
+    assert lib.xv_fused_add_rmsnorm_parts(A, 16384, 4096, 9, A, 4096, A, 4096, A, 4, 4096, f, s) == INVALID
+    assert lib.xv_fused_add_rmsnorm_parts(A, 16386, 4096, 2, A, 4096, A, 4096, A, 4, 4096, f, s) == INVALID
+    assert lib.xv_fused_add_rmsnorm_parts(A, 16384, 4096, 2, A, 4096, U, 4096, A, 4, 4096, f, s) == INVALID
     # RoPE: head_dim other than 128, misaligned q
     assert lib.xv_rotary_embedding(A, 4096, 128, A, 1024, 128, A, A, A, A, 4, 32, 8, 64, s) == INVALID
     assert lib.xv_rotary_embedding(U, 4096, 128, A, 1024, 128, A, A, A, A, 4, 32, 8, 128, s) == INVALID

@@ -302,6 +302,88 @@ struct AddRmsLaunch {
   }
 };
 
+// Residual add + RMSNorm whose x arrives as np fp32 partial sums of a
+// split-K GEMM (part p of row r at parts + p*part_stride + r*row_stride):
+// x = bf16(sum of parts) -- the value the unsplit GEMM would have written --
+// then exactly the fused_add_rmsnorm_kernel arithmetic, the result into out.
+constexpr int kMaxParts = 8;
+template <int TPR, int VPT>
+__global__ __launch_bounds__(kNormBlock<TPR>) void fused_add_rmsnorm_parts_kernel(
+    const float* __restrict__ parts, int64_t part_stride, int64_t row_stride, int np, bf16_t* __restrict__ out,
+    int64_t os, bf16_t* __restrict__ res, int64_t rs, const bf16_t* __restrict__ w, int64_t rows, int hidden,
+    float eps) {
+  const int rows_per_block = kNormBlock<TPR> / TPR;
+  int64_t row = (int64_t)blockIdx.x * rows_per_block + threadIdx.x / TPR;
+  int lane = threadIdx.x % TPR;
+  bool active = row < rows;
+  const float* pr = parts + (active ? row : 0) * row_stride;
+  bf16_t* rr = res + (active ? row : 0) * rs;
+  int nvec = hidden >> 3;
+  float v[VPT][8];
+  Vec8 wv[VPT];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (active && vi < nvec) {
+      // every part's two float4 and the residual in flight before the first add
+      floatx4_t lo[kMaxParts], hi[kMaxParts];
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p) {
+        if (p < np) {
+          const floatx4_t* src = reinterpret_cast<const floatx4_t*>(pr + p * part_stride + vi * 8);
+          lo[p] = __builtin_nontemporal_load(src);
+          hi[p] = __builtin_nontemporal_load(src + 1);
+        }
+      }
+      const Vec8 rv = load_vec8_nt(rr + vi * 8);
+      wv[k] = load_vec8(w + vi * 8);
+      float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int p = 0; p < kMaxParts; ++p) {
+        if (p < np) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) { a[e] += lo[p][e]; a[4 + e] += hi[p][e]; }
+        }
+      }
+      float b[8], xr[8];
+      unpack8(pack8(a), xr);  // the GEMM output's bf16 rounding
+      unpack8(rv, b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) { v[k][e] = xr[e] + b[e]; ss += v[k][e] * v[k][e]; }
+      store_vec8_nt(rr + vi * 8, pack8(v[k]));
+    }
+  }
+  ss = row_sum<TPR>(ss);
+  if (!active) return;
+  float rcp = rsqrtf(ss / (float)hidden + eps);
+  bf16_t* orow = out + row * os;
+#pragma unroll
+  for (int k = 0; k < VPT; ++k) {
+    int vi = lane + k * TPR;
+    if (vi < nvec) {
+      float wf[8], r[8];
+      unpack8(wv[k], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r[e] = (v[k][e] * rcp) * wf[e];
+      store_vec8_nt(orow + vi * 8, pack8(r));
+    }
+  }
+}
+
+template <int TPR, int VPT>
+struct AddRmsPartsLaunch {
+  static int run(int64_t rows, hipStream_t stream, const float* parts, int64_t pst, int64_t rst, int np, bf16_t* out,
+                 int64_t os, bf16_t* r, int64_t rs, const bf16_t* w, int hidden, float eps) {
+    constexpr int rpb = kNormBlock<TPR> / TPR;
+    int64_t blocks = (rows + rpb - 1) / rpb;
+    fused_add_rmsnorm_parts_kernel<TPR, VPT><<<dim3((unsigned)blocks), dim3(kNormBlock<TPR>), 0, stream>>>(
+        parts, pst, rst, np, out, os, r, rs, w, rows, hidden, eps);
+    XV_CHECK_LAUNCH();
+    return 0;
+  }
+};
+
 extern "C" int xv_rmsnorm(const void* x, int64_t x_stride_outer, int64_t x_stride_inner,
                           const void* weight, void* out, int64_t n_outer, int64_t n_inner,
                           int hidden, float eps, hipStream_t stream) {
@@ -321,6 +403,19 @@ extern "C" int xv_fused_add_rmsnorm(void* x, int64_t x_stride, void* residual, i
     return (int)hipErrorInvalidValue;
   return dispatch_norm<AddRmsLaunch>(rows, hidden, stream, (bf16_t*)x, x_stride, (bf16_t*)residual,
                                      residual_stride, (const bf16_t*)weight, hidden, eps);
+}
+
+extern "C" int xv_fused_add_rmsnorm_parts(const float* parts, int64_t part_stride, int64_t row_stride, int num_parts,
+                                          void* out, int64_t out_stride, void* residual, int64_t residual_stride,
+                                          const void* weight, int64_t rows, int hidden, float eps,
+                                          hipStream_t stream) {
+  if (rows < 0 || num_parts < 1 || num_parts > kMaxParts) return (int)hipErrorInvalidValue;
+  if (!xv_al16(parts) || (part_stride | row_stride) & 3 || !xv_al16(out) || !xv_al16(residual) ||
+      !xv_al16(weight) || !xv_st8(out_stride) || !xv_st8(residual_stride))
+    return (int)hipErrorInvalidValue;
+  return dispatch_norm<AddRmsPartsLaunch>(rows, hidden, stream, parts, part_stride, row_stride, num_parts,
+                                          (bf16_t*)out, out_stride, (bf16_t*)residual, residual_stride,
+                                          (const bf16_t*)weight, hidden, eps);
 }
 
 // --------------------------------------------------------------------------

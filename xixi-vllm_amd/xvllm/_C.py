@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "xv_rmsnorm": (i32, [vp, i64, i64, vp, vp, i64, i64, i32, f32, vp]),
     "xv_fused_add_rmsnorm": (i32, [vp, i64, vp, i64, vp, i64, i32, f32, vp]),
+    "xv_fused_add_rmsnorm_parts": (i32, [vp, i64, i64, i32, vp, i64, vp, i64, vp, i64, i32, f32, vp]),
     "xv_rotary_embedding": (i32, [vp, i64, i64, vp, i64, i64, vp, vp, vp, vp, i64, i32, i32, i32, vp]),
     "xv_qk_norm_rope": (
         i32, [vp, i64, i64, vp, i64, i64, vp, vp, f32, vp, vp, vp, vp, i64, i32, i32, i32, vp]

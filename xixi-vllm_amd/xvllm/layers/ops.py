@@ -136,6 +136,36 @@ def _fused_add_rmsnorm_fake(x, residual, weight, eps) -> None:
     return None
 
 
+@torch.library.custom_op("xv::fused_add_rmsnorm_parts", mutates_args=("residual",))
+def fused_add_rmsnorm_parts(parts: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor,
+                            eps: float) -> torch.Tensor:
+    """fused_add_rmsnorm on the fp32 partial sums [P, T, H] of a split-K GEMM:
+    x = bf16(parts.sum(0)); residual <- x + residual; returns rmsnorm(residual)."""
+    require_cuda(parts, residual, weight)
+    require_bf16(residual, weight)
+    if parts.dtype != torch.float32 or parts.dim() != 3 or parts.stride(-1) != 1 or not aligned16(parts):
+        raise ValueError("fused_add_rmsnorm_parts needs fp32 partial sums [P, T, H], rows contiguous")
+    if residual.dim() != 2 or residual.stride(-1) != 1 or residual.stride(0) % 8 or not aligned16(residual):
+        raise ValueError("fused_add_rmsnorm_parts needs a 2-D row-major residual with 16-byte aligned rows")
+    p, t, hidden = parts.shape
+    if residual.shape != (t, hidden) or weight.shape[0] != hidden:
+        raise ValueError(f"shapes: parts {tuple(parts.shape)}, residual {tuple(residual.shape)}, weight {tuple(weight.shape)}")
+    out = torch.empty((t, hidden), dtype=residual.dtype, device=residual.device)
+    w = weight.contiguous()
+    _C.check(
+        _C.lib().xv_fused_add_rmsnorm_parts(ptr(parts), parts.stride(0), parts.stride(1), p, ptr(out), hidden,
+                                            ptr(residual), residual.stride(0), ptr(w), t, hidden, float(eps),
+                                            stream_of(residual)),
+        "xv_fused_add_rmsnorm_parts",
+    )
+    return out
+
+
+@fused_add_rmsnorm_parts.register_fake
+def _fused_add_rmsnorm_parts_fake(parts, residual, weight, eps) -> torch.Tensor:
+    return residual.new_empty(residual.shape)
+
+
 @torch.library.custom_op("xv::qk_norm_rope", mutates_args=())
 def qk_norm_rope(
     q: torch.Tensor,

@@ -18,6 +18,7 @@ from ..config import head_dim as _head_dim
 from ..config import rope_theta as _rope_theta
 from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
 from ..layers.attention import kv_cache_of
+from ..layers.linear import linear_into_norm
 from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
 
@@ -27,9 +28,13 @@ class Qwen3MLP(nn.Module):
         super().__init__()
         self.gate_up_proj = nn.Parameter(torch.empty(2 * inter, hidden))  # [gate; up] (linear.py:297-304)
         self.down_proj = nn.Parameter(torch.empty(hidden, inter))
+        self.split_k = True
 
     def forward(self, x):
-        return F.linear(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj)
+        """SiLU-MLP; the down GEMM may return PartialSums (split-K) for the
+        next residual add + RMSNorm."""
+        return linear_into_norm(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj,
+                                self.split_k)
 
 
 class Qwen3Attention(nn.Module):
@@ -47,8 +52,11 @@ class Qwen3Attention(nn.Module):
         self.rotary_emb = RotaryEmbedding(self.head_dim, self.head_dim, cfg.max_position_embeddings, _rope_theta(cfg))
         self.attn = Attention(self.num_heads, self.head_dim, self.num_kv_heads, layer_id=layer_id)
         self.eps = cfg.rms_norm_eps
+        self.split_k = True
 
     def forward(self, positions, hidden, attn: AttnInputs):
+        """qkv -> q/k norm + RoPE -> attention -> o GEMM (PartialSums when
+        split along K, for post_attention_layernorm)."""
         qkv = F.linear(hidden, self.qkv_proj)
         if not attn.is_prefill:
             # decode: norm + RoPE + KV store in one kernel, attention reads the cache
@@ -57,7 +65,7 @@ class Qwen3Attention(nn.Module):
         else:
             q, k, v = self._split_norm_rope(positions, qkv)
             o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
-        return F.linear(o, self.o_proj)
+        return linear_into_norm(o, self.o_proj, self.split_k)
 
     def _views(self, qkv):
         t = qkv.shape[0]
@@ -94,6 +102,11 @@ class Qwen3DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
 
     def forward(self, positions, hidden, residual, attn: AttnInputs):
+        """(hidden, residual) -> (hidden, residual) as the reference layer
+        (qwen3.py:149-153), except that the returned hidden may be the
+        PartialSums of the split-K down GEMM: the next layer's input norm (or
+        the final norm) consumes them; PartialSums.materialize() gives the
+        bf16 tensor."""
         hidden, residual = self.input_layernorm(hidden, residual)
         hidden = self.self_attn(positions, hidden, attn)
         hidden, residual = self.post_attention_layernorm(hidden, residual)
@@ -123,6 +136,13 @@ class Qwen3ForCausalLM(nn.Module):
 
     def forward(self, input_ids, positions, attn: AttnInputs):
         return self.model(input_ids, positions, attn)
+
+    def set_split_k(self, enabled: bool):
+        """Split-K for o_proj / down_proj at decode batch sizes (on by default)."""
+        for m in self.modules():
+            if isinstance(m, (Qwen3Attention, Qwen3MLP)):
+                m.split_k = enabled
+        return self
 
     def compute_logits(self, hidden):
         return F.linear(hidden, self.lm_head)
