@@ -26,10 +26,10 @@ def test_split_views_sum_to_the_product(m, n, k, p):
 
 def test_split_table():
     # Qwen3-8B o_proj (K 4096) and down_proj (K 12288) at decode batches
-    assert [split_factor(m, 4096, 4096) for m in (1, 8, 64, 128, 256)] == [4, 4, 4, 4, 1]
-    assert [split_factor(m, 4096, 12288) for m in (8, 16, 64, 256, 512)] == [1, 4, 4, 4, 1]
+    assert [split_factor(m, 4096, 4096) for m in (1, 8, 16, 32, 64, 128, 256)] == [4, 4, 4, 1, 1, 8, 1]
+    assert [split_factor(m, 4096, 12288) for m in (8, 16, 32, 64, 128, 256, 512)] == [1, 1, 4, 4, 8, 8, 1]
     # prefill-sized M, wide outputs and short K never split
     assert split_factor(8192, 4096, 12288) == 1
     assert split_factor(64, 24576, 4096) == 1
     assert split_factor(64, 1024, 3072) == 1
-    assert split_factor(64, 4096, 4100) == 1  # K not a multiple of 4 x 64
+    assert split_factor(128, 4096, 4352) == 1  # K not a multiple of 8 x 64

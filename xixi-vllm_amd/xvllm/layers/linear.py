@@ -4,21 +4,23 @@ down_proj, reference src/compute/models/qwen3.py:64,115 feeding the norms of
 :150,:152).
 
 At decode batch sizes an [M, K] x [K, 4096] GEMM has few output tiles for 256
-CUs: hipBLASLt runs o_proj (K 4096) and down_proj (K 12288) of Qwen3-8B at
-M 64 at 1.8-2.8 TB/s.  Cut along K into P slices, the same weights run as a
-batched GEMM of P times the tiles (one bmm over strided views, no copies),
-each slice's fp32 product kept apart; the norm kernel that consumes them sums
-the P partials, rounds to bf16 (the value the unsplit GEMM would have
-written) and continues as fused_add_rmsnorm.  The partials cost P x M x N x 4
-extra bytes of reads in the norm, small next to the weights at these M.
+CUs: hipBLASLt runs Qwen3-8B's o_proj (K 4096) and down_proj (K 12288) at
+1.4-2.7 TB/s between M 32 and 256.  Cut along K into P slices, the same
+weights run as a batched GEMM with P times the tiles (one bmm over strided
+views, no copies), each slice's fp32 product kept apart; the norm kernel
+that consumes them sums the P partials, rounds to bf16 (the value the
+unsplit GEMM would have written) and continues as fused_add_rmsnorm.  The
+partials cost P x M x N x 4 bytes of extra reads in the norm, which the
+table below charges against the GEMM's gain.
 
-Measured on MI355X, graph replay, weights streaming from HBM (us):
+Measured on MI355X, graph replay, more than 1 GB of weights cycled so that
+none is served from the 256 MB last-level cache (us; unsplit -> split):
 
-    M 64:  o_proj 12.1 -> 9.6 (P 4), down_proj 36.8 -> 23.6 (P 4)
-    M 128: o_proj 19.2 -> 12.3 (P 4), down_proj 66.1 -> 30.2 (P 4)
-    M 256: o_proj 18.9 -> 17.0 (P 4, not worth the partial reads),
-           down_proj 55.1 -> 44.1 (P 4)
-    M 8:   o_proj 11.8 -> 8.4 (P 4), down_proj 20.7 -> 21.2 (P 4: no gain)
+    down_proj  M 32: 28.2 -> 22.6 (P 4)   M 64: 37.5 -> 25.0 (P 4)
+               M 128: 66.2 -> 27.3 (P 8)  M 256: 54.4 -> 36.0 (P 8)
+               M 1, 8: no gain
+    o_proj     M 1, 8: 15.3 -> 10.1 (P 4)  M 128: 24.2 -> 15.6 (P 8)
+               M 32, 64, 256: gains below the partials' extra reads
 """
 from __future__ import annotations
 
@@ -42,12 +44,12 @@ class PartialSums(NamedTuple):
 
 def split_factor(m: int, n: int, k: int) -> int:
     """K slices for an [m, k] x [k, n] GEMM feeding a norm (1: no split)."""
-    if n > 8192 or k % (4 * 64):
+    if n > 8192 or k % (8 * 64):
         return 1
     if k >= 8192:
-        return 4 if 16 <= m <= 256 else 1
+        return 4 if 32 <= m < 96 else 8 if 96 <= m <= 256 else 1
     if k >= 4096:
-        return 4 if m <= 128 else 1
+        return 4 if m <= 16 else 8 if 96 <= m <= 192 else 1
     return 1
 
 
