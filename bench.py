@@ -214,6 +214,31 @@ def prefill_suite(torch, dev, iters: int = 20) -> dict:
     return out
 
 
+def copy_ceiling_us(torch, dev, nbytes: int) -> float:
+    """Time per call (us) of the library's streaming copy moving nbytes in
+    all (half read, half written), the better of its two launch shapes,
+    cycling over buffer sets that together exceed the 256 MB MALL: what a
+    plain transfer of a kernel's byte count reaches on this part."""
+    from xvllm import _C
+
+    half = (nbytes // 2) // 16 * 16
+    nsets = max(2, -(-(640 << 20) // (2 * half)))
+    bufs = [(torch.empty(half, dtype=torch.uint8, device=dev).fill_(1), torch.empty(half, dtype=torch.uint8, device=dev))
+            for _ in range(nsets)]
+    best = float("inf")
+    for shape in (0, 1):
+        it = [0]
+
+        def step():
+            src, dst = bufs[it[0] % nsets]
+            it[0] += 1
+            _C.check(_C.lib().xv_stream_copy(src.data_ptr(), dst.data_ptr(), half, shape,
+                                             torch.cuda.current_stream().cuda_stream), "xv_stream_copy")
+        best = min(best, _time(torch, step))
+    del bufs
+    return best
+
+
 def kernel_suite(torch, dev) -> dict:
     """Config 3 (fused elementwise/reduction set at Qwen3-8B width over 8192
     tokens) and the sampler, each against its algorithmic HBM bytes."""
@@ -227,9 +252,13 @@ def kernel_suite(torch, dev) -> dict:
     rnd = lambda *shape: torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)
     out = {}
 
-    def rec(name, us, nbytes):
+    def rec(name, us, nbytes, ceiling=False):
         out[name] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": nbytes}
+        if ceiling:
+            cu = copy_ceiling_us(torch, dev, nbytes)
+            out[name]["copy_us"] = round(cu, 2)
+            out[name]["frac_of_copy"] = round(cu / us, 4)
 
     # Each op cycles through enough input sets that one set plus the others
     # exceed the 256 MB MALL: every call streams its operands from HBM.
@@ -245,7 +274,7 @@ def kernel_suite(torch, dev) -> dict:
     sets = [(rnd(T, H), rnd(T, H)) for _ in range(2)]
     rec("fused_add_rmsnorm_T8192_H4096",
         _time(torch, cycle([lambda x=x, r=r: torch.ops.vllm.fused_add_rmsnorm(x, r, w, 1e-6) for x, r in sets])),
-        T * H * 2 * 4 + H * 2)
+        T * H * 2 * 4 + H * 2, ceiling=True)
     del sets
     qw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
     kw = (torch.randn(D_, generator=g, device=dev) * 0.1 + 1).to(torch.bfloat16)
@@ -257,11 +286,12 @@ def kernel_suite(torch, dev) -> dict:
         k = qkv[:, HQ_ * D_ : (HQ_ + HKV_) * D_].view(T, HKV_, D_)
         pos = torch.randint(0, 32768, (T,), generator=g, device=dev)
         fns.append(lambda q=q, k=k, pos=pos: torch.ops.xv.qk_norm_rope(q, k, qw, kw, 1e-6, pos, cs))
-    rec("qk_norm_rope_T8192_32q8kv", _time(torch, cycle(fns)), T * (HQ_ + HKV_) * D_ * 2 * 2 + 8 * T + T * D_ * 4)
+    rec("qk_norm_rope_T8192_32q8kv", _time(torch, cycle(fns)), T * (HQ_ + HKV_) * D_ * 2 * 2 + 8 * T + T * D_ * 4,
+        ceiling=True)
     del fns, qkv, q, k
     xs = [rnd(T, 2 * I) for _ in range(2)]
     rec("silu_and_mul_T8192_I12288", _time(torch, cycle([lambda x=x: torch.ops.vllm.silu_and_mul(x) for x in xs])),
-        T * 3 * I * 2)
+        T * 3 * I * 2, ceiling=True)
     del xs
     nb = 1024
     fns = []
@@ -272,7 +302,7 @@ def kernel_suite(torch, dev) -> dict:
         slots = torch.randperm(nb * PAGE, generator=g, device=dev)[:T].to(torch.int32)
         fns.append(lambda kk=kk, vv=vv, kc=kc, vc=vc, slots=slots:
                    store_kvcache(kk, vv, kc.view(-1, HKV_, D_), vc.view(-1, HKV_, D_), slots))
-    rec("store_kvcache_T8192", _time(torch, cycle(fns)), 2 * T * HKV_ * D_ * 2 * 2 + 4 * T)
+    rec("store_kvcache_T8192", _time(torch, cycle(fns)), 2 * T * HKV_ * D_ * 2 * 2 + 4 * T, ceiling=True)
     del fns, kc, vc, kk, vv
     V = 151936
     for bsz in (64, 256):
@@ -624,6 +654,7 @@ def main() -> int:
     ap.add_argument("--no-e2e", action="store_true", help="skip the Qwen3-8B decode tok/s measurement")
     ap.add_argument("--e2e-only", action="store_true", help="only the Qwen3-8B decode step (for profiling)")
     ap.add_argument("--prefill-only", action="store_true", help="only the prefill attention cases (for profiling)")
+    ap.add_argument("--suite-only", action="store_true", help="only the config-3 kernel set and the sampler")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill attention cases")
     ap.add_argument("--no-serve", action="store_true", help="skip config 4 (256 requests, greedy and sampled)")
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
@@ -673,6 +704,9 @@ def main() -> int:
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_suite(torch, dev, iters=args.steps)))
+        return 0
+    if args.suite_only:
+        print(json.dumps(kernel_suite(torch, dev)))
         return 0
     cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=args.layout)
     ms, wall, eager_ms = time_decode(torch, cases, args.steps, args.warmup)

@@ -317,6 +317,16 @@ int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
               int64_t* out_ids, void* workspace, size_t workspace_bytes,
               hipStream_t stream);
 
+/*
+ * Streaming copy of `bytes` (a multiple of 16; both pointers 16-byte aligned)
+ * with non-temporal 16-byte loads and stores.  No counterpart in the
+ * reference: a measurement yardstick for the HBM-bound kernels above (what a
+ * plain read-once / write-once transfer of the same size reaches), used by
+ * the benchmark.  shape 0: one 16-byte vector per thread; shape 1: a
+ * 1024-workgroup grid-stride loop, four vectors per lane per round.
+ */
+int xv_stream_copy(const void* src, void* dst, int64_t bytes, int shape, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

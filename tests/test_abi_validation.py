@@ -122,3 +122,9 @@ def test_sampler_workspace_never_shrinks_with_batch(lib):
             cur = lib.xv_sampler_workspace_size(b, v)
             assert cur >= prev and cur >= b * 128, (v, b)
             prev = cur
+
+
+def test_stream_copy_rejects_bad_arguments(lib):
+    for args in ((A, A, 24, 0), (U, A, 32, 0), (A, U, 32, 1), (A, A, -16, 0), (A, A, 32, 2)):
+        assert lib.xv_stream_copy(*args, None) == INVALID, args
+    assert lib.xv_stream_copy(A, A, 0, 0, None) == 0  # nothing to do

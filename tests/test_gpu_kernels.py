@@ -777,3 +777,18 @@ def test_sampler_topk_path_randomized_bitexact(dev):
                      use_top_k=True, use_top_p=bool(flags & 4), use_min_p=bool(flags & 8),
                      max_top_k=int(tks.max())).cpu().numpy()
         assert np.array_equal(got, want), (case, b, v, flags, kind, kmax)
+
+
+@pytest.mark.parametrize("nbytes,shape", [(16, 0), (4096 * 16 + 48, 0), (4096 * 16 + 48, 1), (3 << 20, 1)])
+def test_stream_copy(dev, nbytes, shape):
+    """The benchmark's copy yardstick copies exactly (both launch shapes, a
+    ragged tail) and writes nothing past the end."""
+    from xvllm import _C
+
+    src = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=dev)
+    dst = torch.zeros(nbytes + 64, dtype=torch.uint8, device=dev)
+    _C.check(_C.lib().xv_stream_copy(src.data_ptr(), dst.data_ptr(), nbytes, shape,
+                                     torch.cuda.current_stream().cuda_stream), "xv_stream_copy")
+    torch.cuda.synchronize()
+    assert torch.equal(dst[:nbytes], src)
+    assert int(dst[nbytes:].count_nonzero()) == 0

@@ -34,9 +34,9 @@ __global__ __launch_bounds__(256) void store_kvcache_kernel(
 
 // Tokens whose Hkv*D/8 chunks are a multiple of 64: a unit is 64 chunks of
 // one token (its slot and page address are wave uniform), and each wave moves
-// U consecutive units: the U slots are loaded first (scalar), then all 2U
-// vector loads are issued before any store, so a wave keeps 2U 16-byte loads
-// per lane in flight instead of two.
+// U consecutive units.  The 2U 16-byte K/V loads do not depend on the slots,
+// so they are issued first and the U slot loads (scalar) travel beside them:
+// a wave waits one memory round trip before its stores, not two.
 template <int U>
 __global__ __launch_bounds__(256) void store_kvcache_wave_kernel(
     const bf16_t* __restrict__ key, int64_t ks_tok, int64_t ks_head,
@@ -47,32 +47,35 @@ __global__ __launch_bounds__(256) void store_kvcache_wave_kernel(
   const int u0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * U);
   if (u0 >= num_units) return;
   const int lane = threadIdx.x & 63;
-  int tok[U], slot[U];
+  int tok[U];
+  int64_t hd[U];
+  Vec8 kv[U], vv[U];
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     const int u = min(u0 + j, num_units - 1);
     tok[j] = u / units_per_tok;
-    slot[j] = __builtin_amdgcn_readfirstlane(slots[tok[j]]);
-  }
-  Vec8 kv[U], vv[U];
-  int64_t dst[U];
-#pragma unroll
-  for (int j = 0; j < U; ++j) {
-    const int u = min(u0 + j, num_units - 1);
     const int c = (u - tok[j] * units_per_tok) * 64 + lane;
     const int h = c / chunks_per_head;
     const int d = (c - h * chunks_per_head) * 8;
+    hd[j] = h * cs_head + d;
     kv[j] = load_vec8_nt(key + tok[j] * ks_tok + h * ks_head + d);
     vv[j] = load_vec8_nt(value + tok[j] * vs_tok + h * vs_head + d);
-    const int page = slot[j] / block_size;
-    const int t = slot[j] - page * block_size;
-    dst[j] = (int64_t)page * cs_page + (int64_t)t * cs_tok + h * cs_head + d;
   }
+  int slot[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) slot[j] = __builtin_amdgcn_readfirstlane(slots[tok[j]]);
+  // pin the data loads here: the compiler would otherwise sink them into the
+  // slot-dependent branches below, behind the slot round trip
+#pragma unroll
+  for (int j = 0; j < U; ++j) { pin_vec8(kv[j]); pin_vec8(vv[j]); }
 #pragma unroll
   for (int j = 0; j < U; ++j) {
     if (u0 + j >= num_units || slot[j] < 0) continue;  // padding token (slot -1) writes nothing
-    store_vec8_nt(k_cache + dst[j], kv[j]);
-    store_vec8_nt(v_cache + dst[j], vv[j]);
+    const int page = slot[j] / block_size;
+    const int t = slot[j] - page * block_size;
+    const int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + hd[j];
+    store_vec8_nt(k_cache + dst, kv[j]);
+    store_vec8_nt(v_cache + dst, vv[j]);
   }
 }
 
@@ -632,6 +635,48 @@ extern "C" int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64
   int64_t total = num_tokens * vpr;
   silu_and_mul_kernel<<<dim3((unsigned)((total + 255) / 256)), 256, 0, stream>>>(
       (const bf16_t*)x, x_stride, (bf16_t*)out, out_stride, total, vpr, inter_size);
+  XV_CHECK_LAUNCH();
+  return 0;
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// --------------------------------------------------------------------------
+// Streaming copy: the measurement yardstick for the kernels above (what a
+// plain read-once / write-once transfer of the same byte count reaches on this
+// part), not part of the decode path.
+// --------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4_t* __restrict__ src, u32x4_t* __restrict__ dst,
+                                                          int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+// A grid of 1024 workgroups, four 16-byte vectors per lane per round.
+__global__ __launch_bounds__(256) void stream_copy_grid_kernel(const u32x4_t* __restrict__ src,
+                                                               u32x4_t* __restrict__ dst, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 1024;
+  for (int64_t base = (int64_t)blockIdx.x * 1024 + threadIdx.x; base < n; base += stride) {
+    u32x4_t v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (base + 256 * j < n) v[j] = __builtin_nontemporal_load(src + base + 256 * j);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (base + 256 * j < n) __builtin_nontemporal_store(v[j], dst + base + 256 * j);
+  }
+}
+
+extern "C" int xv_stream_copy(const void* src, void* dst, int64_t bytes, int shape, hipStream_t stream) {
+  if (bytes < 0 || bytes % 16 || !xv_al16(src) || !xv_al16(dst) || (shape != 0 && shape != 1))
+    return (int)hipErrorInvalidValue;
+  const int64_t n = bytes / 16;
+  if (n == 0) return 0;
+  if (shape == 0) {
+    if ((n + 255) / 256 > 0x7fffffff) return (int)hipErrorInvalidValue;
+    stream_copy_kernel<<<dim3((unsigned)((n + 255) / 256)), 256, 0, stream>>>((const u32x4_t*)src, (u32x4_t*)dst, n);
+  } else {
+    stream_copy_grid_kernel<<<dim3(1024), 256, 0, stream>>>((const u32x4_t*)src, (u32x4_t*)dst, n);
+  }
   XV_CHECK_LAUNCH();
   return 0;
 }

@@ -56,6 +56,12 @@ XV_INLINE void store_vec8_nt(bf16_t* p, const Vec8& r) {
   u32x4 v = {r.w[0], r.w[1], r.w[2], r.w[3]};
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
+// An empty asm that reads and writes v's registers: v's load is complete and
+// issued at this point in program order (the compiler may not sink it into a
+// later branch).
+XV_INLINE void pin_vec8(Vec8& v) {
+  __asm__ __volatile__("" : "+v"(v.w[0]), "+v"(v.w[1]), "+v"(v.w[2]), "+v"(v.w[3]));
+}
 XV_INLINE void unpack8(const Vec8& v, float* f) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) { f[2 * i] = bf16lo(v.w[i]); f[2 * i + 1] = bf16hi(v.w[i]); }
