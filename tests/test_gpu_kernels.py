@@ -792,3 +792,40 @@ def test_stream_copy(dev, nbytes, shape):
     torch.cuda.synchronize()
     assert torch.equal(dst[:nbytes], src)
     assert int(dst[nbytes:].count_nonzero()) == 0
+
+
+def _expected_parts(ctx: int, hkv: int, max_blocks: int, slots: int = 1024) -> list[int]:
+    """Partials per kv head of one sequence (B 1, 16-token blocks), from the
+    host's range rule: lmin = max(4, ceil(max_blocks / 128)) pages (129 partial
+    slots at B 1), ranges of L = max(lmin, ceil(total / waves)) pages over the
+    flattened (kv head, page) space, waves = min(slots, ceil(hkv * max_blocks / lmin))."""
+    lmin = max(4, -(-max_blocks // 128))
+    np_ = -(-ctx // 16)
+    total = hkv * np_
+    waves = min(slots, -(-(hkv * max_blocks) // lmin))
+    L = max(lmin, -(-total // waves))
+    return [(h * np_ + np_ - 1) // L - (h * np_) // L + 1 for h in range(hkv)]
+
+
+@pytest.mark.parametrize("ctx,nparts", [(2048, 32), (2060, 33), (4096, 64), (4100, 65)])
+def test_paged_decode_merge_partial_count_boundaries(dev, ctx, nparts):
+    """One sequence whose kv-head segments split into exactly 32, 33, 64 and
+    65 partials: the merge's batch boundaries (32 partials per batch of
+    loads, two batches in flight).  The partial counts the kernel recorded are
+    read back from the workspace (its first B x Hkv int32 words) and must be
+    the expected ones, so each case really sits on its boundary."""
+    from xvllm.layers.attention import decode_workspace, paged_decode_attention
+
+    hq, hkv, d = 32, 8, 128
+    assert set(_expected_parts(ctx, hkv, (ctx + 15) // 16)) == {nparts}
+    g = gen(ctx)
+    need = (ctx + 15) // 16
+    kc, vc, bt, sl = make_paged([ctx], need + 8, hkv, d, g)
+    q = randn_bf16((1, hq, d), g)
+    out = paged_decode_attention(q.view(1, -1).to(dev), kc.to(dev), vc.to(dev), bt.to(dev), sl.to(dev), hq, hkv, d)
+    torch.cuda.synchronize()
+    ws = decode_workspace(dev, 0)
+    recorded = ws[: hkv * 4].view(torch.int32).cpu().tolist()
+    assert recorded == [nparts] * hkv
+    want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
+    _close(f32(out).reshape(1, hq, d), want)
