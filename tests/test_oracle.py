@@ -283,3 +283,32 @@ def test_sampler_greedy_is_torch_argmax():
     for flags, temps in ((1, None), (0, np.zeros(10, np.float32))):
         got = S.sample(bits, temps, None, None, None, np.full(10, 0.5, np.float32), flags)
         np.testing.assert_array_equal(got, want)
+
+
+def test_threaded_decode_attention_equals_numpy_oracle():
+    """The multi-threaded torch restatement used for the CPU baseline computes
+    what the numpy oracle computes (fp32 against float64), padding rows included."""
+    import torch
+
+    import oracle.ops as O
+    import oracle.threaded as TH
+
+    rng = np.random.default_rng(5)
+    ctx = [1, 17, 300, 0, 64]
+    hq, hkv, d, bs = 32, 8, 128, 16
+    need = [(c + bs - 1) // bs for c in ctx]
+    nb = sum(need) + 3
+    kc = rng.standard_normal((nb, bs, hkv, d)).astype(np.float32)
+    vc = rng.standard_normal((nb, bs, hkv, d)).astype(np.float32)
+    perm = rng.permutation(nb)
+    bt = np.full((len(ctx), max(need)), -1, np.int64)
+    o = 0
+    for b, n in enumerate(need):
+        bt[b, :n] = perm[o : o + n]
+        o += n
+    q = rng.standard_normal((len(ctx), hq, d)).astype(np.float32)
+    want = O.paged_decode_attention(q, kc, vc, bt, np.array(ctx))
+    got = TH.paged_decode_attention(torch.from_numpy(q), torch.from_numpy(kc), torch.from_numpy(vc),
+                                    np.where(bt < 0, 0, bt), ctx, threads=4).numpy()
+    np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
+    assert not got[3].any()
