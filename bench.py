@@ -39,19 +39,23 @@ MEASURED_TRAFFIC_BYTES = int((2 * 319336.1 + 3226.4) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
-def algo_bytes(ctx: list[int], hq=HQ, hkv=HKV, d=D) -> int:
-    """sum ctx*Hkv*D*2(K,V)*2B + q and o (2*B*Hq*D*2B) + block-table ints + seqlens."""
-    kv = sum(ctx) * hkv * d * 2 * 2
+def algo_bytes(ctx: list[int], hq=HQ, hkv=HKV, d=D, kv_elem: int = 2) -> int:
+    """sum ctx*Hkv*D*2(K,V)*kv_elem B + q and o (2*B*Hq*D*2B) + block-table ints
+    + seqlens (kv_elem 2: bf16 pages, 1: fp8 pages)."""
+    kv = sum(ctx) * hkv * d * 2 * kv_elem
     qo = 2 * len(ctx) * hq * d * 2
     bt = sum((c + PAGE - 1) // PAGE for c in ctx) * 4
     return kv + qo + bt + 4 * len(ctx)
 
 
-def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = "hnd"):
+FP8_SCALE = 0.125  # fp8 pages: N(0,1) values stored as e4m3fn(x * 8), k_scale = v_scale = 1/8
+
+
+def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = "hnd", fp8: bool = False):
     """Per layer: q, K pool, V pool, block tables, seqlens.  layout "hnd" (the
     default KVPool order) stores [NB, Hkv, BS, D] and passes the transposed
     view with the reference's logical shape [NB, BS, Hkv, D]; "nhd" is the
-    reference's memory order."""
+    reference's memory order.  fp8: e4m3fn pages (the optional pool format)."""
     g = torch.Generator().manual_seed(seed)
     need = [(c + PAGE - 1) // PAGE for c in ctx]
     pool = math.ceil(1.25 * sum(need))
@@ -68,11 +72,20 @@ def make_case(torch, ctx: list[int], layers: int, dev, seed: int, layout: str = 
         shape = (pool, PAGE, HKV, D) if layout == "nhd" else (pool, HKV, PAGE, D)
         kc = torch.randn(shape, generator=gd, device=dev).to(torch.bfloat16)
         vc = torch.randn(shape, generator=gd, device=dev).to(torch.bfloat16)
+        if fp8:
+            kc = (kc.float() / FP8_SCALE).to(torch.float8_e4m3fn)
+            vc = (vc.float() / FP8_SCALE).to(torch.float8_e4m3fn)
         if layout == "hnd":
             kc, vc = kc.transpose(1, 2), vc.transpose(1, 2)
         q = torch.randn((len(ctx), HQ * D), generator=gd, device=dev).to(torch.bfloat16)
         cases.append((q, kc, vc, bt.to(dev), torch.tensor(ctx, dtype=torch.int32, device=dev)))
     return cases
+
+
+def _scales(kc) -> dict:
+    import torch
+
+    return {"k_scale": FP8_SCALE, "v_scale": FP8_SCALE} if kc.dtype == torch.float8_e4m3fn else {}
 
 
 def time_decode(torch, cases, steps: int, warmup: int):
@@ -88,7 +101,7 @@ def time_decode(torch, cases, steps: int, warmup: int):
 
     def step(i):
         q, kc, vc, bt, sl = cases[i % len(cases)]
-        paged_decode_attention(q, kc, vc, bt, sl, HQ, HKV, D, out=outs[i % len(cases)])
+        paged_decode_attention(q, kc, vc, bt, sl, HQ, HKV, D, out=outs[i % len(cases)], **_scales(kc))
 
     for i in range(warmup):
         step(i)
@@ -126,7 +139,7 @@ def time_decode_graph(torch, cases, iters: int = 48) -> float:
 
     def call():
         q, kc, vc, bt, sl = cases[i[0] % len(cases)]
-        paged_decode_attention(q, kc, vc, bt, sl, HQ, HKV, D, out=outs[i[0] % len(cases)])
+        paged_decode_attention(q, kc, vc, bt, sl, HQ, HKV, D, out=outs[i[0] % len(cases)], **_scales(kc))
         i[0] += 1
 
     return _time(torch, call, iters=iters, warmup=len(cases))
@@ -743,6 +756,16 @@ def main() -> int:
         m2, _, _ = time_decode(torch, cs, args.steps, 20)
         sweep[f"config2_{other}_pages"] = {"us": round(m2 * 1e3, 2), "GB/s": round(nbytes / (m2 * 1e-3) / 1e9, 1),
                                            "frac": round(nbytes / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        del cs
+        torch.cuda.empty_cache()
+        # the pool's fp8 (e4m3fn) format: config 2 on fp8 pages in the headline's page order, timed
+        # the same way; GB/s counts the fp8 bytes, bf16_equiv_GB/s the bf16 path's bytes in that time
+        cs = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=args.layout, fp8=True)
+        m2, _, _ = time_decode(torch, cs, args.steps, 20)
+        nb8 = algo_bytes(ctx, kv_elem=1)
+        sweep["config2_fp8_pages"] = {"us": round(m2 * 1e3, 2), "GB/s": round(nb8 / (m2 * 1e-3) / 1e9, 1),
+                                      "frac": round(nb8 / (m2 * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                      "bf16_equiv_GB/s": round(nbytes / (m2 * 1e-3) / 1e9, 1)}
         del cs
         torch.cuda.empty_cache()
 

@@ -48,6 +48,24 @@ int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t key_stride
                      int num_kv_heads, int head_dim, hipStream_t stream);
 
 /*
+ * KV store into an fp8 (OCP e4m3fn) cache.  No counterpart in the reference,
+ * whose pool holds the model dtype (src/compute/kv_pool.py:49-51): an optional
+ * on-HBM format that halves the KV bytes the decode streams.  As
+ * xv_store_kvcache, with each bf16 value x stored as e4m3fn(x * (1/scale))
+ * (1/scale in fp32, one fp32 multiply, round to nearest even; a product past
+ * the format's range, |p| > 464, becomes NaN, as torch's float8_e4m3fn cast
+ * does), k_scale for key and v_scale for value, both finite and > 0.  Cache
+ * strides are in elements (= bytes); cache rows and strides 8-byte aligned;
+ * num_kv_heads * head_dim a multiple of 512.
+ */
+int xv_store_kvcache_fp8(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                         const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                         void* k_cache, void* v_cache,
+                         int64_t cache_page_stride, int64_t cache_tok_stride, int64_t cache_head_stride,
+                         int block_size, const int32_t* slot_mapping, int64_t num_tokens,
+                         int num_kv_heads, int head_dim, float k_scale, float v_scale, hipStream_t stream);
+
+/*
  * Paged GQA decode attention (one query token per sequence, causal = attends
  * to every cached token including the one stored this step).
  * Replaces the decode branch of vllm::attention -> flash_attn_with_kvcache,
@@ -87,6 +105,27 @@ int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_str
                               int batch, int num_q_heads, int num_kv_heads, int head_dim,
                               int block_size, int max_blocks_per_seq, float scale,
                               hipStream_t stream);
+
+/*
+ * xv_paged_decode_attention over an fp8 (OCP e4m3fn) cache written by
+ * xv_store_kvcache_fp8.  No counterpart in the reference (its pool holds the
+ * model dtype, src/compute/kv_pool.py:49-51): the on-HBM format option of the
+ * KV pool, half the bytes per token.  Attends to K = k_cache * k_scale and
+ * V = v_cache * v_scale (each fp8 value is exact in bf16; k_scale is folded
+ * into the softmax scale, v_scale multiplies the output).  Cache strides are
+ * in elements (= bytes) and multiples of 16; the same workspace as
+ * xv_paged_decode_attention (xv_paged_decode_workspace_size).
+ */
+int xv_paged_decode_attention_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                  const void* k_cache, const void* v_cache,
+                                  int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                  const int32_t* block_tables, int64_t bt_stride,
+                                  const int32_t* cache_seqlens,
+                                  void* out, int64_t out_stride_tok,
+                                  void* workspace, size_t workspace_bytes,
+                                  int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                  int block_size, int max_blocks_per_seq, float scale,
+                                  float k_scale, float v_scale, hipStream_t stream);
 
 /*
  * Shared-prefix (cascade) decode attention: xv_paged_decode_attention for a

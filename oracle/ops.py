@@ -162,3 +162,40 @@ def silu_and_mul(x):
     i = x.shape[-1] // 2
     g, u = x64[..., :i], x64[..., i:]
     return round_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+
+
+# ---------------------------------------------------------------- fp8 pages
+# The optional fp8 pool format of this build (the reference's pool holds the
+# model dtype, src/compute/kv_pool.py:49-51): OCP float8 e4m3fn, sign, 4
+# exponent bits (bias 7), 3 mantissa bits, no infinities, 0x7f / 0xff NaN.
+def fp8_e4m3fn_values() -> np.ndarray:
+    """float32 value of each of the 256 codes, from the format definition."""
+    c = np.arange(256)
+    s, e, m = c >> 7, (c >> 3) & 15, c & 7
+    mag = np.where(e == 0, m * 2.0**-9, (1.0 + m / 8.0) * 2.0 ** (e - 7))
+    v = np.where(s == 1, -mag, mag)
+    v = np.where((e == 15) & (m == 7), np.nan, v)
+    return v.astype(np.float32)
+
+
+def quantize_fp8(x, inv_scale: float) -> np.ndarray:
+    """e4m3fn codes of float32(x) * float32(inv_scale): round to nearest, ties
+    to the even code, except that a tie at 464 (halfway from the largest value
+    448 to the next binade's 480) gives 448; |product| > 464 and NaN give NaN
+    (0x7f, sign kept for the product)."""
+    p = (np.asarray(x, np.float32) * np.float32(inv_scale)).astype(np.float32)
+    pos = fp8_e4m3fn_values()[:127].astype(np.float64)  # codes 0..126 ascending: 0 .. 448
+    a = np.abs(p.astype(np.float64))
+    hi = np.clip(np.searchsorted(pos, a, side="left"), 0, 126)  # first value >= a
+    lo = np.clip(hi - 1, 0, 126)
+    d_lo, d_hi = a - pos[lo], pos[hi] - a
+    code = np.where(d_lo < d_hi, lo, np.where(d_hi < d_lo, hi, np.where(lo % 2 == 0, lo, hi)))
+    code = np.where(a > 448.0, np.where(a <= 464.0, 126, 127), code)
+    code = np.where(np.isnan(a), 127, code)
+    sign = np.signbit(p) & ~np.isnan(p)
+    return (code | np.where(sign, 0x80, 0)).astype(np.uint8)
+
+
+def dequantize_fp8(codes, scale: float) -> np.ndarray:
+    """float64 values the decode attends to: value(code) * scale."""
+    return fp8_e4m3fn_values()[np.asarray(codes, np.uint8)].astype(np.float64) * float(scale)

@@ -128,3 +128,26 @@ def test_stream_copy_rejects_bad_arguments(lib):
     for args in ((A, A, 24, 0), (U, A, 32, 0), (A, U, 32, 1), (A, A, -16, 0), (A, A, 32, 2)):
         assert lib.xv_stream_copy(*args, None) == INVALID, args
     assert lib.xv_stream_copy(A, A, 0, 0, None) == 0  # nothing to do
+
+
+def test_fp8_entry_points_reject_bad_arguments(lib):
+    def dec(**kw):
+        a = dict(q=A, kc=A, vc=A, ps=16384, ts=1024, hs=128, B=64, BS=16, ks=1.0, vs=1.0)
+        a.update(kw)
+        return lib.xv_paged_decode_attention_fp8(a["q"], 4096, 128, a["kc"], a["vc"], a["ps"], a["ts"], a["hs"], A, 256,
+                                                 A, A, 4096, A, 1 << 30, a["B"], 32, 8, 128, a["BS"], 256, 0.088,
+                                                 a["ks"], a["vs"], None)
+    for kw in (dict(ts=1032), dict(hs=136), dict(kc=U), dict(ks=0.0), dict(vs=-1.0), dict(ks=float("inf")),
+               dict(vs=float("nan")), dict(BS=8)):
+        assert dec(**kw) == INVALID, kw
+    assert dec(B=0) == 0
+
+    def store(**kw):
+        a = dict(k=A, kc=A, ps=16384, ts=1024, hs=128, n=8, hkv=8, d=128, ks=1.0, vs=1.0)
+        a.update(kw)
+        return lib.xv_store_kvcache_fp8(a["k"], 1024, 128, A, 1024, 128, a["kc"], A, a["ps"], a["ts"], a["hs"], 16, A,
+                                        a["n"], a["hkv"], a["d"], a["ks"], a["vs"], None)
+    for kw in (dict(k=U), dict(kc=A + 4), dict(ts=1028), dict(ks=0.0), dict(vs=float("inf")), dict(hkv=2, d=128),
+               dict(d=12)):
+        assert store(**kw) == INVALID, kw
+    assert store(n=0) == 0

@@ -312,3 +312,32 @@ def test_threaded_decode_attention_equals_numpy_oracle():
                                     np.where(bt < 0, 0, bt), ctx, threads=4).numpy()
     np.testing.assert_allclose(got, want, rtol=1e-5, atol=1e-5)
     assert not got[3].any()
+
+
+def test_fp8_codec_equals_torch_float8_e4m3fn():
+    """The fp8 format of the optional pool: the decode table and the
+    quantizer (round to nearest even, NaN past the range) equal torch's
+    float8_e4m3fn cast, over a dense sweep of float32 bit patterns and the
+    special values."""
+    import torch
+
+    import oracle.ops as O
+
+    codes = torch.arange(256, dtype=torch.uint8)
+    want = codes.view(torch.float8_e4m3fn).float().numpy()
+    got = O.fp8_e4m3fn_values()
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(got[~np.isnan(got)], want[~np.isnan(want)])
+    i = np.arange(1 << 20, dtype=np.uint64)
+    x = (i * 4096 + 77 * (i & 3)).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, np.float32([0.0, -0.0, 448.0, 456.0, 463.99, 464.0, 480.0, -464.0, 2.0**-10,
+                                       3 * 2.0**-10, 2.0**-9 * 1.5, 2.0**-9 * 2.5, 1e-30, -1e-30])])
+    fin = np.isfinite(x)
+    tq = torch.from_numpy(x[fin].copy()).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    oq = O.quantize_fp8(x[fin], 1.0)
+    assert np.array_equal(oq, tq), np.where(oq != tq)[0][:5]
+    # a non-unit scale: one fp32 multiply before the rounding
+    y = np.random.default_rng(0).standard_normal(4096).astype(np.float32) * 3
+    inv = np.float32(1.0) / np.float32(0.37)
+    tq = (torch.from_numpy(y) * torch.tensor(inv)).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(O.quantize_fp8(y, inv), tq)

@@ -55,6 +55,7 @@ struct DecodeArgs {
   int max_parts;  // partial slots per (sequence, head) in the workspace
   int nwaves;     // workgroups of the main kernel (the range count)
   float scale_log2;
+  float v_scale;  // fp8 pages: the V dequantisation scale, applied to the output (1 for bf16 pages)
   // Cascade (shared-prefix) decode; pre_tokens == nullptr otherwise.  Row b's
   // first pre_tokens[b] tokens were attended by the prefix pass, whose
   // partials (normalised output, log2-sum-exp) sit at pre_o / pre_lse slot
@@ -88,6 +89,11 @@ constexpr int kPageLds = 2 * kVPageBytes;  // K then V
 constexpr int kNontemporal = 2;  // buffer instruction cache-policy bits: nt
 
 XV_INLINE int swz(int t) { return ((t & 7) << 1) | (t >> 3); }
+// fp8 page image: token r's 128-byte row at r * 128, 16-byte piece p in slot
+// p ^ swz8(r), so the 16 tokens of a K read (same piece) and the V conversion
+// reads hit distinct banks.
+XV_INLINE int swz8(int r) { return (r & 7) ^ (r >> 3); }
+constexpr int kF8Half = 2048;  // V rows of an fp8 page image start here
 
 // base and bytes are wave uniform: readfirstlane lets the compiler keep the
 // resource in SGPRs (otherwise it emits a per-lane "waterfall" loop).
@@ -102,6 +108,9 @@ XV_INLINE __amdgpu_buffer_rsrc_t page_rsrc(const bf16_t* base, uint32_t bytes) {
 // Per-lane offsets, fixed for the whole kernel.
 struct LaneOffsets {
   int g[4];  // global byte offset of load instruction s within a page
+  int g8[2];  // fp8 pages: global byte offset of load instruction s (8 rows of 128 bytes each)
+  uint32_t k8[2];  // fp8 pages: LDS offsets of this lane's two K pieces (its S^T A operands)
+  uint32_t v8[2];  // fp8 pages: LDS offsets of the two V pieces this lane converts to bf16
   uint32_t k[4];  // LDS byte offset of this lane's K A-operand chunk for MFMA step s
   uint32_t v[8];  // LDS byte offset (V half) of this lane's transposed read for O tile n
 };
@@ -115,6 +124,22 @@ XV_INLINE LaneOffsets lane_offsets(int64_t tok_stride, int lane) {
     o.g[s] = (int)(t * tok_stride * 2) + ((i ^ swz(t)) << 4);
     // K A operand of step s: row = token i, d-chunk 4s + g
     o.k[s] = (uint32_t)(i * 256 + (((4 * s + g) ^ swz(i)) << 4));
+  }
+  // fp8 rows (tok_stride in bytes): instruction s moves tokens 8s .. 8s+7;
+  // lane l fills slot l%8 of token r = 8s + l/8 with piece (l%8) ^ swz8(r)
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int r = 8 * s + (lane >> 3);
+    o.g8[s] = (int)(r * tok_stride) + (((lane & 7) ^ swz8(r)) << 4);
+  }
+  // K: lane (g, i) takes token i's values 32g .. 32g+31 (pieces 2g, 2g+1):
+  // MFMA step s contracts d-chunk 4g + s (q is read in the same order).
+  // V: lane l converts token l/4's values 32(l%4) .. +31.
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    o.k8[h] = (uint32_t)(i * 128 + (((2 * g + h) ^ swz8(i)) << 4));
+    const int r = lane >> 2, p = 2 * (lane & 3) + h;
+    o.v8[h] = (uint32_t)(kF8Half + r * 128 + ((p ^ swz8(r)) << 4));
   }
   // V B operand of tile n: lane (g, i) supplies token 4g + i/4, columns
   // 16n + 4(i%4) .. +3 = chunk 2n + (i%4)/2, bytes 8*(i%2) of it
@@ -142,6 +167,39 @@ XV_INLINE void issue_page(char* buf, const A& a, int page, int sub, int kvh, int
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + 1024 * s), 16, lo.g[s], 0, 0, kNontemporal);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kVPageBytes + 1024 * s), 16, lo.g[s], 0, 0,
                                              kNontemporal);
+  }
+}
+
+// The same page with fp8 (e4m3fn) K and V, strides in bytes: rows of 128
+// bytes, two LDS-DMA instructions of eight whole rows per tensor, K at buf
+// and V at buf + kF8PageBytes / 2 (token r's row at r * 128).  Rows past the
+// sequence end read as zeros, as above.
+template <typename A>
+XV_INLINE void issue_page_f8(char* buf, const A& a, int page, int sub, int kvh, int valid_rows,
+                             const LaneOffsets& lo) {
+  const int64_t base =
+      (int64_t)page * a.page_stride + (int64_t)sub * kPage * a.tok_stride + (int64_t)kvh * a.head_stride;
+  const uint32_t bytes = (uint32_t)((int64_t)(valid_rows - 1) * a.tok_stride + kD);
+  const __amdgpu_buffer_rsrc_t rk =
+      page_rsrc(reinterpret_cast<const bf16_t*>(reinterpret_cast<const char*>(a.kc) + base), bytes);
+  const __amdgpu_buffer_rsrc_t rv =
+      page_rsrc(reinterpret_cast<const bf16_t*>(reinterpret_cast<const char*>(a.vc) + base), bytes);
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_void*)(buf + 1024 * s), 16, lo.g8[s], 0, 0, kNontemporal);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_void*)(buf + kF8Half + 1024 * s), 16, lo.g8[s], 0, 0,
+                                             kNontemporal);
+  }
+}
+
+// 16 fp8 (e4m3fn) values -> 16 bf16 (exact: every e4m3fn value is a bf16).
+XV_INLINE void fp8x16_to_bf16(const u32x4_t& w, uint32_t (&o)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], false);
+    const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w[k], true);
+    o[2 * k] = pack_bf16x2(lo[0], lo[1]);
+    o[2 * k + 1] = pack_bf16x2(hi[0], hi[1]);
   }
 }
 
@@ -188,7 +246,7 @@ struct PageRegs {
   bf16x8_t kr[4];
   short4_t vt[8];
 };
-template <int VM>
+template <int VM, bool WAIT = true>
 XV_INLINE void read_page(PageRegs& pr, const char* buf, const LaneOffsets& lo) {
   const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
 #define XV_PAGE_READS                                                                                   \
@@ -203,21 +261,98 @@ XV_INLINE void read_page(PageRegs& pr, const char* buf, const LaneOffsets& lo) {
   "ds_read_b64_tr_b16 %8, %20\n\t"                                                                      \
   "ds_read_b64_tr_b16 %9, %21\n\t"                                                                      \
   "ds_read_b64_tr_b16 %10, %22\n\t"                                                                     \
-  "ds_read_b64_tr_b16 %11, %23\n\t"                                                                     \
-  "s_waitcnt lgkmcnt(0)"
+  "ds_read_b64_tr_b16 %11, %23\n\t"
 #define XV_PAGE_OPERANDS                                                                                \
   : "=&v"(pr.kr[0]), "=&v"(pr.kr[1]), "=&v"(pr.kr[2]), "=&v"(pr.kr[3]), "=&v"(pr.vt[0]), "=&v"(pr.vt[1]), \
     "=&v"(pr.vt[2]), "=&v"(pr.vt[3]), "=&v"(pr.vt[4]), "=&v"(pr.vt[5]), "=&v"(pr.vt[6]), "=&v"(pr.vt[7])  \
   : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),       \
     "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),       \
     "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7])
-  if constexpr (VM >= 0) {
+  if constexpr (VM >= 0 && WAIT) {
+    __asm__ __volatile__("s_waitcnt vmcnt(%24)\n\t" XV_PAGE_READS "s_waitcnt lgkmcnt(0)" XV_PAGE_OPERANDS, "n"(VM)
+                         : "memory");
+  } else if constexpr (VM >= 0) {
     __asm__ __volatile__("s_waitcnt vmcnt(%24)\n\t" XV_PAGE_READS XV_PAGE_OPERANDS, "n"(VM) : "memory");
   } else {
-    __asm__ __volatile__(XV_PAGE_READS XV_PAGE_OPERANDS : "memory");
+    __asm__ __volatile__(XV_PAGE_READS "s_waitcnt lgkmcnt(0)" XV_PAGE_OPERANDS : "memory");
   }
 #undef XV_PAGE_READS
 #undef XV_PAGE_OPERANDS
+}
+
+// The same operands from an fp8 page image: the lane's two K pieces become
+// its four bf16 A operands in registers (each fp8 value is exact in bf16);
+// V goes through a bf16 image in LDS (the layout read_page reads, at vimg)
+// for the transposed B-operand reads.  VM as in read_page.
+// The raw fp8 pieces of one page a lane reads: two K, two V.
+struct RawF8 {
+  u32x4_t k0, k1, v0, v1;
+};
+template <int VM, bool WAIT = true>
+XV_INLINE void read_raw_f8(RawF8& w, const char* buf, const LaneOffsets& lo) {
+  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+#define XV_RAW_READS         \
+  "s_waitcnt vmcnt(%4)\n\t"  \
+  "ds_read_b128 %0, %5\n\t"  \
+  "ds_read_b128 %1, %6\n\t"  \
+  "ds_read_b128 %2, %7\n\t"  \
+  "ds_read_b128 %3, %8\n\t"
+#define XV_RAW_OPERANDS                                                                                     \
+  : "=&v"(w.k0), "=&v"(w.k1), "=&v"(w.v0), "=&v"(w.v1)                                                        \
+  : "n"(VM), "v"(b0 + lo.k8[0]), "v"(b0 + lo.k8[1]), "v"(b0 + lo.v8[0]), "v"(b0 + lo.v8[1])
+  if constexpr (WAIT) {
+    __asm__ __volatile__(XV_RAW_READS "s_waitcnt lgkmcnt(0)" XV_RAW_OPERANDS : "memory");
+  } else {
+    __asm__ __volatile__(XV_RAW_READS XV_RAW_OPERANDS : "memory");
+  }
+#undef XV_RAW_READS
+#undef XV_RAW_OPERANDS
+}
+// Operands of the page whose raw pieces are in w (already complete).
+XV_INLINE void finish_page_f8(PageRegs& pr, const RawF8& w, char* vimg, const LaneOffsets& lo, int lane) {
+  const u32x4_t k0 = w.k0, k1 = w.k1, v0 = w.v0, v1 = w.v1;
+  {
+    const int r = lane >> 2, q = lane & 3;
+    uint32_t o[2][8];
+    fp8x16_to_bf16(v0, o[0]);
+    fp8x16_to_bf16(v1, o[1]);
+    char* row = vimg + r * 256;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // bf16 chunk 4q + j: values 8j .. 8j+7 of the lane's 32
+      const uint32_t* w = &o[j >> 1][4 * (j & 1)];
+      *reinterpret_cast<uint4*>(row + (((4 * q + j) ^ swz(r)) << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+  {
+    uint32_t o[2][8];
+    fp8x16_to_bf16(k0, o[0]);
+    fp8x16_to_bf16(k1, o[1]);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) __builtin_memcpy(&pr.kr[j], &o[j >> 1][4 * (j & 1)], 16);
+  }
+  // the transposed V reads of read_page (their offsets include the K half)
+  const uint32_t vb = (uint32_t)reinterpret_cast<uintptr_t>(vimg) - kVPageBytes;
+  __asm__ __volatile__(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(pr.vt[0]), "=&v"(pr.vt[1]), "=&v"(pr.vt[2]), "=&v"(pr.vt[3]), "=&v"(pr.vt[4]), "=&v"(pr.vt[5]),
+        "=&v"(pr.vt[6]), "=&v"(pr.vt[7])
+      : "v"(vb + lo.v[0]), "v"(vb + lo.v[1]), "v"(vb + lo.v[2]), "v"(vb + lo.v[3]), "v"(vb + lo.v[4]),
+        "v"(vb + lo.v[5]), "v"(vb + lo.v[6]), "v"(vb + lo.v[7])
+      : "memory");
+}
+template <int VM>
+XV_INLINE void read_page_f8(PageRegs& pr, const char* buf, char* vimg, const LaneOffsets& lo, int lane) {
+  RawF8 w;
+  read_raw_f8<VM>(w, buf, lo);
+  finish_page_f8(pr, w, vimg, lo, lane);
 }
 
 // S^T = K Q^T, the online softmax update and O += P V for one page already
@@ -264,14 +399,22 @@ XV_INLINE void page_math(SplitState& st, const PageRegs& pr, const bf16x8_t (&qb
   for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
 }
 
-template <int G, int NB>
-XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
-                            int page_tok0, int ctx, float scale_log2, int lane) {
-  // The page arrived by LDS-DMA; the 8 VMEM operations of each of the
-  // NB-1 pages issued after it may still be in flight: vmcnt(8*(NB-1))
-  // waits exactly for this page.
+// VMEM operations one page issue makes: 4 LDS-DMA instructions each for K
+// and V, or 2 each for fp8 pages.
+template <bool F8> constexpr int kPageOps = F8 ? 4 : 8;
+
+template <int G, int NB, bool F8>
+XV_INLINE void process_page(SplitState& st, const char* buf, char* img, const LaneOffsets& lo,
+                            const bf16x8_t (&qb)[4], int page_tok0, int ctx, float scale_log2, int lane) {
+  // The page arrived by LDS-DMA; the VMEM operations of each of the NB-1
+  // pages issued after it may still be in flight: vmcnt(ops*(NB-1)) waits
+  // exactly for this page.
   PageRegs pr;
-  read_page<8 * (NB - 1)>(pr, buf, lo);
+  if constexpr (F8) {
+    read_page_f8<kPageOps<true> * (NB - 1)>(pr, buf, img, lo, lane);
+  } else {
+    read_page<kPageOps<false> * (NB - 1)>(pr, buf, lo);
+  }
   page_math<G>(st, pr, qb, page_tok0, ctx, scale_log2, lane);
 }
 
@@ -318,8 +461,16 @@ XV_INLINE int seq_of(const int* pref, int batch, int hkv, int64_t f) {
 // One LDS-DMA instruction moves 4 rows (1 KB); rows past G read as zeros.
 template <int G> constexpr int kQSlot = G <= 4 ? 1024 : G * 256;
 template <int G> constexpr int kBufBytes = kPageLds + kQSlot<G>;
+// fp8 pages: 2 KB of K and 2 KB of V per page buffer, the q slot after them,
+// plus one bf16 image per wave that each page is converted into
+constexpr int kF8PageBytes = kPageLds / 2;
+template <int G, bool F8> constexpr int kPageBufBytes = F8 ? kF8PageBytes : kPageLds;
+template <int G, bool F8> constexpr int kBufBytesT = kPageBufBytes<G, F8> + kQSlot<G>;
 // Page buffers per wave: 4 (3 at G = 8) keeps four waves' LDS within a CU.
 template <int G> constexpr int kNbufG = G <= 4 ? 4 : 3;
+// fp8 pages: the same count (4, 5 or 6 buffers measured alike: the fp8
+// kernel's pace is set by its per-page work, not by the bytes in flight)
+template <int G, bool F8> constexpr int kNbufT = kNbufG<G>;
 
 template <int G>
 XV_INLINE void issue_q(char* slot, const DecodeArgs& a, int b, int kvh, int lane) {
@@ -337,19 +488,21 @@ XV_INLINE void issue_q(char* slot, const DecodeArgs& a, int b, int kvh, int lane
 // Q^T B operand of MFMA step s from the q slot: column i holds head i % G,
 // k = d-chunk 4s + g.  The slot arrived with the page it was issued with:
 // the same vmcnt as that page's wait covers it.
-template <int G, int NB>
+// F8: step s contracts d-chunk 4g + s instead (the fp8 path's K order).
+template <int G, int NB, int OPS, bool F8 = false>
 XV_INLINE void read_q(bf16x8_t (&qb)[4], const char* slot, int lane) {
   const int i = lane & 15, g = lane >> 4;
-  const uint32_t a0 = (uint32_t)reinterpret_cast<uintptr_t>(slot) + (i % G) * 256 + g * 16;
+  const uint32_t a0 = (uint32_t)reinterpret_cast<uintptr_t>(slot) + (i % G) * 256 + g * (F8 ? 64 : 16);
+  constexpr int st = F8 ? 16 : 64;  // bytes between steps
   __asm__ __volatile__(
       "s_waitcnt vmcnt(%5)\n\t"
       "ds_read_b128 %0, %4\n\t"
-      "ds_read_b128 %1, %4 offset:64\n\t"
-      "ds_read_b128 %2, %4 offset:128\n\t"
-      "ds_read_b128 %3, %4 offset:192\n\t"
+      "ds_read_b128 %1, %4 offset:%6\n\t"
+      "ds_read_b128 %2, %4 offset:%7\n\t"
+      "ds_read_b128 %3, %4 offset:%8\n\t"
       "s_waitcnt lgkmcnt(0)"
       : "=&v"(qb[0]), "=&v"(qb[1]), "=&v"(qb[2]), "=&v"(qb[3])
-      : "v"(a0), "n"(8 * (NB - 1))
+      : "v"(a0), "n"(OPS * (NB - 1)), "n"(st), "n"(2 * st), "n"(3 * st)
       : "memory");
 }
 
@@ -363,7 +516,7 @@ XV_INLINE void finish_row(const DecodeArgs& a, const SplitState& st, float lsum,
   const float mh = head_of_row<G, RR>(st.m, g);
   const int row = 4 * g + RR;
   if (row >= G) return;  // rows past G are replicas
-  const float inv = 1.0f / lh;
+  const float inv = a.v_scale / lh;
   const int head = head0 + row;
   if (full) {
     bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
@@ -467,12 +620,14 @@ XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
 #define XV_DECODE_TIMESTAMP(slot)
 #endif
 
-template <int G>
+template <int G, bool F8 = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WPE, XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
   XV_DECODE_TIMESTAMP(0);
-  constexpr int NB = kNbufG<G>;
-  constexpr int BUF = kBufBytes<G>;
+  constexpr int NB = kNbufT<G, F8>;
+  constexpr int BUF = kBufBytesT<G, F8>;
+  constexpr int QOFF = kPageBufBytes<G, F8>;  // the q slot within a page buffer
   __shared__ __attribute__((aligned(16))) char lds[NB * BUF];
+  __shared__ __attribute__((aligned(16))) char img[F8 ? kVPageBytes : 16];  // fp8 pages: the bf16 V image
   __shared__ int pref[kMaxBatch + 1];  // pages of sequences 0..b-1
   __shared__ int sl[kMaxBatch];        // cache_seqlens
   __shared__ __attribute__((aligned(16))) char idtab[2 * kIdWindow * 4];
@@ -538,9 +693,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
       issued = y;
       if (y % kIdWindow == 0 && y > 0)  // entering window k: request window k+1
         load_window(idtab + ((y / kIdWindow + 1) & 1) * (kIdWindow * 4), a, rbt, pref, f0, y + kIdWindow, n, lane);
-      if (newseg) issue_q<G>(buf + kPageLds, a, ic.b, ic.kvh, lane);
+      if (newseg) issue_q<G>(buf + QOFF, a, ic.b, ic.kvh, lane);
     }
-    issue_page(buf, a, page_id, ic.sub, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
+    if constexpr (F8) issue_page_f8(buf, a, page_id, ic.sub, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
+    else issue_page(buf, a, page_id, ic.sub, ic.kvh, min(kPage, ic.ctx - ic.pg * kPage), offs);
   };
 
   SplitState st;
@@ -563,19 +719,31 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
       if (pc.pg == 0) {
         finish(prev);
         reset(st);
-        read_q<G, NB>(qb, buf + kPageLds, lane);
+        read_q<G, NB, kPageOps<F8>, F8>(qb, buf + QOFF, lane);
       }
     } else {
-      read_q<G, NB>(qb, buf + kPageLds, lane);
+      read_q<G, NB, kPageOps<F8>, F8>(qb, buf + QOFF, lane);
     }
-    process_page<G, NB>(st, buf, offs, qb, pc.pg * kPage, pc.ctx, a.scale_log2, lane);
+    process_page<G, NB, F8>(st, buf, img, offs, qb, pc.pg * kPage, pc.ctx, a.scale_log2, lane);
   };
 
-  static_assert(NB <= 4, "four ids per lookup");
-  {
-    const Ids4 ids = lookup4(idtab, 0, n);
+  static_assert(NB <= 8, "at most eight ids per lookup");
+  // ids of positions y0 .. y0 + 7 (the second four only when NB needs them)
+  auto lookup = [&](int y0, int (&v)[8]) {
+    const Ids4 a4 = lookup4(idtab, y0, n);
 #pragma unroll
-    for (int k = 0; k < NB - 1; ++k) issue(min(k, n - 1), k, ids.v[k]);
+    for (int k = 0; k < 4; ++k) v[k] = a4.v[k];
+    if constexpr (NB > 4) {
+      const Ids4 b4 = lookup4(idtab, y0 + 4, n);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 + k] = b4.v[k];
+    }
+  };
+  {
+    int ids[8];
+    lookup(0, ids);
+#pragma unroll
+    for (int k = 0; k < NB - 1; ++k) issue(min(k, n - 1), k, ids[k]);
   }
   // window 1; every page wait before its first use orders it
   load_window(idtab + kIdWindow * 4, a, rbt, pref, f0, kIdWindow, n, lane);
@@ -583,10 +751,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WP
     // ids of the NB positions issued in this round; window k+1 of the table
     // was requested when the issue side entered window k, at least
     // kIdWindow - 2*NB positions before any of them
-    const Ids4 ids = lookup4(idtab, x0 + NB - 1, n);
+    int ids[8];
+    lookup(x0 + NB - 1, ids);
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
-      issue(min(x0 + u + NB - 1, n - 1), (u + NB - 1) % NB, ids.v[u]);
+      issue(min(x0 + u + NB - 1, n - 1), (u + NB - 1) % NB, ids[u]);
       if (x0 + u < n) process(x0 + u, u);
     }
   }
@@ -1024,7 +1193,7 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
                  const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
                  int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
                  int num_kv_heads, int nsub, int max_pages, float scale, hipStream_t stream,
-                 const CascadeParts& cp = CascadeParts()) {
+                 const CascadeParts& cp = CascadeParts(), bool f8 = false, float v_scale = 1.0f) {
   const size_t need = chunk_workspace_bytes(batch, num_q_heads, num_kv_heads, max_pages);
   if (workspace == nullptr || workspace_bytes < need) return (int)hipErrorInvalidValue;
   const int group = num_q_heads / num_kv_heads;
@@ -1044,12 +1213,22 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_pages;
   a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.v_scale = v_scale;
   a.pre_tokens = cp.pre_tokens; a.pre_chunk_pages = cp.chunk_pages; a.pre_o = cp.pre_o; a.pre_lse = cp.pre_lse;
-  switch (group) {
-    case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;
-    case 2: paged_decode_kernel<2><<<a.nwaves, 64, 0, stream>>>(a); break;
-    case 4: paged_decode_kernel<4><<<a.nwaves, 64, 0, stream>>>(a); break;
-    default: paged_decode_kernel<8><<<a.nwaves, 64, 0, stream>>>(a); break;
+  if (f8) {
+    switch (group) {
+      case 1: paged_decode_kernel<1, true><<<a.nwaves, 64, 0, stream>>>(a); break;
+      case 2: paged_decode_kernel<2, true><<<a.nwaves, 64, 0, stream>>>(a); break;
+      case 4: paged_decode_kernel<4, true><<<a.nwaves, 64, 0, stream>>>(a); break;
+      default: paged_decode_kernel<8, true><<<a.nwaves, 64, 0, stream>>>(a); break;
+    }
+  } else {
+    switch (group) {
+      case 1: paged_decode_kernel<1><<<a.nwaves, 64, 0, stream>>>(a); break;
+      case 2: paged_decode_kernel<2><<<a.nwaves, 64, 0, stream>>>(a); break;
+      case 4: paged_decode_kernel<4><<<a.nwaves, 64, 0, stream>>>(a); break;
+      default: paged_decode_kernel<8><<<a.nwaves, 64, 0, stream>>>(a); break;
+    }
   }
   XV_CHECK_LAUNCH();
   merge_parts_kernel<<<dim3((unsigned)(batch * num_q_heads)), 64, 0, stream>>>(a);
@@ -1061,7 +1240,7 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
 int decode_check(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
                  const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride, void* out,
                  int64_t out_stride_tok, int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-                 int max_blocks_per_seq) {
+                 int max_blocks_per_seq, bool f8 = false) {
   if (head_dim != kD || block_size <= 0 || block_size % kPage || batch < 0 || num_kv_heads <= 0 ||
       num_q_heads % num_kv_heads || max_blocks_per_seq <= 0)
     return (int)hipErrorInvalidValue;
@@ -1070,8 +1249,8 @@ int decode_check(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   const int64_t max_pages = pages_per_seq(max_blocks_per_seq, block_size);
   if (max_pages > (1 << 24)) return (int)hipErrorInvalidValue;  // 256M tokens per sequence
   // rows move by 16-byte LDS-DMA: aligned bases, strides in whole 16-byte units
-  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 ||
-      (q_stride_tok | q_stride_head | page_stride | tok_stride | head_stride) & 7)
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15 || (q_stride_tok | q_stride_head) & 7 ||
+      (page_stride | tok_stride | head_stride) & (f8 ? 15 : 7))  // cache strides in elements: 2 or 1 bytes
     return (int)hipErrorInvalidValue;
   if ((uintptr_t)out & 3 || out_stride_tok & 1) return (int)hipErrorInvalidValue;  // bf16 pairs stored as 4 bytes
   return 0;
@@ -1084,10 +1263,10 @@ int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const
                const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens, void* out,
                int64_t out_stride_tok, void* workspace, size_t workspace_bytes, int batch, int num_q_heads,
                int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq, float scale,
-               hipStream_t stream) {
+               hipStream_t stream, bool f8 = false, float k_scale = 1.0f, float v_scale = 1.0f) {
   const int rc0 = decode_check(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride,
                                head_stride, out, out_stride_tok, batch, num_q_heads, num_kv_heads, head_dim,
-                               block_size, max_blocks_per_seq);
+                               block_size, max_blocks_per_seq, f8);
   if (rc0 || batch == 0) return rc0;
   const int64_t max_pages = pages_per_seq(max_blocks_per_seq, block_size);
   for (int c0 = 0; c0 < batch; c0 += kMaxBatch) {
@@ -1095,7 +1274,8 @@ int decode_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const
         (const bf16_t*)q + (int64_t)c0 * q_stride_tok, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride,
         tok_stride, head_stride, block_tables + (int64_t)c0 * bt_stride, bt_stride, cache_seqlens + c0,
         (bf16_t*)out + (int64_t)c0 * out_stride_tok, out_stride_tok, workspace, workspace_bytes,
-        min(kMaxBatch, batch - c0), num_q_heads, num_kv_heads, block_size / kPage, (int)max_pages, scale, stream);
+        min(kMaxBatch, batch - c0), num_q_heads, num_kv_heads, block_size / kPage, (int)max_pages,
+        f8 ? scale * k_scale : scale, stream, CascadeParts(), f8, f8 ? v_scale : 1.0f);
     if (rc) return rc;
   }
   return 0;
@@ -1116,6 +1296,27 @@ extern "C" int xv_paged_decode_attention(const void* q, int64_t q_stride_tok, in
   return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
                     block_tables, bt_stride, cache_seqlens, out, out_stride_tok, workspace, workspace_bytes, batch,
                     num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream);
+}
+
+// fp8 (e4m3fn) K/V pages: the same kernels with a per-page conversion to bf16
+// in LDS; k_scale multiplies the scores (folded into the softmax scale) and
+// v_scale the output.
+extern "C" int xv_paged_decode_attention_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                             const void* k_cache, const void* v_cache,
+                                             int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                             const int32_t* block_tables, int64_t bt_stride,
+                                             const int32_t* cache_seqlens,
+                                             void* out, int64_t out_stride_tok,
+                                             void* workspace, size_t workspace_bytes,
+                                             int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                             int block_size, int max_blocks_per_seq, float scale,
+                                             float k_scale, float v_scale, hipStream_t stream) {
+  if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || !isfinite(k_scale) || !isfinite(v_scale))
+    return (int)hipErrorInvalidValue;
+  return decode_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
+                    block_tables, bt_stride, cache_seqlens, out, out_stride_tok, workspace, workspace_bytes, batch,
+                    num_q_heads, num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream, true,
+                    k_scale, v_scale);
 }
 
 // ---------------------------------------------------------------------------

@@ -125,6 +125,95 @@ extern "C" int xv_store_kvcache(const void* key, int64_t key_stride_tok, int64_t
   return 0;
 }
 
+// fp8 (e4m3fn) cache: each bf16 value x is stored as e4m3fn(x * inv_scale)
+// (one fp32 multiply, then the hardware's round-to-nearest-even conversion,
+// which gives torch's float8_e4m3fn cast of the product: values past the
+// format's range become NaN, as there).  Same unit structure as the bf16
+// wave kernel: a lane's 16-byte chunk of 8 values becomes 8 bytes.
+template <int U>
+__global__ __launch_bounds__(256) void store_kvcache_fp8_kernel(
+    const bf16_t* __restrict__ key, int64_t ks_tok, int64_t ks_head,
+    const bf16_t* __restrict__ value, int64_t vs_tok, int64_t vs_head,
+    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+    int64_t cs_page, int64_t cs_tok, int64_t cs_head, int block_size, const int32_t* __restrict__ slots,
+    int num_units, int units_per_tok, int chunks_per_head, float k_inv, float v_inv) {
+  const int u0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + (threadIdx.x >> 6)) * U);
+  if (u0 >= num_units) return;
+  const int lane = threadIdx.x & 63;
+  int tok[U];
+  int64_t hd[U];
+  Vec8 kv[U], vv[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    const int u = min(u0 + j, num_units - 1);
+    tok[j] = u / units_per_tok;
+    const int c = (u - tok[j] * units_per_tok) * 64 + lane;
+    const int h = c / chunks_per_head;
+    const int d = (c - h * chunks_per_head) * 8;
+    hd[j] = h * cs_head + d;
+    kv[j] = load_vec8_nt(key + tok[j] * ks_tok + h * ks_head + d);
+    vv[j] = load_vec8_nt(value + tok[j] * vs_tok + h * vs_head + d);
+  }
+  int slot[U];
+#pragma unroll
+  for (int j = 0; j < U; ++j) slot[j] = __builtin_amdgcn_readfirstlane(slots[tok[j]]);
+#pragma unroll
+  for (int j = 0; j < U; ++j) { pin_vec8(kv[j]); pin_vec8(vv[j]); }
+  auto to_fp8 = [](const Vec8& x, float inv) {
+    float f[8];
+    unpack8(x, f);
+    uint32_t lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0] * inv, f[1] * inv, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4] * inv, f[5] * inv, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6] * inv, f[7] * inv, hi, true);
+    return make_uint2(lo, hi);
+  };
+#pragma unroll
+  for (int j = 0; j < U; ++j) {
+    if (u0 + j >= num_units || slot[j] < 0) continue;  // padding token (slot -1) writes nothing
+    const int page = slot[j] / block_size;
+    const int t = slot[j] - page * block_size;
+    const int64_t dst = (int64_t)page * cs_page + (int64_t)t * cs_tok + hd[j];
+    *reinterpret_cast<uint2*>(k_cache + dst) = to_fp8(kv[j], k_inv);
+    *reinterpret_cast<uint2*>(v_cache + dst) = to_fp8(vv[j], v_inv);
+  }
+}
+
+extern "C" int xv_store_kvcache_fp8(const void* key, int64_t key_stride_tok, int64_t key_stride_head,
+                                    const void* value, int64_t value_stride_tok, int64_t value_stride_head,
+                                    void* k_cache, void* v_cache,
+                                    int64_t cache_page_stride, int64_t cache_tok_stride, int64_t cache_head_stride,
+                                    int block_size, const int32_t* slot_mapping, int64_t num_tokens,
+                                    int num_kv_heads, int head_dim, float k_scale, float v_scale,
+                                    hipStream_t stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || block_size <= 0)
+    return (int)hipErrorInvalidValue;
+  if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || !__builtin_isfinite(k_scale) || !__builtin_isfinite(v_scale))
+    return (int)hipErrorInvalidValue;
+  // bf16 rows as 16-byte chunks; fp8 cache rows as 8-byte pieces
+  if (!xv_al16(key) || !xv_al16(value) || ((uintptr_t)k_cache | (uintptr_t)v_cache) & 7 ||
+      !xv_st8(key_stride_tok) || !xv_st8(key_stride_head) || !xv_st8(value_stride_tok) ||
+      !xv_st8(value_stride_head) || (cache_page_stride | cache_tok_stride | cache_head_stride) & 7)
+    return (int)hipErrorInvalidValue;
+  if (num_tokens == 0) return 0;
+  const int cph = head_dim / 8;
+  const int cpt = cph * num_kv_heads;
+  if (cpt % 64) return (int)hipErrorInvalidValue;  // whole 64-chunk units per token (Hkv * D a multiple of 512)
+  if (num_tokens * cpt >= ((int64_t)1 << 31)) return (int)hipErrorInvalidValue;
+  const int upt = cpt / 64;
+  const int units = (int)num_tokens * upt;
+  const float k_inv = 1.0f / k_scale, v_inv = 1.0f / v_scale;
+  constexpr int kU = 2;
+  const int waves = (units + kU - 1) / kU;
+  store_kvcache_fp8_kernel<kU><<<dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, stream>>>(
+      (const bf16_t*)key, key_stride_tok, key_stride_head, (const bf16_t*)value, value_stride_tok, value_stride_head,
+      (uint8_t*)k_cache, (uint8_t*)v_cache, cache_page_stride, cache_tok_stride, cache_head_stride, block_size,
+      slot_mapping, units, upt, cph, k_inv, v_inv);
+  XV_CHECK_LAUNCH();
+  return 0;
+}
+
 // --------------------------------------------------------------------------
 // RMSNorm family.  TPR lanes own one row (16 = a DPP row, 64 = a wave); each
 // lane keeps up to VPT 8-element vectors of the row in registers.

@@ -17,11 +17,19 @@ SIGNATURES: dict[str, tuple] = {
     "xv_error_string": (C.c_char_p, [i32]),
     "xv_abi_version": (i32, []),
     "xv_store_kvcache": (i32, [vp, i64, i64, vp, i64, i64, vp, vp, i64, i64, i64, i32, vp, i64, i32, i32, vp]),
+    "xv_store_kvcache_fp8": (
+        i32, [vp, i64, i64, vp, i64, i64, vp, vp, i64, i64, i64, i32, vp, i64, i32, i32, f32, f32, vp]
+    ),
     "xv_paged_decode_workspace_size": (sz, [i32, i32, i32, i32, i32, i32]),
     "xv_paged_decode_attention": (
         i32,
         [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, i64, vp, sz,
          i32, i32, i32, i32, i32, i32, f32, vp],
+    ),
+    "xv_paged_decode_attention_fp8": (
+        i32,
+        [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, i64, vp, sz,
+         i32, i32, i32, i32, i32, i32, f32, f32, f32, vp],
     ),
     "xv_paged_decode_attention_noalloc": (
         i32,

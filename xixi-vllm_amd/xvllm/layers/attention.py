@@ -116,12 +116,20 @@ def paged_decode_attention(
     head_dim: int,
     softmax_scale: float | None = None,
     out: torch.Tensor | None = None,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Causal decode over the paged cache: q [B, Hq*D] (or [B, Hq, D]),
     k_cache/v_cache [NB, BS, Hkv, D], block_tables int32 [B, max_blocks],
-    cache_seqlens int32 [B] (0 = padding row) -> [B, Hq*D]."""
+    cache_seqlens int32 [B] (0 = padding row) -> [B, Hq*D].  An fp8 cache
+    (torch.float8_e4m3fn, written by store_kvcache with the same scales)
+    attends to k_cache * k_scale and v_cache * v_scale."""
     require_cuda(q, k_cache, v_cache, block_tables, cache_seqlens)
-    require_bf16(q, k_cache, v_cache)
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    require_bf16(q, *(() if fp8 else (k_cache, v_cache)))
+    if fp8 and v_cache.dtype != torch.float8_e4m3fn:
+        raise TypeError("k_cache and v_cache must share one dtype")
     q3, qs0, qs1 = _q_view(q, num_qo_heads, head_dim)
     bsz = q3.shape[0]
     nb, page, hkv, d = k_cache.shape
@@ -138,6 +146,17 @@ def paged_decode_attention(
     ws_bytes = L.xv_paged_decode_workspace_size(bsz, num_qo_heads, num_kv_heads, max_blocks, page, head_dim)
     ws = decode_workspace(q.device, ws_bytes)
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
+    if fp8:
+        _C.check(
+            L.xv_paged_decode_attention_fp8(
+                ptr(q3), qs0, qs1, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
+                k_cache.stride(2), ptr(bt), bt.stride(0), ptr(sl), ptr(out), out.stride(0), ptr(ws), ws.numel(),
+                bsz, num_qo_heads, num_kv_heads, head_dim, page, max_blocks, float(scale), float(k_scale),
+                float(v_scale), stream_of(q),
+            ),
+            "xv_paged_decode_attention_fp8",
+        )
+        return out
     _C.check(
         L.xv_paged_decode_attention(
             ptr(q3), qs0, qs1, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1),
