@@ -415,7 +415,15 @@ XV_INLINE void process_page(SplitState& st, const char* buf, char* img, const La
   } else {
     read_page<kPageOps<false> * (NB - 1)>(pr, buf, lo);
   }
+#ifdef XV_NO_MATH
+  // timing probe: consume the operands without the MFMA/softmax work
+  float acc = 0.f;
+  for (int j = 0; j < 4; ++j) acc += (float)pr.kr[j][0];
+  for (int n = 0; n < 8; ++n) acc += (float)pr.vt[n][0];
+  st.l += acc;
+#else
   page_math<G>(st, pr, qb, page_tok0, ctx, scale_log2, lane);
+#endif
 }
 
 // Stream positions per half of the page-id table.
@@ -468,9 +476,18 @@ template <int G, bool F8> constexpr int kPageBufBytes = F8 ? kF8PageBytes : kPag
 template <int G, bool F8> constexpr int kBufBytesT = kPageBufBytes<G, F8> + kQSlot<G>;
 // Page buffers per wave: 4 (3 at G = 8) keeps four waves' LDS within a CU.
 template <int G> constexpr int kNbufG = G <= 4 ? 4 : 3;
-// fp8 pages: the same count (4, 5 or 6 buffers measured alike: the fp8
-// kernel's pace is set by its per-page work, not by the bytes in flight)
-template <int G, bool F8> constexpr int kNbufT = kNbufG<G>;
+// fp8 pages: two waves per SIMD with two page buffers each.  One wave per
+// SIMD left the fp8 kernel paced by its per-page chain (page wait, LDS reads,
+// conversion, V image round trip, math; 93 us at config 2, 69 us with the
+// math removed); a second wave on the SIMD overlaps one wave's chain with
+// the other's, 66 us.  The buffers shrink to fit eight waves' LDS in a CU.
+#ifndef XV_F8_WPE
+#define XV_F8_WPE 2
+#endif
+#ifndef XV_F8_NB
+#define XV_F8_NB 2
+#endif
+template <int G, bool F8> constexpr int kNbufT = (F8 && XV_F8_NB > 0) ? XV_F8_NB : kNbufG<G>;
 
 template <int G>
 XV_INLINE void issue_q(char* slot, const DecodeArgs& a, int b, int kvh, int lane) {
@@ -621,7 +638,8 @@ XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
 #endif
 
 template <int G, bool F8 = false>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(XV_DECODE_WPE, XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_WPE : XV_DECODE_WPE,
+                                                                      F8 ? XV_F8_WPE : XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
   XV_DECODE_TIMESTAMP(0);
   constexpr int NB = kNbufT<G, F8>;
   constexpr int BUF = kBufBytesT<G, F8>;
@@ -1120,22 +1138,28 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   }
 }
 
-int waves_for(int group) {
+template <bool F8>
+int occupancy(int group) {
+  int per_cu = 0;
+  switch (group) {
+    case 1: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<1, F8>, 64, 0); break;
+    case 2: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<2, F8>, 64, 0); break;
+    case 4: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<4, F8>, 64, 0); break;
+    default: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<8, F8>, 64, 0); break;
+  }
+  return per_cu;
+}
+int waves_for(int group, bool f8 = false) {
   // resident single-wave workgroups: CUs x per-CU occupancy (queried once per device)
-  static int cached[4] = {0, 0, 0, 0};
-  const int slot = group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3;
+  static int cached[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  const int slot = (group == 1 ? 0 : group == 2 ? 1 : group == 4 ? 2 : 3) + (f8 ? 4 : 0);
   if (cached[slot]) return cached[slot];
-  int dev = 0, cus = 0, per_cu = 0;
+  int dev = 0, cus = 0;
   hipGetDevice(&dev);
   hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-  switch (group) {
-    case 1: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<1>, 64, 0); break;
-    case 2: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<2>, 64, 0); break;
-    case 4: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<4>, 64, 0); break;
-    default: hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, paged_decode_kernel<8>, 64, 0); break;
-  }
+  int per_cu = f8 ? occupancy<true>(group) : occupancy<false>(group);
 #if XV_DECODE_WAVES_PER_CU > 0
-  per_cu = min(per_cu, XV_DECODE_WAVES_PER_CU);
+  per_cu = min(per_cu, XV_DECODE_WAVES_PER_CU * (f8 ? XV_F8_WPE : 1));
 #endif
   cached[slot] = max(1, cus) * max(1, per_cu);
   return cached[slot];
@@ -1211,7 +1235,7 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin; a.nsub = nsub;
   // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_pages;
-  a.nwaves = (int)min((int64_t)waves_for(group), (max_total + lmin - 1) / lmin);
+  a.nwaves = (int)min((int64_t)waves_for(group, f8), (max_total + lmin - 1) / lmin);
   a.scale_log2 = scale * 1.4426950408889634f;
   a.v_scale = v_scale;
   a.pre_tokens = cp.pre_tokens; a.pre_chunk_pages = cp.chunk_pages; a.pre_o = cp.pre_o; a.pre_lse = cp.pre_lse;
