@@ -345,10 +345,12 @@ def kernel_suite(torch, dev) -> dict:
     return out
 
 
-def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = False) -> dict:
+def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = False, fp8: bool = False,
+               model=None):
     """Qwen3-8B (36 layers, random bf16 weights ~N(0,0.02)) decode step at the
     given per-sequence contexts: hipGraph replay of the decode body + LM head +
-    sampler, steady state (metadata staged once)."""
+    sampler, steady state (metadata staged once).  fp8: the KV pool in the
+    optional fp8 (e4m3fn) page format.  Returns (record, model)."""
     from xvllm.batch import SeqSchedule
     from xvllm.config import QWEN3_8B
     from xvllm.kv_pool import KVPool
@@ -362,11 +364,22 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(dev):
-            model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
-            kv = KVPool(cfg, num_blocks=pool, block_size=PAGE, device=dev, dtype=torch.bfloat16)
+            if model is None:
+                model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
+            if fp8:
+                kv = KVPool(cfg, num_blocks=pool, block_size=PAGE, device=dev, dtype=torch.float8_e4m3fn,
+                            k_scale=FP8_SCALE, v_scale=FP8_SCALE)
+            else:
+                kv = KVPool(cfg, num_blocks=pool, block_size=PAGE, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
-    kv.kv_cache.normal_()
+    if fp8:  # N(0, 1) values in fp8 at scale 1/8, one layer at a time
+        for i in range(2):
+            for layer in range(kv.num_layers):
+                view = kv.kv_cache[i, layer]
+                view.copy_((torch.randn(view.shape, device=dev) / FP8_SCALE).to(torch.float8_e4m3fn))
+    else:
+        kv.kv_cache.normal_()
     max_ctx = max(ctx) + 1
     runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=max_ctx, device=dev)
     g = torch.Generator().manual_seed(11)
@@ -395,14 +408,16 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
-    kvbytes = sum(ctx) * cfg.num_hidden_layers * cfg.num_key_value_heads * 128 * 2 * 2
+    kvbytes = sum(ctx) * cfg.num_hidden_layers * cfg.num_key_value_heads * 128 * 2 * (1 if fp8 else 2)
     roof_ms = (wbytes + kvbytes) / (HBM_PEAK_GBS * 1e9) * 1e3
     runner.destroy()
+    del kv, runner
     assert ids.shape[0] == bsz
     return {"batch": bsz, "mean_ctx": round(sum(ctx) / bsz, 1), "sampling": "T0.7/k50/p0.9" if sampled else "greedy",
+            "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
             "ms_per_step": round(ms, 4), "tok_per_s": round(bsz / (ms * 1e-3), 1),
             "roofline_ms": round(roof_ms, 4), "roofline_tok_per_s": round(bsz / (roof_ms * 1e-3), 1),
-            "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}
+            "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}, model
 
 
 def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bool = True, model=None):
@@ -500,7 +515,7 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
 
 
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
-              max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, model=None) -> dict:
+              max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, model=None, fp8: bool = False) -> dict:
     """Config 4: Qwen3-8B (random bf16 weights ~N(0,0.02)) serving 256 requests
     with random-token prompts of U[128, 2048] tokens, each generating `gen`
     tokens (EOS ignored), under continuous batching with the reference
@@ -526,7 +541,11 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
         with torch.device(dev):
             if model is None:
                 model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
-            kv = KVPool(cfg, num_blocks=pages_needed + 16, block_size=PAGE, device=dev, dtype=torch.bfloat16)
+            if fp8:  # the optional fp8 (e4m3fn) page format
+                kv = KVPool(cfg, num_blocks=pages_needed + 16, block_size=PAGE, device=dev,
+                            dtype=torch.float8_e4m3fn, k_scale=FP8_SCALE, v_scale=FP8_SCALE)
+            else:
+                kv = KVPool(cfg, num_blocks=pages_needed + 16, block_size=PAGE, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
     samp = dict(temperature=0.7, top_p=0.9, top_k=50) if sampled else None
@@ -542,7 +561,8 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
     out_tokens = sum(len(o) for o in outs)
     assert out_tokens == n_req * gen
     return {"requests": n_req, "prompt_tokens": sum(plens), "generated_tokens": out_tokens, "steps": st.steps,
-            "sampling": "T0.7/k50/p0.9" if sampled else "greedy", "wall_s": round(st.wall_s, 3),
+            "sampling": "T0.7/k50/p0.9" if sampled else "greedy", "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
+            "wall_s": round(st.wall_s, 3),
             "output_tok_per_s": round(out_tokens / st.wall_s, 1),
             "total_tok_per_s": round((out_tokens + sum(plens)) / st.wall_s, 1),
             "host_s_before_sync": round(st.host_s, 3),
@@ -715,7 +735,9 @@ def main() -> int:
     g = torch.Generator().manual_seed(args.seed)
     ctx = torch.randint(512, 4097, (64,), generator=g).tolist()
     if args.e2e_only:
-        print(json.dumps(decode_e2e(torch, dev, ctx, steps=args.steps)))
+        rec, model = decode_e2e(torch, dev, ctx, steps=args.steps)
+        rec8, model = decode_e2e(torch, dev, ctx, steps=args.steps, fp8=True, model=model)
+        print(json.dumps({"decode_e2e": rec, "decode_e2e_fp8": rec8}))
         return 0
     if args.config5_only:
         c5, model = decode_config5(torch, dev, cascade=False)
@@ -725,7 +747,8 @@ def main() -> int:
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)
         sampled, model = serve_e2e(torch, dev, sampled=True, model=model)
-        print(json.dumps({"serve_greedy": greedy, "serve_sampled": sampled}))
+        greedy8, model = serve_e2e(torch, dev, sampled=False, model=model, fp8=True)
+        print(json.dumps({"serve_greedy": greedy, "serve_sampled": sampled, "serve_greedy_fp8": greedy8}))
         return 0
     if args.prefill_only:
         print(json.dumps(prefill_suite(torch, dev, iters=args.steps)))
@@ -813,8 +836,12 @@ def main() -> int:
     if not args.no_e2e:
         del cases
         torch.cuda.empty_cache()
-        line["decode_e2e"] = decode_e2e(torch, dev, ctx)
+        line["decode_e2e"], model = decode_e2e(torch, dev, ctx)
         line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
+        # the same step on an fp8 (e4m3fn) KV pool, the pool's optional page format
+        line["decode_e2e_fp8"], model = decode_e2e(torch, dev, ctx, fp8=True, model=model)
+        del model
+        torch.cuda.empty_cache()
     if args.config5:
         torch.cuda.empty_cache()
         line["config5"], model = decode_config5(torch, dev, cascade=False)
@@ -825,6 +852,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["serve_greedy"], model = serve_e2e(torch, dev, sampled=False)
         line["serve_sampled"], model = serve_e2e(torch, dev, sampled=True, model=model)
+        line["serve_greedy_fp8"], model = serve_e2e(torch, dev, sampled=False, model=model, fp8=True)
         del model
         torch.cuda.empty_cache()
     if not args.no_cpu:

@@ -128,6 +128,22 @@ int xv_paged_decode_attention_fp8(const void* q, int64_t q_stride_tok, int64_t q
                                   float k_scale, float v_scale, hipStream_t stream);
 
 /*
+ * Chunked prefill over fp8 pages: every sequence's keys (cache rows 0 ..
+ * cu_seqlens_k[b+1] - cu_seqlens_k[b] - 1 through its block table, the
+ * cached prefix and this chunk, already stored) dequantized as
+ * bf16(value * scale) into rows cu_seqlens_k[b] + t of k_out / v_out
+ * ([T_k, Hkv, 128] at out_stride_tok), the varlen k/v that
+ * xv_prefill_attention then reads.  No counterpart in the reference (fp8 pool
+ * format); max_seqlen_k bounds every sequence's keys.  Cache strides in
+ * elements (= bytes), multiples of 8.
+ */
+int xv_gather_kv_fp8(const void* k_cache, const void* v_cache, int64_t cache_page_stride,
+                     int64_t cache_tok_stride, int64_t cache_head_stride, const int32_t* block_tables,
+                     int64_t bt_stride, int block_size, const int32_t* cu_seqlens_k, int batch,
+                     int max_seqlen_k, int num_kv_heads, int head_dim, float k_scale, float v_scale,
+                     void* k_out, void* v_out, int64_t out_stride_tok, hipStream_t stream);
+
+/*
  * Shared-prefix (cascade) decode attention: xv_paged_decode_attention for a
  * batch whose rows may share their first tokens' cache blocks, as a radix
  * prefix cache maps them (the reference's prefix index,
@@ -304,6 +320,19 @@ int xv_qk_norm_rope_store(const void* q, int64_t q_stride_tok, int64_t q_stride_
                           int64_t cache_tok_stride, int64_t cache_head_stride, int block_size,
                           const int32_t* slot_mapping, int64_t num_tokens, int num_q_heads,
                           int num_kv_heads, int head_dim, hipStream_t stream);
+/* The same over an fp8 (e4m3fn) cache: the roped k (rounded to bf16) and v are
+ * stored as e4m3fn(x * (1/scale)), as xv_store_kvcache_fp8 stores them.  No
+ * counterpart in the reference (fp8 pool format). */
+int xv_qk_norm_rope_store_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                              const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                              const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                              const void* q_weight, const void* k_weight, float eps,
+                              const int64_t* positions, const float* cos_sin_cache, void* q_out,
+                              void* k_cache, void* v_cache, int64_t cache_page_stride,
+                              int64_t cache_tok_stride, int64_t cache_head_stride, int block_size,
+                              const int32_t* slot_mapping, int64_t num_tokens, int num_q_heads,
+                              int num_kv_heads, int head_dim, float k_scale, float v_scale,
+                              hipStream_t stream);
 
 /*
  * SiLU-and-mul.

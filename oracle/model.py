@@ -21,10 +21,12 @@ def linear(x, w):
 
 
 def decode_layer(w: dict, hidden, residual, positions, k_cache, v_cache, block_tables, seqlens, slots, cos_sin,
-                 hq: int, hkv: int, d: int, eps: float):
+                 hq: int, hkv: int, d: int, eps: float, kv_fp8: tuple | None = None):
     """One decoder layer for a decode batch.  Mutates k_cache/v_cache (stores
     this step's K/V).  Returns dict(attn=attention output [B, Hq*D],
-    hidden=layer output, residual=residual stream)."""
+    hidden=layer output, residual=residual stream).  kv_fp8 = (k_scale,
+    v_scale): the caches hold dequantized fp8 pages (this build's optional
+    pool format), and this step's K/V are stored as the fp8 store rounds them."""
     if residual is None:
         x, residual = O.rmsnorm(hidden, w["input_layernorm"], eps), round_bf16(hidden)
     else:
@@ -35,6 +37,10 @@ def decode_layer(w: dict, hidden, residual, positions, k_cache, v_cache, block_t
     k = qkv[:, hq * d : (hq + hkv) * d].reshape(t, hkv, d)
     v = qkv[:, (hq + hkv) * d :].reshape(t, hkv, d)
     q, k = O.qk_norm_rope(q, k, w["q_norm"], w["k_norm"], eps, positions, cos_sin)
+    if kv_fp8 is not None:
+        ks, vs = (np.float32(x) for x in kv_fp8)
+        k = O.dequantize_fp8(O.quantize_fp8(k, np.float32(1.0) / ks), ks)
+        v = O.dequantize_fp8(O.quantize_fp8(v, np.float32(1.0) / vs), vs)
     O.store_kvcache(k, v, k_cache, v_cache, slots)
     attn = round_bf16(O.paged_decode_attention(q, k_cache, v_cache, block_tables, seqlens).astype(np.float32))
     attn = attn.reshape(t, hq * d)

@@ -176,3 +176,120 @@ def test_fp8_store_then_decode_round_trip(dev):
     kq_want = O.quantize_fp8(f32(key), np.float32(1.0) / np.float32(ks))
     sls = slots.numpy()
     assert np.array_equal(kq.reshape(-1, hkv, d)[sls], kq_want)
+
+
+def test_qk_norm_rope_store_fp8_equals_bf16_store_then_quantize(dev):
+    """The fused decode store into an fp8 cache writes exactly the fp8 codes
+    of what the bf16 fused store writes (roped k and v, rounded to bf16),
+    and returns the same q."""
+    import xvllm.layers.ops  # noqa: F401
+    from xvllm.layers.rotary import build_cos_sin_cache
+
+    g = gen(91)
+    t, hq, hkv, d, nb, page = 37, 32, 8, 128, 12, 16
+    qkv = randn_bf16((t, (hq + 2 * hkv) * d), g, std=2.0).to(dev)
+    q = qkv[:, : hq * d].view(t, hq, d)
+    k = qkv[:, hq * d : (hq + hkv) * d].view(t, hkv, d)
+    v = qkv[:, (hq + hkv) * d :].view(t, hkv, d)
+    qw, kw = randn_bf16((d,), g, 0.1, 1.0).to(dev), randn_bf16((d,), g, 0.1, 1.0).to(dev)
+    pos = torch.randint(0, 4096, (t,), generator=g).to(dev)
+    cs = build_cos_sin_cache(d, 4096, 1e6).to(dev)
+    slots = torch.randperm(nb * page, generator=g)[:t].to(torch.int32)
+    slots[::6] = -1
+    slots = slots.to(dev)
+    kb = torch.zeros((nb, page, hkv, d), dtype=torch.bfloat16, device=dev)
+    vb = torch.zeros_like(kb)
+    k8 = torch.zeros((nb, page, hkv, d), dtype=torch.float8_e4m3fn, device=dev)
+    v8 = torch.zeros_like(k8)
+    ks, vs = 0.03, 0.5
+    qa = torch.ops.xv.qk_norm_rope_store(q, k, v, qw, kw, 1e-6, pos, cs, kb, vb, slots)
+    qb = torch.ops.xv.qk_norm_rope_store(q, k, v, qw, kw, 1e-6, pos, cs, k8, v8, slots, ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(qa.view(torch.int16), qb.view(torch.int16))
+    sl = slots.cpu().numpy()
+    sl = sl[sl >= 0]
+    kq = O.quantize_fp8(f32(kb).reshape(-1, hkv, d)[sl], np.float32(1.0) / np.float32(ks))
+    vq = O.quantize_fp8(f32(vb).reshape(-1, hkv, d)[sl], np.float32(1.0) / np.float32(vs))
+    assert np.array_equal(k8.cpu().view(torch.uint8).numpy().reshape(-1, hkv, d)[sl], kq)
+    assert np.array_equal(v8.cpu().view(torch.uint8).numpy().reshape(-1, hkv, d)[sl], vq)
+
+
+def test_chunked_prefill_over_fp8_pages(dev):
+    """Chunked prefill whose keys (cached prefix + chunk) come from fp8 pages
+    through the block tables: the oracle's causal attention over the
+    dequantized pages, within the bf16 tolerance."""
+    from xvllm.layers.attention import prefill_attention
+
+    g = gen(123)
+    hq, hkv, d, page = 32, 8, 128, 16
+    pre, new = [40, 0, 300, 17], [24, 33, 1, 64]
+    klens = [p_ + n_ for p_, n_ in zip(pre, new)]
+    need = [(k_ + page - 1) // page for k_ in klens]
+    kc, vc, bt, _ = make_paged(klens, sum(need) + 5, hkv, d, g)
+    ks, vs = 0.05, 0.1
+    kq = O.quantize_fp8(f32(kc), np.float32(1.0) / np.float32(ks))
+    vq = O.quantize_fp8(f32(vc), np.float32(1.0) / np.float32(vs))
+    q = randn_bf16((sum(new), hq, d), g)
+    cu_q = torch.tensor([0] + np.cumsum(new).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + np.cumsum(klens).tolist(), dtype=torch.int32)
+    out = prefill_attention(q.view(sum(new), -1).to(dev), None, None, cu_q.to(dev), cu_k.to(dev), max(new), hq, hkv,
+                            d, k_cache=_to_fp8(kq).to(dev), v_cache=_to_fp8(vq).to(dev), block_tables=bt.to(dev),
+                            max_seqlen_k=max(klens), kv_scale=(ks, vs))
+    torch.cuda.synchronize()
+    want = O.prefill_attention(f32(q), cu_q.numpy(), cu_k.numpy(), k_cache=O.dequantize_fp8(kq, ks),
+                               v_cache=O.dequantize_fp8(vq, vs), block_tables=bt.numpy())
+    _close(f32(out).reshape(-1, hq, d), want)
+
+
+def test_config1_layer_decode_on_fp8_pool(dev):
+    """Config 1's decoder layer with an fp8 pool (scales 1/16 and 1/8): the
+    layer stores this step's K/V as fp8 and attends over fp8 pages; the
+    oracle layer on the dequantized pages (its store rounds K/V the same
+    way) matches the attention output and the layer output at the bf16
+    tolerance."""
+    from test_gpu_model import D, EPS, FFN, HIDDEN, HKV, HQ, _layer_case
+    import oracle.model as OM
+    from xvllm.config import Qwen3Shape
+    from xvllm.layers.attention import AttnInputs, AttnMetadata, attention_context
+    from xvllm.layers.rotary import build_cos_sin_cache
+    from xvllm.models.qwen3 import Qwen3DecoderLayer
+
+    ctx, bt, w, kc, vc, hidden, pos, slots = _layer_case(seed=5)
+    ks, vs = 1.0 / 16, 1.0 / 8
+    kq = O.quantize_fp8(f32(kc), np.float32(1.0) / np.float32(ks))
+    vq = O.quantize_fp8(f32(vc), np.float32(1.0) / np.float32(vs))
+    cfg = Qwen3Shape(HIDDEN, HQ, HKV, D, FFN, 1, max_position_embeddings=4096)
+    with torch.device(dev):
+        layer = Qwen3DecoderLayer(cfg, 0).to(torch.bfloat16)
+        layer.self_attn.rotary_emb.cos_sin_cache = build_cos_sin_cache(D, 4096, 1e6).to(dev)
+    with torch.no_grad():
+        for name, mod in (("qkv_proj", layer.self_attn), ("o_proj", layer.self_attn), ("gate_up_proj", layer.mlp),
+                          ("down_proj", layer.mlp)):
+            getattr(mod, name).copy_(w[name])
+        layer.self_attn.q_norm.weight.copy_(w["q_norm"])
+        layer.self_attn.k_norm.weight.copy_(w["k_norm"])
+        layer.input_layernorm.weight.copy_(w["input_layernorm"])
+        layer.post_attention_layernorm.weight.copy_(w["post_attention_layernorm"])
+    pool = torch.stack([_to_fp8(kq), _to_fp8(vq)])[:, None].to(dev)
+    attn_in = AttnInputs(slot_mapping=slots.to(dev), is_prefill=False,
+                         cache_seqlens=torch.tensor(ctx, dtype=torch.int32, device=dev), block_tables=bt.to(dev))
+    captured = {}
+    orig = layer.self_attn.attn.forward
+
+    def spy(q, k, v, a):
+        captured["attn"] = orig(q, k, v, a)
+        return captured["attn"]
+
+    layer.self_attn.attn.forward = spy
+    with torch.no_grad(), attention_context(AttnMetadata(pool, k_scale=ks, v_scale=vs)):
+        h, res = layer(pos.to(dev), hidden.to(dev), None, attn_in)
+    torch.cuda.synchronize()
+    cs = O.build_cos_sin_cache(D, 4096, 1e6)
+    wn = {k2: f32(v2) for k2, v2 in w.items()}
+    kcn, vcn = O.dequantize_fp8(kq, ks), O.dequantize_fp8(vq, vs)
+    ref = OM.decode_layer(wn, f32(hidden), None, pos.numpy(), kcn, vcn, bt.numpy(), np.array(ctx), slots.numpy(), cs,
+                          HQ, HKV, D, EPS, kv_fp8=(ks, vs))
+    _close(f32(captured["attn"]), ref["attn"])
+    h_ref, r_ref = OM.post_attention(wn, f32(captured["attn"]), f32(hidden), EPS)
+    _close(f32(h), h_ref)
+    _close(f32(res), r_ref)

@@ -21,7 +21,7 @@ pytestmark = pytest.mark.gpu
 V = 151936
 
 
-def _model(dev, layers=2, seed=3, num_blocks=1024):
+def _model(dev, layers=2, seed=3, num_blocks=1024, fp8=False):
     from xvllm.config import Qwen3Shape
     from xvllm.kv_pool import KVPool
     from xvllm.models import Qwen3ForCausalLM
@@ -31,10 +31,17 @@ def _model(dev, layers=2, seed=3, num_blocks=1024):
     try:
         with torch.device(dev):
             model = Qwen3ForCausalLM(cfg).random_init_(seed=seed)
-            kv = KVPool(cfg, num_blocks=num_blocks, block_size=16, device=dev, dtype=torch.bfloat16)
+            if fp8:
+                kv = KVPool(cfg, num_blocks=num_blocks, block_size=16, device=dev, dtype=torch.float8_e4m3fn,
+                            k_scale=0.125, v_scale=0.125)
+            else:
+                kv = KVPool(cfg, num_blocks=num_blocks, block_size=16, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
-    kv.kv_cache.normal_()
+    if fp8:
+        kv.kv_cache.view(torch.uint8).fill_(0x7f)  # NaN: pages are read only where a prompt wrote them
+    else:
+        kv.kv_cache.normal_()
     return model, kv
 
 
@@ -126,3 +133,21 @@ def test_config4_reduced_serving(dev):
     assert s1 == s2, "seeded sampled serving is not reproducible"
     assert all(0 <= t < V for o in s1 + greedy1 for t in o)
     assert s1 != greedy1
+
+
+def test_config4_reduced_serving_fp8_pool(dev):
+    """The same reduced serving run on an fp8 (e4m3fn) KV pool (chunked
+    prefill over fp8 pages, the fused RoPE + fp8 store, fp8 decode under
+    hipGraph; unused pool rows hold NaN): greedy reproducible, sampled steps
+    equal the oracle on the device's logits, every id in range."""
+    model, kv = _model(dev, seed=11, num_blocks=1024, fp8=True)
+    g = torch.Generator().manual_seed(404)
+    prompts = [torch.randint(0, V, (int(n),), generator=g).tolist() for n in torch.randint(16, 301, (24,), generator=g)]
+    gen = 20
+    greedy1, st = _serve(dev, model, kv, prompts, gen, None, 0, check=False)
+    greedy2, _ = _serve(dev, model, kv, prompts, gen, None, 0, check=False)
+    assert greedy1 == greedy2, "greedy serving on the fp8 pool is not reproducible"
+    assert st.steps > gen and st.prefill_tokens == sum(len(p) for p in prompts)
+    samp = dict(temperature=0.7, top_p=0.9, top_k=50)
+    s1, _ = _serve(dev, model, kv, prompts, gen, samp, 7, check=True)
+    assert all(0 <= t < V for o in s1 + greedy1 for t in o)

@@ -214,6 +214,63 @@ extern "C" int xv_store_kvcache_fp8(const void* key, int64_t key_stride_tok, int
   return 0;
 }
 
+// Chunked prefill over fp8 pages: every sequence's keys (cached prefix and
+// this chunk, already stored) dequantized into bf16 rows at cu_seqlens_k[b]
+// + t, the varlen k/v layout xv_prefill_attention reads: bf16(value * scale).
+// One thread per 8-value piece of one (token, kv head).
+__global__ __launch_bounds__(256) void gather_kv_fp8_kernel(
+    const uint8_t* __restrict__ kc, const uint8_t* __restrict__ vc, int64_t ps, int64_t ts, int64_t hs,
+    const int32_t* __restrict__ bt, int64_t bt_stride, int block_size, const int32_t* __restrict__ cu_k, int hkv,
+    float k_scale, float v_scale, bf16_t* __restrict__ ko, bf16_t* __restrict__ vo, int64_t o_st) {
+  const int b = blockIdx.y;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int per_tok = hkv * 16;  // 8-value pieces of a token (D = 128)
+  const int t = (int)(idx / per_tok);
+  const int k0 = cu_k[b];
+  if (t >= cu_k[b + 1] - k0) return;
+  const int rem = (int)(idx - (int64_t)t * per_tok), h = rem >> 4, c = rem & 15;
+  const int64_t blk = bt[(int64_t)b * bt_stride + t / block_size];
+  const int64_t src = blk * ps + (int64_t)(t % block_size) * ts + (int64_t)h * hs + c * 8;
+  const uint2 kq = *reinterpret_cast<const uint2*>(kc + src);
+  const uint2 vq = *reinterpret_cast<const uint2*>(vc + src);
+  auto dq = [](uint2 w, float sc) {
+    float f[8];
+    const uint32_t ww[2] = {w.x, w.y};
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(ww[j], false);
+      const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(ww[j], true);
+      f[4 * j] = lo[0] * sc; f[4 * j + 1] = lo[1] * sc; f[4 * j + 2] = hi[0] * sc; f[4 * j + 3] = hi[1] * sc;
+    }
+    return pack8(f);
+  };
+  const int64_t dst = (int64_t)(k0 + t) * o_st + h * 128 + c * 8;
+  store_vec8(ko + dst, dq(kq, k_scale));
+  store_vec8(vo + dst, dq(vq, v_scale));
+}
+
+extern "C" int xv_gather_kv_fp8(const void* k_cache, const void* v_cache, int64_t cache_page_stride,
+                                int64_t cache_tok_stride, int64_t cache_head_stride, const int32_t* block_tables,
+                                int64_t bt_stride, int block_size, const int32_t* cu_seqlens_k, int batch,
+                                int max_seqlen_k, int num_kv_heads, int head_dim, float k_scale, float v_scale,
+                                void* k_out, void* v_out, int64_t out_stride_tok, hipStream_t stream) {
+  if (head_dim != 128 || batch < 0 || max_seqlen_k < 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      batch > 65535 || !(k_scale > 0.0f) || !(v_scale > 0.0f))
+    return (int)hipErrorInvalidValue;
+  if (((uintptr_t)k_cache | (uintptr_t)v_cache) & 7 || (cache_page_stride | cache_tok_stride | cache_head_stride) & 7 ||
+      !xv_al16(k_out) || !xv_al16(v_out) || !xv_st8(out_stride_tok) || out_stride_tok < (int64_t)num_kv_heads * 128)
+    return (int)hipErrorInvalidValue;
+  if (batch == 0 || max_seqlen_k == 0) return 0;
+  const int64_t pieces = (int64_t)max_seqlen_k * num_kv_heads * 16;
+  if ((pieces + 255) / 256 > 0x7fffffff) return (int)hipErrorInvalidValue;
+  gather_kv_fp8_kernel<<<dim3((unsigned)((pieces + 255) / 256), (unsigned)batch), 256, 0, stream>>>(
+      (const uint8_t*)k_cache, (const uint8_t*)v_cache, cache_page_stride, cache_tok_stride, cache_head_stride,
+      block_tables, bt_stride, block_size, cu_seqlens_k, num_kv_heads, k_scale, v_scale, (bf16_t*)k_out,
+      (bf16_t*)v_out, out_stride_tok);
+  XV_CHECK_LAUNCH();
+  return 0;
+}
+
 // --------------------------------------------------------------------------
 // RMSNorm family.  TPR lanes own one row (16 = a DPP row, 64 = a wave); each
 // lane keeps up to VPT 8-element vectors of the row in registers.
@@ -523,7 +580,20 @@ struct CacheDst {
   int block_size;
   const int32_t* slots;
   const bf16_t* v; int64_t vs_tok, vs_head;
+  float k_inv = 1.0f, v_inv = 1.0f;  // fp8 caches: 1 / scale
 };
+
+// Eight bf16 values x -> e4m3fn(x * inv) as 8 bytes (the fp8 KV store's rule).
+XV_INLINE uint2 vec8_to_fp8(const Vec8& x, float inv) {
+  float f[8];
+  unpack8(x, f);
+  uint32_t lo = 0, hi = 0;
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0] * inv, f[1] * inv, lo, false);
+  lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4] * inv, f[5] * inv, hi, false);
+  hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6] * inv, f[7] * inv, hi, true);
+  return make_uint2(lo, hi);
+}
 
 // One wave per token: 16-lane row r of the wave handles heads r, r+4, r+8, ...
 // The token's position, its fp32 cos/sin row, the norm weights and the slot
@@ -538,7 +608,7 @@ struct CacheDst {
 constexpr int kRopeBatch = XV_ROPE_BATCH;
 constexpr int kRopeRows = XV_ROPE_ROWS;
 
-template <bool NORM, bool STORE>
+template <bool NORM, bool STORE, bool F8 = false>
 __global__ __launch_bounds__(256) void rope_kernel(
     const bf16_t* __restrict__ q, int64_t qs_tok, int64_t qs_head,
     const bf16_t* __restrict__ k, int64_t ks_tok, int64_t ks_head,
@@ -588,7 +658,11 @@ __global__ __launch_bounds__(256) void rope_kernel(
       const int h = h0 + kRopeRows * j;
       if (h >= heads) break;
       if (STORE && h >= nrot) {  // v head: plain copy into the cache
-        if (slot >= 0) store_vec8_nt(cd.vc + cache_off + (int64_t)(h - nrot) * cd.hs, xv[j]);
+        if (slot >= 0) {
+          const int64_t off = cache_off + (int64_t)(h - nrot) * cd.hs;
+          if constexpr (F8) *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(cd.vc) + off) = vec8_to_fp8(xv[j], cd.v_inv);
+          else store_vec8_nt(cd.vc + off, xv[j]);
+        }
         continue;
       }
       const bool is_q = h < hq;
@@ -613,7 +687,12 @@ __global__ __launch_bounds__(256) void rope_kernel(
       if (is_q) {
         store_vec8_nt(q_out + (tok * hq + h) * D + lane * 8, pack8(r));
       } else if constexpr (STORE) {
-        if (slot >= 0) store_vec8_nt(cd.kc + cache_off + (int64_t)(h - hq) * cd.hs, pack8(r));
+        if (slot >= 0) {
+          const int64_t off = cache_off + (int64_t)(h - hq) * cd.hs;
+          // fp8: the roped k rounded to bf16 first, as the unfused store sees it
+          if constexpr (F8) *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(cd.kc) + off) = vec8_to_fp8(pack8(r), cd.k_inv);
+          else store_vec8_nt(cd.kc + off, pack8(r));
+        }
       } else {
         store_vec8_nt(k_out + (tok * hkv + (h - hq)) * D + lane * 8, pack8(r));
       }
@@ -621,7 +700,7 @@ __global__ __launch_bounds__(256) void rope_kernel(
   }
 }
 
-template <bool NORM, bool STORE>
+template <bool NORM, bool STORE, bool F8 = false>
 static int launch_rope_t(const void* q, int64_t qst, int64_t qsh, const void* k, int64_t kst, int64_t ksh,
                          const void* qw, const void* kw, float eps, const int64_t* positions, const float* cs,
                          void* q_out, void* k_out, int64_t T, int hq, int hkv, const CacheDst& cd,
@@ -632,9 +711,9 @@ static int launch_rope_t(const void* q, int64_t qst, int64_t qsh, const void* k,
     return (int)hipErrorInvalidValue;
   if (STORE && (!xv_al16(cd.kc) || !xv_al16(cd.vc) || !xv_al16(cd.v) || !xv_st8(cd.ps) || !xv_st8(cd.ts) ||
                 !xv_st8(cd.hs) || !xv_st8(cd.vs_tok) || !xv_st8(cd.vs_head)))
-    return (int)hipErrorInvalidValue;
+    return (int)hipErrorInvalidValue;  // (fp8 caches: 8-byte pieces, the same element strides suffice)
   const unsigned blocks = (unsigned)((T * kRopeRows + 15) / 16);
-  rope_kernel<NORM, STORE><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
+  rope_kernel<NORM, STORE, F8><<<blocks, 256, 0, stream>>>((const bf16_t*)q, qst, qsh, (const bf16_t*)k, kst, ksh,
                                                        (const bf16_t*)qw, (const bf16_t*)kw, eps, positions, cs,
                                                        (bf16_t*)q_out, (bf16_t*)k_out, T, hq, hkv, cd);
   XV_CHECK_LAUNCH();
@@ -673,6 +752,31 @@ extern "C" int xv_qk_norm_rope_store(const void* q, int64_t q_stride_tok, int64_
   return launch_rope_t<true, true>(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, q_weight, k_weight,
                                    eps, positions, cos_sin_cache, q_out, nullptr, num_tokens, num_q_heads,
                                    num_kv_heads, cd, stream);
+}
+
+extern "C" int xv_qk_norm_rope_store_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                         const void* k, int64_t k_stride_tok, int64_t k_stride_head,
+                                         const void* v, int64_t v_stride_tok, int64_t v_stride_head,
+                                         const void* q_weight, const void* k_weight, float eps,
+                                         const int64_t* positions, const float* cos_sin_cache, void* q_out,
+                                         void* k_cache, void* v_cache, int64_t cache_page_stride,
+                                         int64_t cache_tok_stride, int64_t cache_head_stride, int block_size,
+                                         const int32_t* slot_mapping, int64_t num_tokens, int num_q_heads,
+                                         int num_kv_heads, int head_dim, float k_scale, float v_scale,
+                                         hipStream_t stream) {
+  if (head_dim != 128 || num_q_heads <= 0 || num_kv_heads <= 0 || num_tokens < 0 || block_size <= 0)
+    return (int)hipErrorInvalidValue;
+  if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || !__builtin_isfinite(k_scale) || !__builtin_isfinite(v_scale))
+    return (int)hipErrorInvalidValue;
+  if (num_tokens == 0) return 0;
+  CacheDst cd;
+  cd.kc = (bf16_t*)k_cache; cd.vc = (bf16_t*)v_cache;
+  cd.ps = cache_page_stride; cd.ts = cache_tok_stride; cd.hs = cache_head_stride; cd.block_size = block_size;
+  cd.slots = slot_mapping; cd.v = (const bf16_t*)v; cd.vs_tok = v_stride_tok; cd.vs_head = v_stride_head;
+  cd.k_inv = 1.0f / k_scale; cd.v_inv = 1.0f / v_scale;
+  return launch_rope_t<true, true, true>(q, q_stride_tok, q_stride_head, k, k_stride_tok, k_stride_head, q_weight,
+                                         k_weight, eps, positions, cos_sin_cache, q_out, nullptr, num_tokens,
+                                         num_q_heads, num_kv_heads, cd, stream);
 }
 
 extern "C" int xv_rotary_embedding(const void* q, int64_t q_stride_tok, int64_t q_stride_head,

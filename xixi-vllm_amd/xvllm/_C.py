@@ -58,6 +58,13 @@ SIGNATURES: dict[str, tuple] = {
         i32, [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp, f32, vp, vp, vp, vp, vp, i64, i64, i64, i32, vp,
               i64, i32, i32, i32, vp]
     ),
+    "xv_qk_norm_rope_store_fp8": (
+        i32, [vp, i64, i64, vp, i64, i64, vp, i64, i64, vp, vp, f32, vp, vp, vp, vp, vp, i64, i64, i64, i32, vp,
+              i64, i32, i32, i32, f32, f32, vp]
+    ),
+    "xv_gather_kv_fp8": (
+        i32, [vp, vp, i64, i64, i64, vp, i64, i32, vp, i32, i32, i32, i32, f32, f32, vp, vp, i64, vp]
+    ),
     "xv_silu_and_mul": (i32, [vp, i64, vp, i64, i64, i32, vp]),
     "xv_stream_copy": (i32, [vp, vp, i64, i32, vp]),
     "xv_sampler_workspace_size": (sz, [i32, i32]),

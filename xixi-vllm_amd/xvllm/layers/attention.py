@@ -48,6 +48,10 @@ class AttnInputs(NamedTuple):
 @dataclass
 class AttnMetadata:
     kv_cache: torch.Tensor  # [2, L, NB, BS, Hkv, D]
+    # fp8 (e4m3fn) pools only: the dequantisation scales of K and V (this
+    # build's optional pool format; the reference's pool holds the model dtype)
+    k_scale: float = 1.0
+    v_scale: float = 1.0
 
 
 # Active metadata, innermost context last (the reference keeps one module
@@ -64,6 +68,14 @@ def attention_context(meta: AttnMetadata):
         yield meta
     finally:
         _META_STACK.pop()
+
+
+def kv_scales() -> tuple[float, float]:
+    """(k_scale, v_scale) of the active pool (1, 1 for a bf16 pool)."""
+    if not _META_STACK:
+        raise RuntimeError("vllm::attention needs an active attention_context(AttnMetadata(kv_cache=...))")
+    m = _META_STACK[-1]
+    return m.k_scale, m.v_scale
 
 
 def _layer_caches(layer_id: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -236,10 +248,14 @@ def prefill_attention(
     v_cache: torch.Tensor | None = None,
     block_tables: torch.Tensor | None = None,
     softmax_scale: float | None = None,
+    max_seqlen_k: int = 0,
+    kv_scale: tuple[float, float] | None = None,
 ) -> torch.Tensor:
     """Varlen causal attention, bottom-right aligned.  With block_tables the
     keys come from the paged cache (cached prefix + this chunk), otherwise
-    from k/v rows cu_seqlens_k[b] .. cu_seqlens_k[b+1]."""
+    from k/v rows cu_seqlens_k[b] .. cu_seqlens_k[b+1].  An fp8 paged cache
+    needs max_seqlen_k and its (k_scale, v_scale) (default: the active
+    attention_context's)."""
     q3, qs0, qs1 = _q_view(q, num_qo_heads, head_dim)
     require_cuda(q3, cu_seqlens_q, cu_seqlens_k)
     require_bf16(q3)
@@ -248,6 +264,28 @@ def prefill_attention(
     cuk = cu_seqlens_k.to(torch.int32).contiguous()
     out = torch.empty((q3.shape[0], num_qo_heads * head_dim), dtype=q.dtype, device=q.device)
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
+    if block_tables is not None and k_cache is not None and k_cache.dtype == torch.float8_e4m3fn:
+        # fp8 pages: the sequences' keys dequantized into varlen bf16 rows, then the dense path
+        k_scale, v_scale = kv_scales() if kv_scale is None else kv_scale
+        if max_seqlen_k <= 0:
+            raise ValueError("prefill over an fp8 paged cache needs max_seqlen_k (the longest key run)")
+        hkv = k_cache.shape[2]
+        bt = block_tables.to(torch.int32)
+        if bt.stride(-1) != 1:
+            bt = bt.contiguous()
+        rows = bsz * int(max_seqlen_k)
+        kd = torch.empty((max(rows, 1), hkv, head_dim), dtype=torch.bfloat16, device=q.device)
+        vd = torch.empty_like(kd)
+        _C.check(
+            _C.lib().xv_gather_kv_fp8(
+                ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2), ptr(bt),
+                bt.stride(0), k_cache.shape[1], ptr(cuk), bsz, int(max_seqlen_k), hkv, head_dim, float(k_scale),
+                float(v_scale), ptr(kd), ptr(vd), kd.stride(0), stream_of(q),
+            ),
+            "xv_gather_kv_fp8",
+        )
+        return prefill_attention(q, kd, vd, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, num_qo_heads, num_kv_heads,
+                                 head_dim, softmax_scale=softmax_scale)
     if block_tables is not None:
         assert k_cache is not None and v_cache is not None
         require_bf16(k_cache, v_cache)
@@ -304,19 +342,22 @@ def attention(
     k_cache, v_cache = _layer_caches(layer_id)
     k3 = k.view(-1, num_kv_heads, head_dim)
     v3 = v.view(-1, num_kv_heads, head_dim)
+    ks, vs = kv_scales()
     if slot_mapping is not None:  # None: this step's K/V are already in the cache (fused store)
-        store_kvcache(k3, v3, k_cache, v_cache, slot_mapping)  # paged view, written in place
+        store_kvcache(k3, v3, k_cache, v_cache, slot_mapping, k_scale=ks, v_scale=vs)  # paged view, in place
     if is_prefill:
         if block_tables is not None:
             return prefill_attention(
                 q, None, None, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, num_qo_heads, num_kv_heads,
-                head_dim, k_cache=k_cache, v_cache=v_cache, block_tables=block_tables,
+                head_dim, k_cache=k_cache, v_cache=v_cache, block_tables=block_tables, max_seqlen_k=max_seqlen_k,
+                kv_scale=(ks, vs),
             )
         return prefill_attention(
             q, k3, v3, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, num_qo_heads, num_kv_heads, head_dim
         )
     return paged_decode_attention(
-        q, k_cache, v_cache, block_tables, cache_seqlens, num_qo_heads, num_kv_heads, head_dim
+        q, k_cache, v_cache, block_tables, cache_seqlens, num_qo_heads, num_kv_heads, head_dim,
+        k_scale=ks, v_scale=vs,
     )
 
 

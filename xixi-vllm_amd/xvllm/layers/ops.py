@@ -221,12 +221,18 @@ def qk_norm_rope_store(
     k_cache: torch.Tensor,
     v_cache: torch.Tensor,
     slot_mapping: torch.Tensor,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """Decode-step fusion: q/k head RMSNorm + RoPE; q returned [T, Hq, D], k (roped)
     and v written into the paged caches at slot_mapping (reference
-    qwen3.py:117-128 followed by kv_ops.store_kvcache)."""
+    qwen3.py:117-128 followed by kv_ops.store_kvcache).  fp8 caches
+    (torch.float8_e4m3fn) store e4m3fn(x / scale), as store_kvcache does."""
     require_cuda(q, k, v, k_cache, v_cache, slot_mapping)
-    require_bf16(q, k, v, k_cache, v_cache)
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    require_bf16(q, k, v, *(() if fp8 else (k_cache, v_cache)))
+    if fp8 and v_cache.dtype != torch.float8_e4m3fn:
+        raise TypeError("k_cache and v_cache must share one dtype")
     q3, qs0, qs1 = _head_view(q)
     k3, ks0, ks1 = _head_view(k)
     v3, vs0, vs1 = _head_view(v)
@@ -236,6 +242,17 @@ def qk_norm_rope_store(
     slots = slot_mapping.to(torch.int32).contiguous()
     pos = positions.to(torch.int64).contiguous()
     qo = torch.empty((n, hq, d), dtype=q.dtype, device=q.device)
+    if fp8:
+        _C.check(
+            _C.lib().xv_qk_norm_rope_store_fp8(
+                ptr(q3), qs0, qs1, ptr(k3), ks0, ks1, ptr(v3), vs0, vs1, ptr(q_weight.contiguous()),
+                ptr(k_weight.contiguous()), float(eps), ptr(pos), ptr(cos_sin_cache.contiguous()), ptr(qo),
+                ptr(k_cache), ptr(v_cache), ps, ts, hs, bs, ptr(slots), n, hq, k3.shape[1], d, float(k_scale),
+                float(v_scale), stream_of(q),
+            ),
+            "xv_qk_norm_rope_store_fp8",
+        )
+        return qo
     _C.check(
         _C.lib().xv_qk_norm_rope_store(
             ptr(q3), qs0, qs1, ptr(k3), ks0, ks1, ptr(v3), vs0, vs1, ptr(q_weight.contiguous()),
@@ -249,5 +266,5 @@ def qk_norm_rope_store(
 
 @qk_norm_rope_store.register_fake
 def _qk_norm_rope_store_fake(q, k, v, q_weight, k_weight, eps, positions, cos_sin_cache, k_cache, v_cache,
-                             slot_mapping):
+                             slot_mapping, k_scale=1.0, v_scale=1.0):
     return torch.empty(q.shape, dtype=q.dtype, device=q.device)

@@ -64,7 +64,10 @@ class ModelRunner:
         self.block_size = kv.block_size
         cfg = model.config
         self.hidden_size = cfg.hidden_size
-        self._meta = AttnMetadata(kv_cache=kv.kv_cache)
+        self._meta = AttnMetadata(kv_cache=kv.kv_cache, k_scale=getattr(kv, "k_scale", 1.0),
+                                  v_scale=getattr(kv, "v_scale", 1.0))
+        if kv.dtype == torch.float8_e4m3fn and cascade_groups:
+            raise ValueError("cascade decode reads bf16 pages only; use cascade_groups=0 with an fp8 pool")
         n_model_layers = len(model.model.layers)
         if kv.num_layers < n_model_layers:  # layer aliasing: layer i reads pool layer i % pool layers
             for i, layer in enumerate(model.model.layers):
@@ -77,7 +80,8 @@ class ModelRunner:
                            cascade_max_prefix_blocks=cascade_max_prefix_blocks, cascade_min_blocks=cascade_min_blocks,
                            cascade_max_rows=max(1, 128 // (cfg.num_attention_heads // cfg.num_key_value_heads)))
         self.vocab_size = cfg.vocab_size
-        self._decode_out = torch.zeros(self.max_bs, self.hidden_size, dtype=kv.dtype, device=self.device)
+        act_dtype = torch.bfloat16 if kv.dtype == torch.float8_e4m3fn else kv.dtype  # activations stay bf16
+        self._decode_out = torch.zeros(self.max_bs, self.hidden_size, dtype=act_dtype, device=self.device)
         self._decode_ids = torch.zeros(self.max_bs, dtype=torch.int64, device=self.device)
         self._uniforms = torch.zeros(self.max_bs, dtype=torch.float32, device=self.device)
         self._copy_stream = torch.cuda.Stream(device=self.device)

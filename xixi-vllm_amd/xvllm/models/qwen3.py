@@ -17,7 +17,7 @@ from torch import nn
 from ..config import head_dim as _head_dim
 from ..config import rope_theta as _rope_theta
 from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
-from ..layers.attention import kv_cache_of
+from ..layers.attention import kv_cache_of, kv_scales
 from ..layers.linear import linear_into_norm
 from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
@@ -77,9 +77,10 @@ class Qwen3Attention(nn.Module):
     def _split_norm_rope_store(self, positions, qkv, slot_mapping):
         q, k, v = self._views(qkv)
         k_cache, v_cache = kv_cache_of(self.attn.layer_id)
+        ks, vs = kv_scales()
         q = torch.ops.xv.qk_norm_rope_store(
             q, k, v, self.q_norm.weight, self.k_norm.weight, self.eps, positions, self.rotary_emb.cos_sin_cache,
-            k_cache, v_cache, slot_mapping,
+            k_cache, v_cache, slot_mapping, ks, vs,
         )
         return q, k, v
 
