@@ -151,3 +151,23 @@ def test_fp8_entry_points_reject_bad_arguments(lib):
                dict(d=12)):
         assert store(**kw) == INVALID, kw
     assert store(n=0) == 0
+
+
+def test_fp8_model_entry_points_reject_bad_arguments(lib):
+    def rope(**kw):
+        a = dict(D=128, ks=1.0, vs=1.0, T=4)
+        a.update(kw)
+        return lib.xv_qk_norm_rope_store_fp8(A, 6144, 128, A, 6144, 128, A, 6144, 128, A, A, 1e-6, A, A, A, A, A,
+                                             16384, 1024, 128, 16, A, a["T"], 32, 8, a["D"], a["ks"], a["vs"], None)
+    for kw in (dict(D=64), dict(ks=0.0), dict(vs=float("inf"))):
+        assert rope(**kw) == INVALID, kw
+    assert rope(T=0) == 0
+
+    def gather(**kw):
+        a = dict(kc=A, ts=1024, out=A, ost=1024, B=4, D=128, ks=1.0)
+        a.update(kw)
+        return lib.xv_gather_kv_fp8(a["kc"], A, 16384, a["ts"], 128, A, 64, 16, A, a["B"], 512, 8, a["D"], a["ks"],
+                                    1.0, a["out"], A, a["ost"], None)
+    for kw in (dict(kc=A + 4), dict(ts=1028), dict(out=U), dict(ost=512), dict(D=64), dict(ks=-1.0)):
+        assert gather(**kw) == INVALID, kw
+    assert gather(B=0) == 0
