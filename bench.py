@@ -420,7 +420,8 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
             "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}, model
 
 
-def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bool = True, model=None):
+def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bool = True, model=None,
+                   fp8: bool = False):
     """Config 5: Qwen3-32B-shaped decode (64 layers, hidden 5120, 64 q / 8 kv
     heads, FFN 25600, random bf16 weights ~N(0,0.02)), batch 32 at context
     32768; 16 requests share an 8192-token prefix, 16 are independent; top-p
@@ -434,7 +435,8 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
     layer i reads pool layer i % pool_layers: every layer streams the same
     bytes in the same pattern as with a full pool (what this leaves out: the
-    real memory footprint and the TLB reach of 243 GB)."""
+    real memory footprint and the TLB reach of 243 GB).  fp8: the pool in the
+    optional fp8 (e4m3fn) page format (plain decode: cascade reads bf16 only)."""
     from xvllm.batch import SeqSchedule
     from xvllm.config import QWEN3_32B
     from xvllm.kv_pool import KVPool
@@ -466,11 +468,22 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
         with torch.device(dev):
             if model is None:
                 model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
-            kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
-                        num_layers=pool_layers)
+            if fp8:
+                kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.float8_e4m3fn,
+                            num_layers=pool_layers, k_scale=FP8_SCALE, v_scale=FP8_SCALE)
+            else:
+                kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
+                            num_layers=pool_layers)
     finally:
         torch.set_default_dtype(torch.float32)
-    kv.kv_cache.normal_()
+    if fp8:
+        assert not cascade, "cascade decode reads bf16 pages only"
+        for i in range(2):
+            for layer in range(kv.num_layers):
+                view = kv.kv_cache[i, layer]
+                view.copy_((torch.randn(view.shape, device=dev) / FP8_SCALE).to(torch.float8_e4m3fn))
+    else:
+        kv.kv_cache.normal_()
     casc = dict(cascade_groups=2, cascade_max_prefix_blocks=ppg, cascade_min_blocks=64) if cascade else {}
     runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx, device=dev, **casc)
     runner.generator = torch.Generator(device=dev).manual_seed(5)
@@ -495,7 +508,7 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
-    per_tok_layer = cfg.num_key_value_heads * 128 * 2 * 2
+    per_tok_layer = cfg.num_key_value_heads * 128 * 2 * (1 if fp8 else 2)
     kv_seq = bsz * ctx * cfg.num_hidden_layers * per_tok_layer
     kv_unique = unique * PAGE * cfg.num_hidden_layers * per_tok_layer
     kv_read = kv_unique if cascade else kv_seq  # per-step KV bytes the decode streams
@@ -507,6 +520,7 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     return {"model": "Qwen3-32B-shaped (64 layers, 64q/8kv, FFN 25600)", "batch": bsz, "context": ctx,
             "shared_prefix": f"{shared} requests x {prefix} tokens (radix prefix cache)",
             "attention": "cascade (shared blocks read once per kv head)" if cascade else "plain paged decode",
+            "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
             "sampling": "top-p 0.95 (T 1.0)", "kv_pool_layers": pool_layers, "ms_per_step": round(ms, 3),
             "tok_per_s": round(bsz / (ms * 1e-3), 1), "weight_bytes": wbytes, "kv_bytes_per_seq": kv_seq,
             "kv_bytes_unique_pages": kv_unique, "kv_bytes_read_per_step": kv_read,
@@ -742,7 +756,8 @@ def main() -> int:
     if args.config5_only:
         c5, model = decode_config5(torch, dev, cascade=False)
         c5c, model = decode_config5(torch, dev, cascade=True, model=model)
-        print(json.dumps({"config5": c5, "config5_cascade": c5c}))
+        c58, model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
+        print(json.dumps({"config5": c5, "config5_cascade": c5c, "config5_fp8": c58}))
         return 0
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)
@@ -846,6 +861,7 @@ def main() -> int:
         torch.cuda.empty_cache()
         line["config5"], model = decode_config5(torch, dev, cascade=False)
         line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
+        line["config5_fp8"], model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
         del model
         torch.cuda.empty_cache()
     if not args.no_serve:
