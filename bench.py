@@ -34,8 +34,10 @@ sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
-# 2 x 319336.1 KiB read (FETCH_SIZE counts half on this part) + 3226.4 KiB written.
-MEASURED_TRAFFIC_BYTES = int((2 * 319336.1 + 3226.4) * 1024)
+# 2 x 319430.4 KiB read (FETCH_SIZE counts half on this part) + 3225.5 KiB written;
+# on fp8 pages 2 x 160864.7 + 5336.4 KiB.
+MEASURED_TRAFFIC_BYTES = int((2 * 319430.4 + 3225.5) * 1024)
+MEASURED_TRAFFIC_BYTES_FP8 = int((2 * 160864.7 + 5336.4) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
@@ -723,6 +725,8 @@ def main() -> int:
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-split-k", action="store_true", help="plain o_proj / down_proj GEMMs in the model runs")
+    ap.add_argument("--kv-dtype", choices=("bf16", "fp8"), default="bf16",
+                    help="KV page format of the headline calls (fp8: the pool's optional e4m3fn pages, for profiling)")
     ap.add_argument("--layout", choices=("hnd", "nhd"), default="hnd",
                     help="KV page memory order of the headline (hnd: KVPool's default; nhd: the reference's)")
     args = ap.parse_args()
@@ -771,9 +775,10 @@ def main() -> int:
     if args.suite_only:
         print(json.dumps(kernel_suite(torch, dev)))
         return 0
-    cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=args.layout)
+    fp8 = args.kv_dtype == "fp8"
+    cases = make_case(torch, ctx, layers=4, dev=dev, seed=args.seed + 1, layout=args.layout, fp8=fp8)
     ms, wall, eager_ms = time_decode(torch, cases, args.steps, args.warmup)
-    nbytes = algo_bytes(ctx)
+    nbytes = algo_bytes(ctx, kv_elem=1 if fp8 else 2)
     gbs = nbytes / (ms * 1e-3) / 1e9
 
     sweep = {}
@@ -825,6 +830,7 @@ def main() -> int:
             "batch": 64,
             "total_ctx_tokens": sum(ctx),
             "kv_pools_cycled": 4,
+            "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
             "kv_page_layout": args.layout + (" (KVPool default: [page][kv head][token][d] in memory, the reference's"
                                              " logical [page][token][kv head][d] view)" if args.layout == "hnd"
                                              else " (the reference's memory order)"),
@@ -835,9 +841,9 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": MEASURED_TRAFFIC_BYTES,
+            "traffic": MEASURED_TRAFFIC_BYTES_FP8 if fp8 else MEASURED_TRAFFIC_BYTES,
             "algorithmic_bytes_per_call": nbytes,
-            "kernel": "paged_decode_kernel<4> + merge_parts_kernel (one call)",
+            "kernel": f"paged_decode_kernel<4, {'true' if fp8 else 'false'}> + merge_parts_kernel (one call)",
         },
         "sweep": sweep,
         "wall_s_timed_region": round(wall, 4),
