@@ -1295,6 +1295,16 @@ struct RowConsts {
   uint32_t kmax, kmin;
   float inv_t, zmax, bs;
 };
+// From lane values already loaded (segment `lane` of the row, or 0 / ~0).
+XV_INLINE RowConsts row_consts_of(uint32_t kmax_lane, uint32_t kmin_lane, float temp) {
+  RowConsts c;
+  c.kmax = wave_max_u(kmax_lane);
+  c.kmin = wave_min_u(kmin_lane);
+  c.inv_t = 1.0f / temp;
+  c.zmax = bf16_to_f32(key_to_bits(c.kmax)) * c.inv_t;
+  c.bs = c.kmax ? bucket_scale(log2_ratio(key_to_bits(c.kmin), c.inv_t, c.zmax)) : 16.0f;
+  return c;
+}
 XV_INLINE RowConsts row_consts(const SegArgs& a, int b, float temp) {
   // every wave reduces the R <= 64 segment values itself: one load per lane
   RowConsts c;
@@ -1411,11 +1421,27 @@ __global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(SegArgs a) {
 __global__ __launch_bounds__(kSegThreads) void row_plan_kernel(SegArgs a) {
   static_assert(kSegThreads == kBuckets, "one thread per bucket");
   __shared__ SegRed red;
-  const int b = blockIdx.x, t = threadIdx.x;
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
   RowPlan& plan = a.plans[b];
+  // Every load the plan can need goes out before any is used: one memory
+  // round trip instead of one per dependent step.  Segment indices past R
+  // reload segment R-1 (no branch between the loads) and are masked below;
+  // entries a row's path did not write this call are loaded and ignored.
+  uint32_t c_all[kMaxSegs];
+  unsigned long long m_all[kMaxSegs];
+#pragma unroll
+  for (int j = 0; j < kMaxSegs; ++j) {
+    const int64_t o = ((int64_t)b * a.R + min(j, a.R - 1)) * kBuckets + t;
+    c_all[j] = a.seg_cnt[o];
+    m_all[j] = a.seg_mass[o];
+  }
+  const int sl = min(lane, a.R - 1);
+  const uint32_t kmax_l = a.seg_kmax[b * a.R + sl], kmin_l = a.seg_kmin[b * a.R + sl];
+  const uint32_t minp_l = a.seg_minp[b * a.R + sl];
+  const unsigned long long best_l = a.seg_best[b * a.R + min(t, a.R - 1)];
   const RowParams p = row_params(a, b);
   if (p.greedy) {
-    unsigned long long best = t < a.R ? a.seg_best[b * a.R + t] : 0ull;
+    unsigned long long best = t < a.R ? best_l : 0ull;
     best = seg_max_ull(red, best);
     if (t == 0) {
       a.out_ids[b] = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
@@ -1423,7 +1449,7 @@ __global__ __launch_bounds__(kSegThreads) void row_plan_kernel(SegArgs a) {
     }
     return;
   }
-  const RowConsts rc = row_consts(a, b, p.temp);
+  const RowConsts rc = row_consts_of(lane < a.R ? kmax_l : 0u, lane < a.R ? kmin_l : 0xffffffffu, p.temp);
   if (rc.kmax == 0) {  // every logit NaN: nothing has mass
     if (t == 0) {
       a.out_ids[b] = 0;
@@ -1432,23 +1458,13 @@ __global__ __launch_bounds__(kSegThreads) void row_plan_kernel(SegArgs a) {
     return;
   }
   int64_t cnt = 0, mass = 0;
-  for (int i0 = 0; i0 < a.R; i0 += 8) {  // eight segments' loads in flight
-    uint32_t c8[8];
-    unsigned long long m8[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t o = ((int64_t)b * a.R + min(i0 + j, a.R - 1)) * kBuckets + t;
-      c8[j] = a.seg_cnt[o];
-      m8[j] = p.use_k ? 0ull : a.seg_mass[o];
+  for (int j = 0; j < kMaxSegs; ++j)
+    if (j < a.R) {
+      cnt += c_all[j];
+      mass += p.use_k ? 0 : (int64_t)m_all[j];
     }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (i0 + j < a.R) {
-        cnt += c8[j];
-        mass += (int64_t)m8[j];
-      }
-  }
-  const uint32_t kminp = wave_min_u((t & 63) < a.R ? a.seg_minp[b * a.R + (t & 63)] : 0xffffffffu);
+  const uint32_t kminp = wave_min_u(lane < a.R ? minp_l : 0xffffffffu);
   const int64_t cnt_incl = seg_incl_scan(red, cnt);
   const int64_t mass_incl = seg_incl_scan(red, mass);
   const int64_t total = seg_sum_l(red, mass);
@@ -1544,7 +1560,7 @@ __global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
   __shared__ SegRed red;
   __shared__ uint32_t base_lds;
   const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x;
-  const RowPlan& plan = a.plans[b];
+  const RowPlan plan = a.plans[b];  // read fields in one round trip (the count is reserved through a.plans)
   if (plan.status != kPlanGather) return;
   const uint32_t klo = plan.klo, khi = plan.khi;
   const bf16_t* row = a.logits + (int64_t)b * a.stride;
@@ -1991,7 +2007,7 @@ XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t 
 __global__ __launch_bounds__(kSegThreads) void seg_kept_kernel(SegArgs a) {
   __shared__ SegRed red;
   const int b = blockIdx.y, r = blockIdx.x;
-  const RowPlan& plan = a.plans[b];
+  const RowPlan plan = a.plans[b];  // every field in one round trip
   if (plan.status != kPlanDraw) return;
   const uint32_t key_cut = plan.key_cut;
   const int64_t id_cut = plan.id_cut;
@@ -2010,15 +2026,17 @@ __global__ __launch_bounds__(kSegThreads) void row_draw_kernel(SegArgs a) {
   __shared__ SegRed red;
   __shared__ int64_t pick;
   const int b = blockIdx.x, t = threadIdx.x;
-  const RowPlan& plan = a.plans[b];
+  // the segment masses and the draw load beside the plan (one round trip)
+  const int64_t sm_l = a.seg_kept[b * a.R + min(t, a.R - 1)];
+  const float u = a.uniforms ? a.uniforms[b] : 0.5f;
+  const RowPlan plan = a.plans[b];  // every field in one round trip
   if (plan.status != kPlanDraw) return;
   const uint32_t key_cut = plan.key_cut;
   const int64_t id_cut = plan.id_cut;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
-  const float u = a.uniforms ? a.uniforms[b] : 0.5f;
   const int64_t rdraw = draw_point(u, plan.M);
   // the segment holding rdraw: inclusive sums of the segment masses
-  const int64_t sm = t < a.R ? a.seg_kept[b * a.R + t] : 0;
+  const int64_t sm = t < a.R ? sm_l : 0;
   const int64_t incl = seg_incl_scan(red, sm);
   const int r = (int)seg_min_l(red, (t < a.R && rdraw < incl) ? t : kMaxSegs);
   if (r >= a.R) {  // no kept mass (cannot happen for a row with a finite logit)
