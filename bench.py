@@ -438,7 +438,7 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     layer i reads pool layer i % pool_layers: every layer streams the same
     bytes in the same pattern as with a full pool (what this leaves out: the
     real memory footprint and the TLB reach of 243 GB).  fp8: the pool in the
-    optional fp8 (e4m3fn) page format (plain decode: cascade reads bf16 only)."""
+    optional fp8 (e4m3fn) page format, plain or cascade decode."""
     from xvllm.batch import SeqSchedule
     from xvllm.config import QWEN3_32B
     from xvllm.kv_pool import KVPool
@@ -479,7 +479,6 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     finally:
         torch.set_default_dtype(torch.float32)
     if fp8:
-        assert not cascade, "cascade decode reads bf16 pages only"
         for i in range(2):
             for layer in range(kv.num_layers):
                 view = kv.kv_cache[i, layer]
@@ -761,7 +760,8 @@ def main() -> int:
         c5, model = decode_config5(torch, dev, cascade=False)
         c5c, model = decode_config5(torch, dev, cascade=True, model=model)
         c58, model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
-        print(json.dumps({"config5": c5, "config5_cascade": c5c, "config5_fp8": c58}))
+        c58c, model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
+        print(json.dumps({"config5": c5, "config5_cascade": c5c, "config5_fp8": c58, "config5_cascade_fp8": c58c}))
         return 0
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)
@@ -868,6 +868,7 @@ def main() -> int:
         line["config5"], model = decode_config5(torch, dev, cascade=False)
         line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
         line["config5_fp8"], model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
+        line["config5_cascade_fp8"], model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
         del model
         torch.cuda.empty_cache()
     if not args.no_serve:

@@ -187,6 +187,25 @@ int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_s
                                 hipStream_t stream);
 
 /*
+ * xv_cascade_decode_attention over an fp8 (OCP e4m3fn) cache written by
+ * xv_store_kvcache_fp8, scales as xv_paged_decode_attention_fp8 (k_scale
+ * folded into the softmax scale, v_scale applied to the output).  No
+ * counterpart in the reference (its pool holds bf16 pages only).
+ */
+int xv_cascade_decode_attention_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                    const void* k_cache, const void* v_cache,
+                                    int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                    const int32_t* block_tables, int64_t bt_stride,
+                                    const int32_t* cache_seqlens, const int32_t* prefix_tokens,
+                                    const int32_t* group_info, const int32_t* group_rows,
+                                    int num_groups, int max_prefix_blocks,
+                                    void* out, int64_t out_stride_tok,
+                                    void* workspace, size_t workspace_bytes,
+                                    int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int max_blocks_per_seq, float scale,
+                                    float k_scale, float v_scale, hipStream_t stream);
+
+/*
  * xv_paged_decode_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture that must not
  * call hipMalloc, tight serving loops, harnesses that forbid allocation).  It

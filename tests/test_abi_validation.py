@@ -142,6 +142,17 @@ def test_fp8_entry_points_reject_bad_arguments(lib):
         assert dec(**kw) == INVALID, kw
     assert dec(B=0) == 0
 
+    def casc(**kw):
+        a = dict(kc=A, ps=16384, ts=1024, hs=128, B=64, ks=1.0, vs=1.0, pre=A)
+        a.update(kw)
+        return lib.xv_cascade_decode_attention_fp8(A, 4096, 128, a["kc"], A, a["ps"], a["ts"], a["hs"], A, 256, A,
+                                                   a["pre"], A, A, 2, 16, A, 4096, A, 1 << 30, a["B"], 32, 8, 128, 16,
+                                                   256, 0.088, a["ks"], a["vs"], None)
+    for kw in (dict(ts=1032), dict(hs=136), dict(kc=U), dict(ks=0.0), dict(vs=float("nan")), dict(pre=0),
+               dict(B=257)):
+        assert casc(**kw) == INVALID, kw
+    assert casc(B=0) == 0
+
     def store(**kw):
         a = dict(k=A, kc=A, ps=16384, ts=1024, hs=128, n=8, hkv=8, d=128, ks=1.0, vs=1.0)
         a.update(kw)

@@ -91,6 +91,48 @@ def test_cascade_decode_matches_oracle_and_plain_decode(dev, hq, hkv, block, ctx
     assert (f32(out)[np.asarray(ctx) == 0] == 0).all()
 
 
+CASES = [
+    (32, 8, 16, [500, 700, 320, 321, 1000, 150, 130, 200, 77, 1, 0, 640], [([0, 1, 2, 3, 4], 20), ([5, 6, 7], 7)]),
+    (64, 8, 256, [600, 1024, 513, 700, 2000, 300], [([0, 1, 2, 3], 2), ([4, 5], 1)]),
+    (16, 8, 48, [100 + 7 * i for i in range(40)], [(list(range(40)), 2)]),
+    (8, 8, 32, [96, 200, 64, 65], [([0, 1, 2, 3], 2)]),
+]
+
+
+@pytest.mark.parametrize("layout", ["nhd", "hnd"])
+@pytest.mark.parametrize("hq,hkv,block,ctx,shares", CASES)
+def test_cascade_decode_fp8_matches_oracle_and_plain_decode(dev, hq, hkv, block, ctx, shares, layout):
+    """fp8 (e4m3fn) pages: the cascade against the oracle over the
+    dequantized pages and against the plain fp8 decode, both page orders."""
+    from xvllm.layers.attention import cascade_decode_attention, paged_decode_attention
+
+    print(f"cascade fp8 {layout} hq {hq} hkv {hkv} block {block} B {len(ctx)}", flush=True)
+    g = gen(7 * hq + block + len(ctx))
+    d, ks, vs = 128, 0.05, 0.3
+    bt, pool = _shared_case(g, ctx, shares, block)
+    kc, vc = randn_bf16((pool, block, hkv, d), g), randn_bf16((pool, block, hkv, d), g)
+    kq = O.quantize_fp8(f32(kc), np.float32(1.0) / np.float32(ks))
+    vq = O.quantize_fp8(f32(vc), np.float32(1.0) / np.float32(vs))
+
+    def on_dev(codes):
+        t = torch.from_numpy(np.ascontiguousarray(codes)).view(torch.float8_e4m3fn).to(dev)
+        return t.transpose(1, 2).contiguous().transpose(1, 2) if layout == "hnd" else t
+
+    q = randn_bf16((len(ctx), hq, d), g)
+    sl = torch.tensor(ctx, dtype=torch.int32)
+    plan, pre = _plan(bt, ctx, block, dev, max_rows=128 // (hq // hkv))
+    assert (pre > 0).sum() >= 2
+    args = (q.view(len(ctx), -1).to(dev), on_dev(kq), on_dev(vq), bt.to(dev), sl.to(dev))
+    out = cascade_decode_attention(*args, plan, hq, hkv, d, k_scale=ks, v_scale=vs)
+    plain = paged_decode_attention(*args, hq, hkv, d, k_scale=ks, v_scale=vs)
+    torch.cuda.synchronize()
+    want = O.paged_decode_attention(f32(q), O.dequantize_fp8(kq, ks), O.dequantize_fp8(vq, vs), bt.numpy(),
+                                    sl.numpy())
+    _close(f32(out).reshape(len(ctx), hq, d), want)
+    _close(f32(out), f32(plain), rtol=1e-2, atol=1e-2)
+    assert (f32(out)[np.asarray(ctx) == 0] == 0).all()
+
+
 def test_cascade_empty_groups_and_no_groups(dev):
     """A plan with only trailing empty groups (no row shares anything) and a
     plan whose one group is followed by empty ones: both equal the plain decode."""
@@ -142,12 +184,43 @@ def test_cascade_config5_full_size(dev):
         _close(f32(out[r : r + 1].cpu()).reshape(1, HQ, d), want)
 
 
-def test_cascade_decode_graphs_match_eager(dev):
+def test_cascade_config5_full_size_fp8(dev):
+    """Config 5's attention on fp8 pages (scales 0.125): cascade against the
+    plain fp8 decode on every row and the oracle over the dequantized pages on
+    rows from both halves."""
+    from test_gpu_config5 import BSZ, CTX, HKV, HQ, config5_block_tables
+    from xvllm.layers.attention import cascade_decode_attention, paged_decode_attention
+
+    bt, unique = config5_block_tables()
+    g = torch.Generator(device=dev).manual_seed(10)
+    d, sc = 128, 0.125
+    kc = (torch.randn((unique, 16, HKV, d), generator=g, device=dev) / sc).to(torch.float8_e4m3fn)
+    vc = (torch.randn((unique, 16, HKV, d), generator=g, device=dev) / sc).to(torch.float8_e4m3fn)
+    q = torch.randn((BSZ, HQ * d), generator=g, device=dev).to(torch.bfloat16)
+    sl = torch.full((BSZ,), CTX, dtype=torch.int32)
+    plan, pre = _plan(bt, [CTX] * BSZ, 16, dev, groups=2, max_prefix_blocks=512, min_blocks=16)
+    assert pre[:16].tolist() == [8192] * 16 and not pre[16:].any()
+    btd, sld = bt.to(dev), sl.to(dev)
+    out = cascade_decode_attention(q, kc, vc, btd, sld, plan, HQ, HKV, d, k_scale=sc, v_scale=sc)
+    plain = paged_decode_attention(q, kc, vc, btd, sld, HQ, HKV, d, k_scale=sc, v_scale=sc)
+    torch.cuda.synchronize()
+    _close(f32(out), f32(plain), rtol=1e-2, atol=1e-2)
+    for r in (0, 15, 16):
+        pages = btd[r].long()
+        kr = O.dequantize_fp8(kc[pages].cpu().view(torch.uint8).numpy(), sc)
+        vr = O.dequantize_fp8(vc[pages].cpu().view(torch.uint8).numpy(), sc)
+        want = O.paged_decode_attention(f32(q[r : r + 1].cpu()).reshape(1, HQ, d), kr, vr,
+                                        np.arange(CTX // 16, dtype=np.int32)[None, :], np.array([CTX]))
+        _close(f32(out[r : r + 1].cpu()).reshape(1, HQ, d), want)
+
+
+@pytest.mark.parametrize("kv_dtype", ["bf16", "fp8"])
+def test_cascade_decode_graphs_match_eager(dev, kv_dtype):
     """A 2-layer model whose decode batch shares prefixes (rows 0..5 the same
     12 blocks): the runner's decode graphs carry the cascade plan; replays
     equal eager runs and equal a runner without cascade within bf16
     tolerance (relative L2 after two layers); a batch with no sharing runs
-    through the same graphs."""
+    through the same graphs.  Also on an fp8 pool (scales 0.25)."""
     from xvllm.batch import SeqSchedule
     from xvllm.config import Qwen3Shape
     from xvllm.kv_pool import KVPool
@@ -159,10 +232,17 @@ def test_cascade_decode_graphs_match_eager(dev):
     try:
         with torch.device(dev):
             model = Qwen3ForCausalLM(cfg).random_init_(seed=4)
-            kv = KVPool(cfg, num_blocks=600, block_size=16, device=dev, dtype=torch.bfloat16)
+            if kv_dtype == "fp8":
+                kv = KVPool(cfg, num_blocks=600, block_size=16, device=dev, dtype=torch.float8_e4m3fn,
+                            k_scale=0.25, v_scale=0.25)
+            else:
+                kv = KVPool(cfg, num_blocks=600, block_size=16, device=dev, dtype=torch.bfloat16)
     finally:
         torch.set_default_dtype(torch.float32)
-    kv.kv_cache.normal_()
+    if kv_dtype == "fp8":
+        kv.kv_cache.copy_((torch.randn(kv.kv_cache.shape, device=dev) * 4).to(torch.float8_e4m3fn))
+    else:
+        kv.kv_cache.normal_()
     casc = ModelRunner(model, kv, max_num_seqs=16, context_len=1024, device=dev, cascade_groups=2,
                        cascade_max_prefix_blocks=32, cascade_min_blocks=4)
     plain = ModelRunner(model, kv, max_num_seqs=16, context_len=1024, device=dev)

@@ -796,14 +796,18 @@ def test_stream_copy(dev, nbytes, shape):
 
 def _expected_parts(ctx: int, hkv: int, max_blocks: int, slots: int = 1024) -> list[int]:
     """Partials per kv head of one sequence (B 1, 16-token blocks), from the
-    host's range rule: lmin = max(4, ceil(max_blocks / 128)) pages (129 partial
-    slots at B 1), ranges of L = max(lmin, ceil(total / waves)) pages over the
-    flattened (kv head, page) space, waves = min(slots, ceil(hkv * max_blocks / lmin))."""
+    range rule: the host bound lmin = max(4, ceil(max_blocks / 128)) pages
+    (129 partial slots at B 1) gives max_parts = ceil(max_blocks / lmin) + 1
+    slots and waves = min(slots, ceil(hkv * max_blocks / lmin)); the kernel
+    takes ranges of L = max(4, ceil(np / (max_parts - 1)), ceil(total /
+    waves)) pages over the flattened (kv head, page) space, np the sequence's
+    pages."""
     lmin = max(4, -(-max_blocks // 128))
+    max_parts = -(-max_blocks // lmin) + 1
     np_ = -(-ctx // 16)
     total = hkv * np_
     waves = min(slots, -(-(hkv * max_blocks) // lmin))
-    L = max(lmin, -(-total // waves))
+    L = max(4, -(-np_ // (max_parts - 1)), -(-total // waves))
     return [(h * np_ + np_ - 1) // L - (h * np_) // L + 1 for h in range(hkv)]
 
 
@@ -827,5 +831,29 @@ def test_paged_decode_merge_partial_count_boundaries(dev, ctx, nparts):
     ws = decode_workspace(dev, 0)
     recorded = ws[: hkv * 4].view(torch.int32).cpu().tolist()
     assert recorded == [nparts] * hkv
+    want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
+    _close(f32(out).reshape(1, hq, d), want)
+
+
+@pytest.mark.parametrize("ctx,width", [(512, 2048), (100, 4096), (4100, 8192)])
+def test_paged_decode_ranges_follow_actual_lengths(dev, ctx, width):
+    """A block table far wider than the sequence (a graph captured for long
+    contexts, a cascade suffix): the ranges follow the sequence's own pages,
+    not the table width, so short rows still spread over many waves.  The
+    recorded partial counts equal the rule's and the output the oracle's."""
+    from xvllm.layers.attention import decode_workspace, paged_decode_attention
+
+    hq, hkv, d = 32, 8, 128
+    want_parts = _expected_parts(ctx, hkv, width)
+    g = gen(ctx + width)
+    need = (ctx + 15) // 16
+    kc, vc, bt, sl = make_paged([ctx], need + 8, hkv, d, g)
+    wide = torch.full((1, width), -1, dtype=torch.int32)
+    wide[:, : bt.shape[1]] = bt
+    q = randn_bf16((1, hq, d), g)
+    out = paged_decode_attention(q.view(1, -1).to(dev), kc.to(dev), vc.to(dev), wide.to(dev), sl.to(dev), hq, hkv, d)
+    torch.cuda.synchronize()
+    ws = decode_workspace(dev, 0)
+    assert ws[: hkv * 4].view(torch.int32).cpu().tolist() == want_parts
     want = O.paged_decode_attention(f32(q), f32(kc), f32(vc), bt.numpy(), sl.numpy())
     _close(f32(out).reshape(1, hq, d), want)

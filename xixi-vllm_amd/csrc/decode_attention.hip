@@ -51,7 +51,7 @@ struct DecodeArgs {
   int* ws_nparts;  // partials per (sequence, kv head), written by the wave holding the segment's last page
   int batch, hq, hkv, group;
   int nsub;       // 16-token pages per cache block (block_size / 16)
-  int lmin;       // minimum pages per wave range
+  int lmin;       // minimum pages per wave range for any table of the launch's width (host bound)
   int max_parts;  // partial slots per (sequence, head) in the workspace
   int nwaves;     // workgroups of the main kernel (the range count)
   float scale_log2;
@@ -355,6 +355,25 @@ XV_INLINE void read_page_f8(PageRegs& pr, const char* buf, char* vimg, const Lan
   finish_page_f8(pr, w, vimg, lo, lane);
 }
 
+// One tensor (K or V) of an fp8 page image at `raw` (its 16 rows of 128
+// bytes) widened to the bf16 page layout at `dst` (row t at t * 256, chunk c
+// in slot c ^ swz(t), as the LDS-DMA of a bf16 page leaves it): lane l
+// converts token l / 4's values 32 (l % 4) .. +31.
+XV_INLINE void widen_unit_f8(const char* raw, char* dst, const LaneOffsets& lo, int lane) {
+  const u32x4_t w0 = *reinterpret_cast<const u32x4_t*>(raw + (lo.v8[0] - kF8Half));
+  const u32x4_t w1 = *reinterpret_cast<const u32x4_t*>(raw + (lo.v8[1] - kF8Half));
+  uint32_t o[2][8];
+  fp8x16_to_bf16(w0, o[0]);
+  fp8x16_to_bf16(w1, o[1]);
+  const int r = lane >> 2, q = lane & 3;
+  char* row = dst + r * 256;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t* v = &o[j >> 1][4 * (j & 1)];
+    *reinterpret_cast<uint4*>(row + (((4 * q + j) ^ swz(r)) << 4)) = make_uint4(v[0], v[1], v[2], v[3]);
+  }
+}
+
 // S^T = K Q^T, the online softmax update and O += P V for one page already
 // in registers.  Tokens at page_tok0 + t >= ctx are masked.
 template <int G>
@@ -626,10 +645,18 @@ constexpr int kMaxBatch = 256;  // sequences per launch (larger batches are laun
 #define XV_DECODE_WPE 1  // waves per SIMD the register budget is fitted to
 #endif
 
-// Pages per wave range: identical in both kernels.
-XV_INLINE int range_pages(const DecodeArgs& a, int64_t total) {
+// Pages per wave range, from the launch's actual page counts: a segment of
+// np pages touches at most ceil(np / L) + 1 ranges, so L >= ceil(max np /
+// (max_parts - 1)) keeps every segment's partials within its workspace slots
+// (the host's lmin is the same bound for the widest table the block-table
+// width allows; rows far shorter than the table, such as the suffixes of a
+// cascade decode, get ranges sized to what they hold).  At least
+// kMinRangePages pages keep the page pipeline busy.
+constexpr int kMinRangePages = 4;
+XV_INLINE int range_pages(const DecodeArgs& a, int64_t total, int max_np) {
   const int64_t per = (total + a.nwaves - 1) / a.nwaves;
-  return (int)max((int64_t)a.lmin, per);
+  const int need = (max_np + a.max_parts - 2) / (a.max_parts - 1);
+  return (int)max((int64_t)max(kMinRangePages, need), per);
 }
 
 // Timing hook for out-of-tree instrumentation builds; empty in the library.
@@ -651,11 +678,12 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   __shared__ __attribute__((aligned(16))) char idtab[2 * kIdWindow * 4];
   const int lane = threadIdx.x;
   // prefix sums of the page counts (every wave computes them)
-  int carry = 0;
+  int carry = 0, max_np = 0;
   for (int c = 0; c < a.batch; c += 64) {
     const int b = c + lane;
     const int ctx = b < a.batch ? max(a.seqlens[b], 0) : 0;
     const int np = (ctx + kPage - 1) / kPage;
+    max_np = max(max_np, np);
     int inc = np;
     // inclusive scan by DPP: within 16-lane rows, then across rows
     inc += __builtin_amdgcn_update_dpp(0, inc, 0x111, 0xf, 0xf, true);  // row_shr:1
@@ -672,8 +700,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   }
   if (lane == 0) pref[0] = 0;
   __syncthreads();  // single wave: orders the LDS writes before the reads
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) max_np = max(max_np, __shfl_xor(max_np, m));
   const int64_t total = (int64_t)a.hkv * carry;
-  const int L = range_pages(a, total);
+  const int L = range_pages(a, total, max_np);
   const int64_t f0 = (int64_t)blockIdx.x * L;
   const int n = (int)max((int64_t)0, min(f0 + L, total) - f0);  // pages of this wave's range
   if (n == 0) return;
@@ -949,7 +979,7 @@ static_assert(kMaxParts <= kMergeMaxParts, "the merge holds at most kMergeMaxPar
 int min_range_pages(int batch, int num_q_heads, int max_blocks_per_seq) {
   const size_t per_part = (size_t)max(batch, 1) * max(num_q_heads, 1) * (kD + 1) * sizeof(float);
   const int P = (int)max((size_t)3, min((size_t)kMaxParts, kPartBudget / per_part));
-  return max(4, (max_blocks_per_seq + P - 2) / (P - 1));
+  return max(kMinRangePages, (max_blocks_per_seq + P - 2) / (P - 1));
 }
 
 // ---------------------------------------------------------------------------
@@ -971,6 +1001,12 @@ constexpr int kCascRows = 128;
 constexpr int kCascWaves = kCascRows / 16;  // one 16-row tile per wave
 constexpr int kCascSub = 16;                // pages per sub-chunk (128 KB of LDS)
 constexpr int kCascUnits = 2 * kCascSub / kCascWaves;  // (page, K or V) units each wave moves per sub-chunk
+// fp8 pages: a sub-chunk's raw pages (4 KB each) and two bf16 images of a
+// quarter sub-chunk (4 pages in the bf16 page layout), which the workgroup's
+// waves fill together, one (page, K or V) unit each, and then all read.
+constexpr int kCascQuarter = kCascSub / 4;
+template <bool F8> constexpr int kCascLds = F8 ? kCascSub * (kPageLds / 2) + 2 * kCascQuarter * kPageLds
+                                               : kCascSub * kPageLds;
 
 struct CascadeArgs {
   const bf16_t* q; int64_t q_st, q_sh;
@@ -986,6 +1022,7 @@ struct CascadeArgs {
   bf16_t* pre_o; float* pre_lse;
   int32_t* sbt; int32_t* ssl;  // suffix view: [batch, max_blocks] block table, [batch] lengths
   float scale_log2;
+  float v_scale;  // fp8 pages: the V dequantisation scale, applied to the output (1 for bf16 pages)
 };
 
 XV_INLINE void cascade_suffix_view(const CascadeArgs& a, int v, int nview) {
@@ -998,9 +1035,15 @@ XV_INLINE void cascade_suffix_view(const CascadeArgs& a, int v, int nview) {
   }
 }
 
-template <int G>
+// LDS-DMA instructions of one (page, K or V) unit.
+template <bool F8> constexpr int kUnitOps = F8 ? 2 : 4;
+template <int N>
+XV_INLINE void wait_vm() { __asm__ __volatile__("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory"); }
+
+template <int G, bool F8 = false>
 __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(CascadeArgs a) {
-  __shared__ __attribute__((aligned(16))) char lds[kCascSub * kPageLds];
+  __shared__ __attribute__((aligned(16))) char lds[kCascLds<F8>];
+  constexpr int kUnitPage = F8 ? kPageLds / 2 : kPageLds;  // LDS bytes of one page (K then V)
   // the first num_view workgroups write the suffix view; then (chunk, group,
   // kv head), chunk fastest: the workgroups of empty groups (a graph records a
   // fixed group count) are interleaved with working ones instead of forming a
@@ -1027,7 +1070,7 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
   const int i = lane & 15, g = lane >> 4;
   const bool active = wave * 16 < R;  // this wave's tile holds rows
-  const uint32_t bytes = (uint32_t)(((int64_t)(kPage - 1) * a.tok_stride + kD) * 2);
+  const uint32_t bytes = (uint32_t)(((int64_t)(kPage - 1) * a.tok_stride + kD) * (F8 ? 1 : 2));
   // unit u = wave + kCascWaves * j of a sub-chunk: page u / 2, its K rows (u even) or V rows (u odd)
   auto issue_sub = [&](int s0, int n) {
     int page[kCascUnits];
@@ -1043,14 +1086,27 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
       const int p = s0 + k;
       const int64_t base = (int64_t)page[j] * a.page_stride + (int64_t)(p % a.nsub) * kPage * a.tok_stride +
                            (int64_t)kvh * a.head_stride;
-      const __amdgpu_buffer_rsrc_t r = page_rsrc(((u & 1) ? a.vc : a.kc) + base, bytes);
-      char* dst = lds + (u >> 1) * kPageLds + ((u & 1) ? kVPageBytes : 0);
+      const bf16_t* src = (u & 1) ? a.vc : a.kc;
+      if constexpr (F8) {  // element strides are byte strides
+        const __amdgpu_buffer_rsrc_t r =
+            page_rsrc(reinterpret_cast<const bf16_t*>(reinterpret_cast<const char*>(src) + base), bytes);
+        char* dst = lds + (u >> 1) * kUnitPage + ((u & 1) ? kF8Half : 0);
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g[s], 0, 0, kNontemporal);
+        for (int s = 0; s < 2; ++s)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g8[s], 0, 0,
+                                                   kNontemporal);
+      } else {
+        const __amdgpu_buffer_rsrc_t r = page_rsrc(src + base, bytes);
+        char* dst = lds + (u >> 1) * kUnitPage + ((u & 1) ? kVPageBytes : 0);
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g[s], 0, 0,
+                                                   kNontemporal);
+      }
     }
   };
   // Q^T B operand of the wave's tile: column i = row 16 w + i, k = d-chunk 4s + g
+  // (fp8 pages are widened to the bf16 page layout first: the same order)
   bf16x8_t qb[4];
   {
     const int row = wave * 16 + i;
@@ -1069,7 +1125,10 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   }
   SplitState st;
   reset(st);
-  static_assert(kCascUnits == 4 && kCascWaves == 8, "the waits below count 4 LDS-DMA instructions per unit");
+  static_assert(kCascUnits == 4 && kCascWaves == 8, "the waits below count kCascUnits units per wave");
+  constexpr int kOps = kUnitOps<F8>;
+  static_assert(2 * kCascQuarter == kCascWaves, "fp8 pages: one (page, K or V) unit of a quarter per wave");
+  char* const img0 = lds + kCascSub * kUnitPage;  // fp8 pages: the quarter images
   static_assert(kCascUnits * kCascWaves == 2 * kCascSub, "every (page, K or V) unit of a sub-chunk has one wave");
   // A wave's units go out in order j = 0 .. kCascUnits - 1, unit j of every
   // wave carrying pages 4j .. 4j + 3: once every wave has seen its first
@@ -1080,15 +1139,30 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
     issue_sub(s0, n);
 #pragma unroll
     for (int j = 0; j < kCascUnits; ++j) {
-      if (j == 0) __asm__ __volatile__("s_waitcnt vmcnt(12)" ::: "memory");
-      else if (j == 1) __asm__ __volatile__("s_waitcnt vmcnt(8)" ::: "memory");
-      else if (j == 2) __asm__ __volatile__("s_waitcnt vmcnt(4)" ::: "memory");
-      else __asm__ __volatile__("s_waitcnt vmcnt(0)" ::: "memory");
+      if (j == 0) wait_vm<3 * kOps>();
+      else if (j == 1) wait_vm<2 * kOps>();
+      else if (j == 2) wait_vm<kOps>();
+      else wait_vm<0>();
       __syncthreads();
+      // fp8 pages: wave w widens unit w of the quarter (page 4j + w / 2, K or
+      // V) into image j % 2; the barrier of quarter j - 1 ordered every read
+      // of that image (quarter j - 2) before these writes
+      char* const img = img0 + (j & 1) * kCascQuarter * kPageLds;
+      if constexpr (F8) {
+        const int k = 4 * j + (wave >> 1);
+        if (k < n) {
+          const int half = (wave & 1) ? kF8Half : 0;
+          widen_unit_f8(lds + k * kUnitPage + half, img + (wave >> 1) * kPageLds + 2 * half, offs, lane);
+        }
+        __syncthreads();
+      }
       if (active) {
         for (int k = 4 * j; k < min(n, 4 * j + 4); ++k) {
           PageRegs pr;
-          read_page<-1>(pr, lds + k * kPageLds, offs);
+          if constexpr (F8)
+            read_page<-1>(pr, img + (k - 4 * j) * kPageLds, offs);
+          else
+            read_page<-1>(pr, lds + k * kUnitPage, offs);
           page_math<16>(st, pr, qb, 0, kPage, a.scale_log2, lane);
         }
       }
@@ -1101,13 +1175,14 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   // the wave's 16 x 128 fp32 tile at w * 16 * kORow floats, rows padded to
   // kORow floats to spread the banks.
   constexpr int kORow = kD + 4;
+  static_assert(kCascWaves * 16 * kORow * 4 <= kCascLds<F8>, "the output tiles fit the page buffers");
   float* tile = reinterpret_cast<float*>(lds) + wave * 16 * kORow;
   const float lsum = xor32_sum(xor16_sum(st.l));
   auto put = [&](auto rr_tag) {
     constexpr int RR = decltype(rr_tag)::value;
     const float lh = head_of_row<16, RR>(lsum, g);
     const float mh = head_of_row<16, RR>(st.m, g);
-    const float inv = 1.0f / lh;
+    const float inv = a.v_scale / lh;
     float* o = tile + (4 * g + RR) * kORow + i;
 #pragma unroll
     for (int nn = 0; nn < 8; ++nn) o[16 * nn] = st.o[nn][RR] * inv;
@@ -1374,21 +1449,17 @@ extern "C" size_t xv_cascade_decode_workspace_size(int batch, int num_q_heads, i
   return need;
 }
 
-extern "C" int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
-                                           const void* k_cache, const void* v_cache,
-                                           int64_t page_stride, int64_t tok_stride, int64_t head_stride,
-                                           const int32_t* block_tables, int64_t bt_stride,
-                                           const int32_t* cache_seqlens, const int32_t* prefix_tokens,
-                                           const int32_t* group_info, const int32_t* group_rows,
-                                           int num_groups, int max_prefix_blocks,
-                                           void* out, int64_t out_stride_tok,
-                                           void* workspace, size_t workspace_bytes,
-                                           int batch, int num_q_heads, int num_kv_heads, int head_dim,
-                                           int block_size, int max_blocks_per_seq, float scale,
-                                           hipStream_t stream) {
+namespace {
+int cascade_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k_cache,
+                const void* v_cache, int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                const int32_t* block_tables, int64_t bt_stride, const int32_t* cache_seqlens,
+                const int32_t* prefix_tokens, const int32_t* group_info, const int32_t* group_rows, int num_groups,
+                int max_prefix_blocks, void* out, int64_t out_stride_tok, void* workspace, size_t workspace_bytes,
+                int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size, int max_blocks_per_seq,
+                float scale, hipStream_t stream, bool f8, float k_scale, float v_scale) {
   const int rc0 = decode_check(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride,
                                head_stride, out, out_stride_tok, batch, num_q_heads, num_kv_heads, head_dim,
-                               block_size, max_blocks_per_seq);
+                               block_size, max_blocks_per_seq, f8);
   if (rc0) return rc0;
   if (batch > kMaxBatch || num_groups < 0 || num_groups > 65535 || max_prefix_blocks < 0 ||
       max_prefix_blocks > max_blocks_per_seq || !prefix_tokens || (num_groups > 0 && (!group_info || !group_rows)) ||
@@ -1420,15 +1491,25 @@ extern "C" int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, 
     c.num_groups = max_pre_pages > 0 ? num_groups : 0;
     c.hq = num_q_heads; c.hkv = num_kv_heads; c.chunk_pages = chunk_pages;
     c.pre_o = pre_o; c.pre_lse = pre_lse; c.sbt = sbt; c.ssl = ssl;
-    c.scale_log2 = scale * 1.4426950408889634f;
+    c.scale_log2 = (f8 ? scale * k_scale : scale) * 1.4426950408889634f;
+    c.v_scale = f8 ? v_scale : 1.0f;
     c.num_chunks = max(1, (max_pre_pages + chunk_pages - 1) / chunk_pages);
     c.num_view = min(batch, 64);
     const dim3 grid((unsigned)(c.num_groups * c.num_chunks * num_kv_heads + c.num_view));
-    switch (group) {
-      case 1: cascade_prefix_kernel<1><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
-      case 2: cascade_prefix_kernel<2><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
-      case 4: cascade_prefix_kernel<4><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
-      default: cascade_prefix_kernel<8><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+    if (f8) {
+      switch (group) {
+        case 1: cascade_prefix_kernel<1, true><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        case 2: cascade_prefix_kernel<2, true><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        case 4: cascade_prefix_kernel<4, true><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        default: cascade_prefix_kernel<8, true><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+      }
+    } else {
+      switch (group) {
+        case 1: cascade_prefix_kernel<1><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        case 2: cascade_prefix_kernel<2><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        case 4: cascade_prefix_kernel<4><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+        default: cascade_prefix_kernel<8><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
+      }
     }
     XV_CHECK_LAUNCH();
   }
@@ -1437,8 +1518,48 @@ extern "C" int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, 
   cp.pre_tokens = prefix_tokens; cp.chunk_pages = chunk_pages; cp.pre_o = pre_o; cp.pre_lse = pre_lse;
   return decode_chunk(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride, sbt,
                       max_blocks_per_seq, ssl, out, out_stride_tok, ws + Lw.dec, Lw.total - Lw.dec, batch,
-                      num_q_heads, num_kv_heads, nsub, (int)pages_per_seq(max_blocks_per_seq, block_size), scale,
-                      stream, cp);
+                      num_q_heads, num_kv_heads, nsub, (int)pages_per_seq(max_blocks_per_seq, block_size),
+                      f8 ? scale * k_scale : scale, stream, cp, f8, f8 ? v_scale : 1.0f);
+}
+}  // namespace
+
+extern "C" int xv_cascade_decode_attention(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                           const void* k_cache, const void* v_cache,
+                                           int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                           const int32_t* block_tables, int64_t bt_stride,
+                                           const int32_t* cache_seqlens, const int32_t* prefix_tokens,
+                                           const int32_t* group_info, const int32_t* group_rows,
+                                           int num_groups, int max_prefix_blocks,
+                                           void* out, int64_t out_stride_tok,
+                                           void* workspace, size_t workspace_bytes,
+                                           int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                           int block_size, int max_blocks_per_seq, float scale,
+                                           hipStream_t stream) {
+  return cascade_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
+                     block_tables, bt_stride, cache_seqlens, prefix_tokens, group_info, group_rows, num_groups,
+                     max_prefix_blocks, out, out_stride_tok, workspace, workspace_bytes, batch, num_q_heads,
+                     num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream, false, 1.0f, 1.0f);
+}
+
+// The same on fp8 (e4m3fn) K/V pages, scales as in xv_paged_decode_attention_fp8.
+extern "C" int xv_cascade_decode_attention_fp8(const void* q, int64_t q_stride_tok, int64_t q_stride_head,
+                                               const void* k_cache, const void* v_cache,
+                                               int64_t page_stride, int64_t tok_stride, int64_t head_stride,
+                                               const int32_t* block_tables, int64_t bt_stride,
+                                               const int32_t* cache_seqlens, const int32_t* prefix_tokens,
+                                               const int32_t* group_info, const int32_t* group_rows,
+                                               int num_groups, int max_prefix_blocks,
+                                               void* out, int64_t out_stride_tok,
+                                               void* workspace, size_t workspace_bytes,
+                                               int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                                               int block_size, int max_blocks_per_seq, float scale,
+                                               float k_scale, float v_scale, hipStream_t stream) {
+  if (!(k_scale > 0.0f) || !(v_scale > 0.0f) || !isfinite(k_scale) || !isfinite(v_scale))
+    return (int)hipErrorInvalidValue;
+  return cascade_run(q, q_stride_tok, q_stride_head, k_cache, v_cache, page_stride, tok_stride, head_stride,
+                     block_tables, bt_stride, cache_seqlens, prefix_tokens, group_info, group_rows, num_groups,
+                     max_prefix_blocks, out, out_stride_tok, workspace, workspace_bytes, batch, num_q_heads,
+                     num_kv_heads, head_dim, block_size, max_blocks_per_seq, scale, stream, true, k_scale, v_scale);
 }
 
 // ---------------------------------------------------------------------------

@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple] = {
         [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i32, i32, vp, i64, vp, sz,
          i32, i32, i32, i32, i32, i32, f32, vp],
     ),
+    "xv_cascade_decode_attention_fp8": (
+        i32,
+        [vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, vp, i32, i32, vp, i64, vp, sz,
+         i32, i32, i32, i32, i32, i32, f32, f32, f32, vp],
+    ),
     "xv_prefill_attention": (
         i32,
         [vp, i64, i64, vp, vp, i64, i64, vp, vp, i64, i64, i64, vp, i64, vp, vp, vp, i64,

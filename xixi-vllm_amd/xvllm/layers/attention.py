@@ -195,12 +195,19 @@ def cascade_decode_attention(
     head_dim: int,
     softmax_scale: float | None = None,
     out: torch.Tensor | None = None,
+    *,
+    k_scale: float = 1.0,
+    v_scale: float = 1.0,
 ) -> torch.Tensor:
     """paged_decode_attention with the shared prefixes of `plan` read once per
-    group (xv_cascade_decode_attention).  Same output as the plain decode up
+    group (xv_cascade_decode_attention, or _fp8 on an fp8 cache with the
+    scales of paged_decode_attention).  Same output as the plain decode up
     to fp32 summation order."""
     require_cuda(q, k_cache, v_cache, block_tables, cache_seqlens, plan.prefix_tokens)
-    require_bf16(q, k_cache, v_cache)
+    fp8 = k_cache.dtype == torch.float8_e4m3fn
+    require_bf16(q, *(() if fp8 else (k_cache, v_cache)))
+    if fp8 and v_cache.dtype != torch.float8_e4m3fn:
+        raise TypeError("k_cache and v_cache must share one dtype")
     q3, qs0, qs1 = _q_view(q, num_qo_heads, head_dim)
     bsz = q3.shape[0]
     nb, page, hkv, d = k_cache.shape
@@ -222,15 +229,17 @@ def cascade_decode_attention(
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=q.device)
         _CASCADE_WS[key] = ws
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
-    _C.check(
-        L.xv_cascade_decode_attention(
-            ptr(q3), qs0, qs1, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
-            ptr(bt), bt.stride(0), ptr(sl), ptr(plan.prefix_tokens), ptr(plan.group_info), ptr(plan.group_rows),
-            plan.num_groups, min(plan.max_prefix_blocks, max_blocks), ptr(out), out.stride(0), ptr(ws), ws.numel(),
-            bsz, num_qo_heads, num_kv_heads, head_dim, page, max_blocks, float(scale), stream_of(q),
-        ),
-        "xv_cascade_decode_attention",
+    args = (
+        ptr(q3), qs0, qs1, ptr(k_cache), ptr(v_cache), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        ptr(bt), bt.stride(0), ptr(sl), ptr(plan.prefix_tokens), ptr(plan.group_info), ptr(plan.group_rows),
+        plan.num_groups, min(plan.max_prefix_blocks, max_blocks), ptr(out), out.stride(0), ptr(ws), ws.numel(),
+        bsz, num_qo_heads, num_kv_heads, head_dim, page, max_blocks, float(scale),
     )
+    if fp8:
+        _C.check(L.xv_cascade_decode_attention_fp8(*args, float(k_scale), float(v_scale), stream_of(q)),
+                 "xv_cascade_decode_attention_fp8")
+    else:
+        _C.check(L.xv_cascade_decode_attention(*args, stream_of(q)), "xv_cascade_decode_attention")
     return out
 
 
@@ -385,11 +394,12 @@ class Attention(nn.Module):
         if attn.cascade is not None and not attn.is_prefill:
             # shared-prefix decode: the plan does not fit the vllm::attention schema
             k_cache, v_cache = _layer_caches(self.layer_id)
+            ks, vs = kv_scales()
             if attn.slot_mapping is not None:
                 store_kvcache(k.view(-1, self.num_kv_heads, self.head_dim), v.view(-1, self.num_kv_heads, self.head_dim),
-                              k_cache, v_cache, attn.slot_mapping)
+                              k_cache, v_cache, attn.slot_mapping, k_scale=ks, v_scale=vs)
             return cascade_decode_attention(q, k_cache, v_cache, attn.block_tables, attn.cache_seqlens, attn.cascade,
-                                            self.num_heads, self.num_kv_heads, self.head_dim)
+                                            self.num_heads, self.num_kv_heads, self.head_dim, k_scale=ks, v_scale=vs)
         return torch.ops.vllm.attention(
             q, k, v, attn.slot_mapping, attn.is_prefill, attn.cu_seqlens_q, attn.cu_seqlens_k,
             attn.max_seqlen_q, attn.max_seqlen_k, attn.block_tables, attn.cache_seqlens,

@@ -66,8 +66,6 @@ class ModelRunner:
         self.hidden_size = cfg.hidden_size
         self._meta = AttnMetadata(kv_cache=kv.kv_cache, k_scale=getattr(kv, "k_scale", 1.0),
                                   v_scale=getattr(kv, "v_scale", 1.0))
-        if kv.dtype == torch.float8_e4m3fn and cascade_groups:
-            raise ValueError("cascade decode reads bf16 pages only; use cascade_groups=0 with an fp8 pool")
         n_model_layers = len(model.model.layers)
         if kv.num_layers < n_model_layers:  # layer aliasing: layer i reads pool layer i % pool layers
             for i, layer in enumerate(model.model.layers):
