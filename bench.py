@@ -529,6 +529,70 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
             "achieved_GB/s": round((wbytes + kv_read) / (ms * 1e-3) / 1e9, 1)}, model
 
 
+def cascade_sweep(torch, dev, iters: int = 10) -> dict:
+    """Shared-prefix decode attention alone, plain against cascade, at the
+    Qwen3-32B attention shape (64 q / 8 kv heads, head-major 16-token pages),
+    B 32 x 32768 tokens: `rows` requests share the first `prefix` tokens (the
+    same pages), the rest of the KV is per request.  Two layers of KV are
+    cycled so that a call does not find the previous call's pages in the
+    last-level cache.  us per call (one layer), bf16 and fp8 pages."""
+    import numpy as np
+
+    from xvllm.layers.attention import CascadePlan, cascade_decode_attention, paged_decode_attention
+    from xvllm.prefix_cache import cascade_groups
+
+    hq, hkv, d, ctx, bsz = 64, 8, 128, 32768, 32
+    g = torch.Generator(device=dev).manual_seed(3)
+    q = torch.randn((bsz, hq * d), generator=g, device=dev).to(torch.bfloat16)
+    sl = torch.full((bsz,), ctx, dtype=torch.int32, device=dev)
+    out = {}
+    for rows, prefix in ((16, 8192), (32, 8192), (16, 24576), (32, 24576), (32, ctx - 256)):
+        npg, ppg = ctx // PAGE, prefix // PAGE
+        unique = ppg + rows * (npg - ppg) + (bsz - rows) * npg
+        perm = torch.randperm(unique, generator=torch.Generator().manual_seed(1)).to(torch.int32)
+        bt = torch.empty((bsz, npg), dtype=torch.int32)
+        o = ppg
+        for b in range(bsz):
+            own = npg - ppg if b < rows else npg
+            if b < rows:
+                bt[b, :ppg] = perm[:ppg]
+            bt[b, npg - own:] = perm[o:o + own]
+            o += own
+        pre, info, grp = cascade_groups(bt.numpy(), sl.cpu().numpy(), PAGE, max_rows=128 // (hq // hkv),
+                                        min_blocks=16, max_groups=2, max_prefix_blocks=ppg)
+        t = lambda a: torch.from_numpy(np.ascontiguousarray(a, np.int32)).to(dev)
+        plan = CascadePlan(t(pre), t(info), t(grp) if len(grp) else torch.zeros(1, dtype=torch.int32, device=dev),
+                           2, ppg)
+        btd = bt.to(dev)
+        rec = {}
+        for fp8 in (False, True):
+            caches = []
+            for _ in range(2):
+                kv = torch.randn((2, unique, hkv, PAGE, d), generator=g, device=dev)
+                kv = (kv / FP8_SCALE).to(torch.float8_e4m3fn) if fp8 else kv.to(torch.bfloat16)
+                caches.append((kv[0].transpose(1, 2), kv[1].transpose(1, 2)))
+            kw = _scales(caches[0][0])
+            for name, fn in (("plain", lambda k, v: paged_decode_attention(q, k, v, btd, sl, hq, hkv, d, **kw)),
+                             ("cascade", lambda k, v: cascade_decode_attention(q, k, v, btd, sl, plan, hq, hkv, d,
+                                                                                **kw))):
+                for _ in range(2):
+                    for k, v in caches:
+                        fn(k, v)
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(iters):
+                    for k, v in caches:
+                        fn(k, v)
+                e1.record()
+                torch.cuda.synchronize()
+                rec[f"{'fp8' if fp8 else 'bf16'}_{name}_us"] = round(e0.elapsed_time(e1) / (2 * iters) * 1e3, 1)
+            del caches
+            torch.cuda.empty_cache()
+        out[f"rows{rows}_prefix{prefix}"] = rec
+    return out
+
+
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
               max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, model=None, fp8: bool = False) -> dict:
     """Config 4: Qwen3-8B (random bf16 weights ~N(0,0.02)) serving 256 requests
@@ -720,6 +784,8 @@ def main() -> int:
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
     ap.add_argument("--config5", action="store_true", help="also run config 5 (Qwen3-32B-shaped long-context decode)")
     ap.add_argument("--config5-only", action="store_true", help="only config 5 (for profiling)")
+    ap.add_argument("--cascade-only", action="store_true",
+                    help="only the shared-prefix sweep: plain against cascade decode attention")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy (HBM counter calibration for rocprofv3 --pmc)")
     ap.add_argument("--seed", type=int, default=0)
@@ -762,6 +828,9 @@ def main() -> int:
         c58, model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
         c58c, model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
         print(json.dumps({"config5": c5, "config5_cascade": c5c, "config5_fp8": c58, "config5_cascade_fp8": c58c}))
+        return 0
+    if args.cascade_only:
+        print(json.dumps({"cascade_sweep": cascade_sweep(torch, dev)}))
         return 0
     if args.serve_only:
         greedy, model = serve_e2e(torch, dev, sampled=False)

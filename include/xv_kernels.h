@@ -159,7 +159,8 @@ int xv_gather_kv_fp8(const void* k_cache, const void* v_cache, int64_t cache_pag
  *     with prefix_tokens > 0 belongs to exactly one group, whose rows all have
  *     the same prefix_tokens and the same first prefix_tokens / block_size
  *     block ids; prefix_tokens[b] <= cache_seqlens[b] and
- *     <= max_prefix_blocks * block_size.
+ *     <= max_prefix_blocks * block_size; max_prefix_blocks * block_size
+ *     <= 1048576 (longer shared prefixes: hipErrorInvalidValue).
  *   group_info: int32 [num_groups][4], 16-byte aligned; group g's record is
  *     {first index into group_rows, number of rows, its first batch row,
  *     prefix_tokens of its rows}: the batch rows of group g are

@@ -153,6 +153,16 @@ def test_fp8_entry_points_reject_bad_arguments(lib):
         assert casc(**kw) == INVALID, kw
     assert casc(B=0) == 0
 
+
+def test_cascade_rejects_prefixes_beyond_its_chunk_table(lib):
+    """The prefix pass holds at most 32 chunks of 2048 pages (1M tokens of
+    shared prefix): longer prefixes are rejected before any launch."""
+    for fn, extra in ((lib.xv_cascade_decode_attention, ()), (lib.xv_cascade_decode_attention_fp8, (1.0, 1.0))):
+        blocks = 65536 // 16 + 1  # 256-token blocks: one block over 1M tokens
+        rc = fn(A, 4096, 128, A, A, 256 * 1024, 1024, 128, A, blocks, A, A, A, A, 1, blocks,
+                A, 4096, A, 1 << 45, 1, 32, 8, 128, 256, blocks, 0.088, *extra, None)
+        assert rc == INVALID
+
     def store(**kw):
         a = dict(k=A, kc=A, ps=16384, ts=1024, hs=128, n=8, hkv=8, d=128, ks=1.0, vs=1.0)
         a.update(kw)

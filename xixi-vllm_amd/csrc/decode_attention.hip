@@ -418,6 +418,96 @@ XV_INLINE void page_math(SplitState& st, const PageRegs& pr, const bf16x8_t (&qb
   for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vt[n], st.o[n], 0, 0, 0);
 }
 
+// Two pages whose LDS images sit kPairStride bytes apart (consecutive ring
+// slots or bf16 images), read in one asm block with one wait: the second
+// page's addresses are the first's plus an immediate offset.
+constexpr int kPairStride = kPageLds;
+XV_INLINE void read_page_pair(PageRegs& p0, PageRegs& p1, const char* buf, const LaneOffsets& lo) {
+  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+  static_assert(kPairStride == 8192, "the offsets below are kPairStride");
+  __asm__ __volatile__(
+      "ds_read_b128 %0, %24\n\t"
+      "ds_read_b128 %1, %25\n\t"
+      "ds_read_b128 %2, %26\n\t"
+      "ds_read_b128 %3, %27\n\t"
+      "ds_read_b64_tr_b16 %4, %28\n\t"
+      "ds_read_b64_tr_b16 %5, %29\n\t"
+      "ds_read_b64_tr_b16 %6, %30\n\t"
+      "ds_read_b64_tr_b16 %7, %31\n\t"
+      "ds_read_b64_tr_b16 %8, %32\n\t"
+      "ds_read_b64_tr_b16 %9, %33\n\t"
+      "ds_read_b64_tr_b16 %10, %34\n\t"
+      "ds_read_b64_tr_b16 %11, %35\n\t"
+      "ds_read_b128 %12, %24 offset:8192\n\t"
+      "ds_read_b128 %13, %25 offset:8192\n\t"
+      "ds_read_b128 %14, %26 offset:8192\n\t"
+      "ds_read_b128 %15, %27 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %16, %28 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %17, %29 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %18, %30 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %19, %31 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %20, %32 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %21, %33 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %22, %34 offset:8192\n\t"
+      "ds_read_b64_tr_b16 %23, %35 offset:8192\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(p0.kr[0]), "=&v"(p0.kr[1]), "=&v"(p0.kr[2]), "=&v"(p0.kr[3]), "=&v"(p0.vt[0]), "=&v"(p0.vt[1]),
+        "=&v"(p0.vt[2]), "=&v"(p0.vt[3]), "=&v"(p0.vt[4]), "=&v"(p0.vt[5]), "=&v"(p0.vt[6]), "=&v"(p0.vt[7]),
+        "=&v"(p1.kr[0]), "=&v"(p1.kr[1]), "=&v"(p1.kr[2]), "=&v"(p1.kr[3]), "=&v"(p1.vt[0]), "=&v"(p1.vt[1]),
+        "=&v"(p1.vt[2]), "=&v"(p1.vt[3]), "=&v"(p1.vt[4]), "=&v"(p1.vt[5]), "=&v"(p1.vt[6]), "=&v"(p1.vt[7])
+      : "v"(b0 + lo.k[0]), "v"(b0 + lo.k[1]), "v"(b0 + lo.k[2]), "v"(b0 + lo.k[3]), "v"(b0 + lo.v[0]),
+        "v"(b0 + lo.v[1]), "v"(b0 + lo.v[2]), "v"(b0 + lo.v[3]), "v"(b0 + lo.v[4]), "v"(b0 + lo.v[5]),
+        "v"(b0 + lo.v[6]), "v"(b0 + lo.v[7])
+      : "memory");
+}
+
+// page_math over two pages as one 32-token step (tokens 0..15 from p0,
+// 16..31 from p1; tokens >= ntok masked): one softmax update, the two S^T
+// products and the two P V products as independent MFMA chains.
+template <int G>
+XV_INLINE void page_math_pair(SplitState& st, const PageRegs& p0, const PageRegs& p1, const bf16x8_t (&qb)[4],
+                              int ntok, float scale_log2, int lane) {
+  const int g = lane >> 4;
+  floatx4_t a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    a0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p0.kr[s], qb[s], a0, 0, 0, 0);
+    a1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(p1.kr[s], qb[s], a1, 0, 0, 0);
+  }
+  float sc[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = (4 * g + j < ntok) ? a0[j] * scale_log2 : -INFINITY;
+    sc[4 + j] = (16 + 4 * g + j < ntok) ? a1[j] * scale_log2 : -INFINITY;
+  }
+  float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+  mx = xor32_max(xor16_max(mx));
+  const float m_new = fmaxf(st.m, mx);
+  if (__any(m_new > st.m + kLazy)) {  // lazy rescaling, as in page_math
+    const float alpha = __builtin_amdgcn_exp2f(st.m - m_new);
+    st.m = m_new;
+    st.l *= alpha;
+    rescale_row<G, 0>(st, alpha, g);
+    rescale_row<G, 1>(st, alpha, g);
+    rescale_row<G, 2>(st, alpha, g);
+    rescale_row<G, 3>(st, alpha, g);
+  }
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) p[j] = __builtin_amdgcn_exp2f(sc[j] - st.m);
+  st.l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  short4_t pa0, pa1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    pa0[j] = (short)f32_to_bf16(p[j]);
+    pa1[j] = (short)f32_to_bf16(p[4 + j]);
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa0, p0.vt[n], st.o[n], 0, 0, 0);
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.o[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa1, p1.vt[n], st.o[n], 0, 0, 0);
+}
+
 // VMEM operations one page issue makes: 4 LDS-DMA instructions each for K
 // and V, or 2 each for fp8 pages.
 template <bool F8> constexpr int kPageOps = F8 ? 4 : 8;
@@ -989,22 +1079,22 @@ int min_range_pages(int batch, int num_q_heads, int max_blocks_per_seq) {
 // chunk, kv head, group) reads the chunk's pages once and attends the whole
 // group's query rows to them: R = members x G rows (at most kCascRows), in
 // 16-row tiles on the MFMA columns (each column its own row, G = 16 in the
-// page math), one tile per wave.  Pages arrive in sub-chunks of up to
-// kCascSub pages by LDS-DMA, all of a sub-chunk's loads issued at once (its
-// page ids fetched first), so each workgroup has up to 128 KB in flight; the
-// waves then run their tiles over the sub-chunk.  Each row's normalised
-// chunk output and its log2-sum-exp go to the prefix partial slots, which the merge
-// combines with the row's suffix partials.  The launch's last workgroups
-// write the suffix view of every row instead (block-table rows shifted past
-// the prefix blocks, suffix lengths) for the suffix decode.
+// page math), one tile per wave.  The chunk's pages stream through a ring of
+// four quarters (4 pages each, 32 KB of bf16 pages) by LDS-DMA, three
+// quarters in flight while the tiles run over the fourth; the page ids are
+// fetched into LDS once.  Each row's normalised chunk output and its
+// log2-sum-exp go to the prefix partial slots, which the merge combines with
+// the row's suffix partials.  The same workgroups write the suffix view of
+// every row (block-table rows shifted past the prefix blocks, suffix
+// lengths) for the suffix decode.
 constexpr int kCascRows = 128;
 constexpr int kCascWaves = kCascRows / 16;  // one 16-row tile per wave
-constexpr int kCascSub = 16;                // pages per sub-chunk (128 KB of LDS)
-constexpr int kCascUnits = 2 * kCascSub / kCascWaves;  // (page, K or V) units each wave moves per sub-chunk
-// fp8 pages: a sub-chunk's raw pages (4 KB each) and two bf16 images of a
-// quarter sub-chunk (4 pages in the bf16 page layout), which the workgroup's
-// waves fill together, one (page, K or V) unit each, and then all read.
-constexpr int kCascQuarter = kCascSub / 4;
+constexpr int kCascSub = 16;                // pages in the ring (128 KB of bf16 pages)
+constexpr int kCascQuarter = kCascSub / 4;  // pages per quarter: one (page, K or V) unit per wave
+// fp8 pages: the ring holds raw pages (4 KB each), and two bf16 images of a
+// quarter (4 pages in the bf16 page layout), which the workgroup's waves fill
+// together, one (page, K or V) unit each, and then all read.
+constexpr int kCascMaxChunkPages = 2048;  // pages per prefix chunk (kCascMaxChunks of them: 1M-token prefixes)
 template <bool F8> constexpr int kCascLds = F8 ? kCascSub * (kPageLds / 2) + 2 * kCascQuarter * kPageLds
                                                : kCascSub * kPageLds;
 
@@ -1018,7 +1108,7 @@ struct CascadeArgs {
   const int4* grp_info;     // per group: first index into grp_rows, rows, first row, prefix tokens
   const int32_t* grp_rows;  // batch rows of each group
   const int32_t* pre_tokens;
-  int num_groups, hq, hkv, chunk_pages, num_chunks, num_view;
+  int num_groups, hq, hkv, chunk_pages, num_chunks;
   bf16_t* pre_o; float* pre_lse;
   int32_t* sbt; int32_t* ssl;  // suffix view: [batch, max_blocks] block table, [batch] lengths
   float scale_log2;
@@ -1043,14 +1133,18 @@ XV_INLINE void wait_vm() { __asm__ __volatile__("s_waitcnt vmcnt(%0)" ::"n"(N) :
 template <int G, bool F8 = false>
 __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(CascadeArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[kCascLds<F8>];
+  __shared__ int ids[kCascMaxChunkPages];  // the chunk's page ids
+  __shared__ int rowb[kCascRows];          // batch row of each tile row
   constexpr int kUnitPage = F8 ? kPageLds / 2 : kPageLds;  // LDS bytes of one page (K then V)
-  // the first num_view workgroups write the suffix view; then (chunk, group,
-  // kv head), chunk fastest: the workgroups of empty groups (a graph records a
-  // fixed group count) are interleaved with working ones instead of forming a
-  // tail of their own
-  const int w = (int)blockIdx.x - a.num_view;
-  if (w < 0) {
-    cascade_suffix_view(a, blockIdx.x, a.num_view);
+  // Workgroup w: (chunk, group, kv head), chunk fastest, so the workgroups of
+  // empty groups (a graph records a fixed group count) are interleaved with
+  // working ones instead of forming a tail of their own.  Every workgroup
+  // also writes the suffix view of rows w, w + grid, ... (the launch has at
+  // least min(batch, 64) workgroups); workgroups of their own for the view
+  // would hold this kernel's LDS too and push prefix work into a second round.
+  const int w = (int)blockIdx.x;
+  if (w >= a.num_groups * a.num_chunks * a.hkv) {
+    cascade_suffix_view(a, w, gridDim.x);
     return;
   }
   const int c = w % a.num_chunks, grp = (w / a.num_chunks) % a.num_groups,
@@ -1061,48 +1155,52 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   const int4 info = a.grp_info[grp];
   const int r0 = __builtin_amdgcn_readfirstlane(info.x);
   const int nm = __builtin_amdgcn_readfirstlane(min(info.y, kCascRows / G));
-  if (nm <= 0) return;
+  if (nm <= 0) {
+    cascade_suffix_view(a, w, gridDim.x);
+    return;
+  }
   const int b0 = __builtin_amdgcn_readfirstlane(info.z);
   const int npages = __builtin_amdgcn_readfirstlane(info.w) / kPage;
   const int p0 = c * a.chunk_pages, p1 = min(npages, p0 + a.chunk_pages);
-  if (p0 >= p1) return;
+  if (p0 >= p1) {
+    cascade_suffix_view(a, w, gridDim.x);
+    return;
+  }
   const int R = nm * G;
   const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
   const int i = lane & 15, g = lane >> 4;
   const bool active = wave * 16 < R;  // this wave's tile holds rows
   const uint32_t bytes = (uint32_t)(((int64_t)(kPage - 1) * a.tok_stride + kD) * (F8 ? 1 : 2));
-  // unit u = wave + kCascWaves * j of a sub-chunk: page u / 2, its K rows (u even) or V rows (u odd)
-  auto issue_sub = [&](int s0, int n) {
-    int page[kCascUnits];
+  const int np = p1 - p0;
+  // the chunk's page ids, fetched once into LDS (every issue then reads its
+  // id there instead of waiting on memory)
+  for (int k = threadIdx.x; k < np; k += kCascWaves * 64)
+    ids[k] = a.bt[(int64_t)b0 * a.bt_stride + (p0 + k) / a.nsub];
+  // Quarter q of the chunk: pages 4q .. 4q + 3 in ring slot q % 4 (slot
+  // pages 4 (q % 4) ..); wave w moves page 4q + w / 2, its K rows (w even) or
+  // V rows (w odd).  Pages past the chunk's end read its last page again
+  // (never used), so every issue counts the same kUnitOps instructions.
+  auto issue_quarter = [&](int q) {
+    const int k = min(4 * q + (wave >> 1), np - 1);
+    const int p = p0 + k;
+    const int id = __builtin_amdgcn_readfirstlane(ids[k]);
+    const int64_t base = (int64_t)id * a.page_stride + (int64_t)(p % a.nsub) * kPage * a.tok_stride +
+                         (int64_t)kvh * a.head_stride;
+    const bf16_t* src = (wave & 1) ? a.vc : a.kc;
+    char* const slot = lds + (4 * (q & 3) + (wave >> 1)) * kUnitPage;
+    if constexpr (F8) {  // element strides are byte strides
+      const __amdgpu_buffer_rsrc_t r =
+          page_rsrc(reinterpret_cast<const bf16_t*>(reinterpret_cast<const char*>(src) + base), bytes);
+      char* dst = slot + ((wave & 1) ? kF8Half : 0);
 #pragma unroll
-    for (int j = 0; j < kCascUnits; ++j) {  // the ids first: one wait for all of them
-      const int p = s0 + min((wave + kCascWaves * j) >> 1, n - 1);
-      page[j] = __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b0 * a.bt_stride + p / a.nsub]);
-    }
+      for (int s = 0; s < 2; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g8[s], 0, 0, kNontemporal);
+    } else {
+      const __amdgpu_buffer_rsrc_t r = page_rsrc(src + base, bytes);
+      char* dst = slot + ((wave & 1) ? kVPageBytes : 0);
 #pragma unroll
-    for (int j = 0; j < kCascUnits; ++j) {
-      const int u = wave + kCascWaves * j;
-      const int k = min(u >> 1, n - 1);  // past the sub-chunk: its last page again (never read)
-      const int p = s0 + k;
-      const int64_t base = (int64_t)page[j] * a.page_stride + (int64_t)(p % a.nsub) * kPage * a.tok_stride +
-                           (int64_t)kvh * a.head_stride;
-      const bf16_t* src = (u & 1) ? a.vc : a.kc;
-      if constexpr (F8) {  // element strides are byte strides
-        const __amdgpu_buffer_rsrc_t r =
-            page_rsrc(reinterpret_cast<const bf16_t*>(reinterpret_cast<const char*>(src) + base), bytes);
-        char* dst = lds + (u >> 1) * kUnitPage + ((u & 1) ? kF8Half : 0);
-#pragma unroll
-        for (int s = 0; s < 2; ++s)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g8[s], 0, 0,
-                                                   kNontemporal);
-      } else {
-        const __amdgpu_buffer_rsrc_t r = page_rsrc(src + base, bytes);
-        char* dst = lds + (u >> 1) * kUnitPage + ((u & 1) ? kVPageBytes : 0);
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g[s], 0, 0,
-                                                   kNontemporal);
-      }
+      for (int s = 0; s < 4; ++s)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)(dst + 1024 * s), 16, offs.g[s], 0, 0, kNontemporal);
     }
   };
   // Q^T B operand of the wave's tile: column i = row 16 w + i, k = d-chunk 4s + g
@@ -1112,6 +1210,7 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
     const int row = wave * 16 + i;
     if (row < R) {
       const int b = a.grp_rows[r0 + row / G];
+      if (g == 0) rowb[row] = b;  // for the output rows (ordered by the loop's barriers)
       const bf16_t* qr = a.q + (int64_t)b * a.q_st + (int64_t)(kvh * G + row % G) * a.q_sh;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -1125,50 +1224,49 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
   }
   SplitState st;
   reset(st);
-  static_assert(kCascUnits == 4 && kCascWaves == 8, "the waits below count kCascUnits units per wave");
   constexpr int kOps = kUnitOps<F8>;
-  static_assert(2 * kCascQuarter == kCascWaves, "fp8 pages: one (page, K or V) unit of a quarter per wave");
-  char* const img0 = lds + kCascSub * kUnitPage;  // fp8 pages: the quarter images
-  static_assert(kCascUnits * kCascWaves == 2 * kCascSub, "every (page, K or V) unit of a sub-chunk has one wave");
-  // A wave's units go out in order j = 0 .. kCascUnits - 1, unit j of every
-  // wave carrying pages 4j .. 4j + 3: once every wave has seen its first
-  // j + 1 units land (vmcnt), those pages are complete, so the tiles run over
-  // them while the later pages still stream in.
-  for (int s0 = p0; s0 < p1; s0 += kCascSub) {
-    const int n = min(kCascSub, p1 - s0);
-    issue_sub(s0, n);
-#pragma unroll
-    for (int j = 0; j < kCascUnits; ++j) {
-      if (j == 0) wait_vm<3 * kOps>();
-      else if (j == 1) wait_vm<2 * kOps>();
-      else if (j == 2) wait_vm<kOps>();
-      else wait_vm<0>();
+  static_assert(2 * kCascQuarter == kCascWaves, "one (page, K or V) unit of a quarter per wave");
+  char* const img0 = lds + kCascSub * kUnitPage;  // fp8 pages: the two quarter images
+  const int Q = (np + 3) / 4;
+  __syncthreads();  // the id table
+  // Three quarters in flight ahead of the one the tiles run over.  Step t
+  // waits for quarter t (the quarters issued after it, at most two, may
+  // still be in flight) and, past the barrier that every wave reaches only
+  // once done with quarter t - 1, refills that quarter's slot with quarter t + 3.
+  for (int q = 0; q < min(Q, 3); ++q) issue_quarter(q);
+  for (int t = 0; t < Q; ++t) {
+    if (t + 2 < Q) wait_vm<2 * kOps>();
+    else if (t + 1 < Q) wait_vm<kOps>();
+    else wait_vm<0>();
+    __syncthreads();
+    if (t + 3 < Q) issue_quarter(t + 3);
+    const int k0 = 4 * t, kn = min(np, k0 + 4);
+    char* const ring = lds + 4 * (t & 3) * kUnitPage;
+    // fp8 pages: wave w widens unit w of the quarter (page k0 + w / 2, K or
+    // V) into image t % 2; the first barrier of step t - 1 ordered every read
+    // of that image (step t - 2) before these writes
+    char* const img = img0 + (t & 1) * kCascQuarter * kPageLds;
+    if constexpr (F8) {
+      // every unit, also past the chunk's end (a re-read page): the pair
+      // steps below read whole pairs, masked but finite
+      const int half = (wave & 1) ? kF8Half : 0;
+      widen_unit_f8(ring + (wave >> 1) * kUnitPage + half, img + (wave >> 1) * kPageLds + 2 * half, offs, lane);
       __syncthreads();
-      // fp8 pages: wave w widens unit w of the quarter (page 4j + w / 2, K or
-      // V) into image j % 2; the barrier of quarter j - 1 ordered every read
-      // of that image (quarter j - 2) before these writes
-      char* const img = img0 + (j & 1) * kCascQuarter * kPageLds;
-      if constexpr (F8) {
-        const int k = 4 * j + (wave >> 1);
-        if (k < n) {
-          const int half = (wave & 1) ? kF8Half : 0;
-          widen_unit_f8(lds + k * kUnitPage + half, img + (wave >> 1) * kPageLds + 2 * half, offs, lane);
-        }
-        __syncthreads();
-      }
-      if (active) {
-        for (int k = 4 * j; k < min(n, 4 * j + 4); ++k) {
-          PageRegs pr;
-          if constexpr (F8)
-            read_page<-1>(pr, img + (k - 4 * j) * kPageLds, offs);
-          else
-            read_page<-1>(pr, lds + k * kUnitPage, offs);
-          page_math<16>(st, pr, qb, 0, kPage, a.scale_log2, lane);
-        }
+    }
+    if (active) {
+      // pages in pairs: 32-token steps; a pair's missing second page (odd
+      // count) is a re-read page, masked
+      const char* const src = F8 ? img : ring;
+      static_assert(kPairStride == kPageLds && (F8 || kUnitPage == kPageLds), "pair slots are kPairStride apart");
+      for (int k = k0; k < kn; k += 2) {
+        PageRegs pr0, pr1;
+        read_page_pair(pr0, pr1, src + (k - k0) * kPageLds, offs);
+        page_math_pair<16>(st, pr0, pr1, qb, k + 1 < kn ? 2 * kPage : kPage, a.scale_log2, lane);
       }
     }
-    __syncthreads();  // the next sub-chunk overwrites the buffers
   }
+  __syncthreads();  // the output tiles below reuse the ring
+  cascade_suffix_view(a, w, gridDim.x);  // every wave (the view loops over the workgroup's threads)
   if (!active) return;
   // Rows 16 w + 4 g + RR of O, normalised, go through LDS (the page buffers
   // are free now) so that each row's 512 bytes leave as whole 16-byte pieces:
@@ -1188,7 +1286,7 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
     for (int nn = 0; nn < 8; ++nn) o[16 * nn] = st.o[nn][RR] * inv;
     const int row = wave * 16 + 4 * g + RR;
     if (i == 0 && row < R) {
-      const int b = a.grp_rows[r0 + row / G];
+      const int b = rowb[row];
       a.pre_lse[((int64_t)c * a.batch + b) * a.hq + kvh * G + row % G] = mh + __log2f(lh);
     }
   };
@@ -1205,7 +1303,7 @@ __global__ __launch_bounds__(kCascWaves * 64) void cascade_prefix_kernel(Cascade
     const int rt = 4 * k + (lane >> 4);
     const int row = wave * 16 + rt;
     if (row >= R) break;
-    const int b = a.grp_rows[r0 + row / G];
+    const int b = rowb[row];
     const float* src = tile + rt * kORow + 8 * (lane & 15);
     const float4 lo = *reinterpret_cast<const float4*>(src), hi = *reinterpret_cast<const float4*>(src + 4);
     const float f[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -1477,9 +1575,10 @@ int cascade_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, cons
   const int nsub = block_size / kPage;
   const int group = num_q_heads / num_kv_heads;
   // 1. the prefix pass (at most kCascMaxChunks chunks of the longest prefix),
-  //    and in the launch's last z slice the suffix view of every row
+  //    whose workgroups also write the suffix view of every row
   const int max_pre_pages = max_prefix_blocks * nsub;
   const int chunk_pages = max(4, (max_pre_pages + kCascMaxChunks - 1) / kCascMaxChunks);
+  if (chunk_pages > kCascMaxChunkPages) return (int)hipErrorInvalidValue;  // prefixes beyond 1M tokens
   {
     CascadeArgs c;
     c.q = (const bf16_t*)q; c.q_st = q_stride_tok; c.q_sh = q_stride_head;
@@ -1494,8 +1593,7 @@ int cascade_run(const void* q, int64_t q_stride_tok, int64_t q_stride_head, cons
     c.scale_log2 = (f8 ? scale * k_scale : scale) * 1.4426950408889634f;
     c.v_scale = f8 ? v_scale : 1.0f;
     c.num_chunks = max(1, (max_pre_pages + chunk_pages - 1) / chunk_pages);
-    c.num_view = min(batch, 64);
-    const dim3 grid((unsigned)(c.num_groups * c.num_chunks * num_kv_heads + c.num_view));
+    const dim3 grid((unsigned)max(c.num_groups * c.num_chunks * num_kv_heads, min(batch, 64)));
     if (f8) {
       switch (group) {
         case 1: cascade_prefix_kernel<1, true><<<grid, kCascWaves * 64, 0, stream>>>(c); break;
