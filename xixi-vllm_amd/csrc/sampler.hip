@@ -1108,15 +1108,20 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
 // launches (a launch boundary makes one kernel's global writes visible to the
 // next, across XCDs):
 //   1. seg_stats:  per segment, the largest and smallest key and the greedy best;
-//   2. seg_hist:   per segment, bucket counts and masses, and the min-p key;
+//   2. seg_hist:   per segment, bucket counts and masses, the min-p key, and the
+//                  segment's total mass (its kept mass when the row has no cut);
 //   3. row_plan:   per row, the summed histograms give the bucket(s) holding the
 //                  cut-offs (greedy and all-NaN rows finish here);
 //   4. seg_gather: the candidates of those buckets, appended to the row's list;
 //   5. row_cut:    per row, the sorted list gives the exact cut and the kept
 //                  mass (top-k rows draw from the list and finish); a row whose
-//                  buckets hold more candidates than LDS runs sample_row;
-//   6. seg_kept:   per segment, the kept mass;
-//   7. row_draw:   per row, the segment holding floor(u * M), then the id in it.
+//                  buckets hold more candidates than LDS runs sample_row.  Each
+//                  segment's kept mass follows without another pass over the
+//                  logits: its masses of the buckets before the cut's bucket
+//                  (every candidate there is kept) plus its candidates in the
+//                  sorted list up to the cut (exact integer sums of the same
+//                  per-candidate masses);
+//   6. row_draw:   per row, the segment holding floor(u * M), then the id in it.
 // Buckets, masses, cuts and the draw are those of the one-workgroup path, so
 // the ids are identical to it.
 
@@ -1406,15 +1411,20 @@ __global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(SegArgs a) {
   kminp = seg_min_u(red, kminp);
   __syncthreads();
   const int64_t o = ((int64_t)b * a.R + r) * kBuckets;
-  for (int i = t; i < kBuckets; i += kSegThreads) {
-    uint32_t c = 0;
-    unsigned long long m = 0;
-    for (int ww = 0; ww < kSegWaves; ++ww) { c += wcnt[ww][i]; m += wmass[ww][i]; }
-    if (i == kBuckets - 1) { c += (uint32_t)far_c; m += (unsigned long long)far_m; }
-    a.seg_cnt[o + i] = c;
-    if (!p.use_k) a.seg_mass[o + i] = m;  // top-k rows take their masses from the list
+  static_assert(kSegThreads == kBuckets, "one thread per bucket");
+  uint32_t c = 0;
+  unsigned long long m = 0;
+  for (int ww = 0; ww < kSegWaves; ++ww) { c += wcnt[ww][t]; m += wmass[ww][t]; }
+  if (t == kBuckets - 1) { c += (uint32_t)far_c; m += (unsigned long long)far_m; }
+  a.seg_cnt[o + t] = c;
+  if (!p.use_k) a.seg_mass[o + t] = m;  // top-k rows take their masses from the list
+  // the segment's total mass: its kept mass if the row has no cut (row_cut
+  // replaces it for rows it cuts; top-k rows never reach the draw)
+  const int64_t total = seg_sum_l(red, p.use_k ? 0 : (int64_t)m);
+  if (t == 0) {
+    a.seg_minp[b * a.R + r] = kminp;
+    a.seg_kept[b * a.R + r] = total;
   }
-  if (t == 0) a.seg_minp[b * a.R + r] = kminp;
 }
 
 // One thread per bucket (kSegThreads == kBuckets).
@@ -1616,8 +1626,10 @@ XV_INLINE int64_t wave_first(bool pred, int64_t none) {
 // row_cut for a list of n <= 64 candidates, wave 0 alone: the same cut, kept
 // mass and draw as the workgroup list functions.
 // c: this lane's candidate (0 past n), in any order.
+// segk: per segment, the kept mass of the buckets before the cut's (rows
+// without top-k; the list's part is added here and the sums written out).
 XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
-                                 unsigned long long c) {
+                                 unsigned long long c, unsigned long long* segk) {
   const int lane = threadIdx.x & 63;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
   c = wave_sort_desc(c);
@@ -1662,6 +1674,10 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
     }
     return;
   }
+  // each segment's kept mass: its earlier buckets plus its listed candidates up to the cut
+  if (lane <= jcut) atomicAdd(&segk[cand_id(c) / a.seg_len], (unsigned long long)q);
+  __builtin_amdgcn_wave_barrier();  // the wave's LDS operations stay in order
+  if (lane < a.R) a.seg_kept[b * a.R + lane] = (int64_t)segk[lane];
   if (lane == 0) {
     plan.key_cut = cand_key(edge);
     plan.id_cut = cand_id(edge);
@@ -1670,9 +1686,10 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
   }
 }
 
-XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n) {
+XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
+                            unsigned long long* segk) {
   const int lane = threadIdx.x & 63;
-  row_cut_wave_list(a, plan, p, b, n, lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull);
+  row_cut_wave_list(a, plan, p, b, n, lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull, segk);
 }
 
 __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
@@ -1695,13 +1712,38 @@ __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
   const RowParams p = row_params(a, b);
   const float inv_t = plan.inv_t, zmax = plan.zmax;
   const int n = (int)min(plan.cand_count, (uint32_t)kMaxCand);
+  // Rows without top-k: per segment, the mass of the buckets before the cut's
+  // bucket, all of whose candidates are kept (the list's part is added
+  // below).  Those masses and a long list load in the same memory round trip.
+  __shared__ unsigned long long segk[kMaxSegs];
+  constexpr int kPer = kMaxSegs * kBuckets / kThreads;
+  static_assert(kPer * kThreads == kMaxSegs * kBuckets, "segment x bucket entries per thread");
+  const bool per_seg = !plan.use_k;
+  const int lo = plan.lo, nlo = per_seg ? a.R * lo : 0;
+  unsigned long long pm[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
+    const int idx = t + k * kThreads, r = idx / max(lo, 1);
+    pm[k] = idx < nlo ? a.seg_mass[((int64_t)b * a.R + r) * kBuckets + (idx - r * lo)] : 0ull;
+  }
+  if (n > 64) {
+    const unsigned long long* src = a.cand + (int64_t)b * a.cand_stride;
+    for (int i = t; i < n; i += kThreads) fs.cand[i] = src[i];
+  }
+  if (per_seg) {
+    if (t < kMaxSegs) segk[t] = 0ull;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int idx = t + k * kThreads;
+      if (idx < nlo) atomicAdd(&segk[idx / lo], pm[k]);
+    }
+  }
+  __syncthreads();
   if (n <= 64) {
-    if (t < 64) row_cut_wave(a, plan, p, b, n);
+    if (t < 64) row_cut_wave(a, plan, p, b, n, segk);
     return;
   }
-  const unsigned long long* src = a.cand + (int64_t)b * a.cand_stride;
-  for (int i = t; i < n; i += kThreads) fs.cand[i] = src[i];
-  __syncthreads();
   sort_cand_desc(fs, n);
   int64_t jcut;
   if (plan.use_k) {
@@ -1735,6 +1777,10 @@ __global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
     return;
   }
   const int64_t M = plan.m_before + list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+  for (int i = t; i <= jcut; i += kThreads)
+    atomicAdd(&segk[cand_id(fs.cand[i]) / a.seg_len], (unsigned long long)cand_mass(fs.cand[i], inv_t, zmax));
+  __syncthreads();
+  if (t < a.R) a.seg_kept[b * a.R + t] = (int64_t)segk[t];
   if (t == 0) {
     plan.key_cut = cand_key(edge);
     plan.id_cut = cand_id(edge);
@@ -1995,31 +2041,13 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
     if (sampler_exp2(log2_ratio(key_to_bits(key), pl.inv_t, pl.zmax)) >= p.min_p) kminp = key;
   }
   pl.kminp = wave_min_u(kminp);
-  row_cut_wave_list(a, pl, p, b, n, c);
+  row_cut_wave_list(a, pl, p, b, n, c, nullptr);  // top-k: drawn from the list, no per-segment masses
 }
 
 XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t id_cut, float inv_t, float zmax) {
   const uint32_t key = order_key(bits);
   const bool kept = key && (key > key_cut || (key == key_cut && (int64_t)id <= id_cut));
   return kept ? mass_of(exp_of(bits, inv_t, zmax)) : 0;
-}
-
-__global__ __launch_bounds__(kSegThreads) void seg_kept_kernel(SegArgs a) {
-  __shared__ SegRed red;
-  const int b = blockIdx.y, r = blockIdx.x;
-  const RowPlan plan = a.plans[b];  // every field in one round trip
-  if (plan.status != kPlanDraw) return;
-  const uint32_t key_cut = plan.key_cut;
-  const int64_t id_cut = plan.id_cut;
-  const float inv_t = plan.inv_t, zmax = plan.zmax;
-  const bf16_t* row = a.logits + (int64_t)b * a.stride;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
-  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
-  int64_t m = 0;
-  for_seg(row, vec_ok, beg, end,
-          [&](uint32_t bits, int id) { m += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax); });
-  m = seg_sum_l(red, m);
-  if (threadIdx.x == 0) a.seg_kept[b * a.R + r] = m;
 }
 
 __global__ __launch_bounds__(kSegThreads) void row_draw_kernel(SegArgs a) {
@@ -2224,8 +2252,6 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     seg_gather_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     row_cut_kernel<<<rows, kThreads, 0, stream>>>(a);
-    XV_CHECK_LAUNCH();
-    seg_kept_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     row_draw_kernel<<<rows, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
