@@ -21,6 +21,14 @@ none is served from the 256 MB last-level cache (us; unsplit -> split):
                M 1, 8: no gain
     o_proj     M 1, 8: 15.3 -> 10.1 (P 4)  M 128: 24.2 -> 15.6 (P 8)
                M 32, 64, 256: gains below the partials' extra reads
+
+The other two GEMMs stay unsplit (same measurement, bmm over the same views):
+gate_up (K 4096, N 24576) M 32-128: 45-51 unsplit, no split faster; M 256:
+65.5 -> 59.6 (P 2), less than its 50 MB of fp32 partials cost to write and
+read back.  qkv (N 6144) M 64: 17.5 -> 15.4 (P 4), M 128: 25.0 -> 17.7,
+M 256: 39.3 -> 23.1; its consumer is the fused q/k-norm + RoPE + KV-store
+kernel, which would need a partial-summing form for gains of a few us per
+layer at the largest serving batches.
 """
 from __future__ import annotations
 
