@@ -5,8 +5,9 @@ the rows need (a graph captured for long contexts), both page memory orders,
 and bf16 or fp8 (e4m3fn) pages.  Pool rows no sequence uses hold NaN, so a
 read past a row's end shows in the output.  The cascade (shared-prefix)
 decode gets the same treatment with random groups of rows sharing leading
-blocks.  Tolerance rtol/atol 2e-2 (bf16 output, fp32 accumulate); fp8 pages
-are compared with the oracle over the dequantized pages."""
+blocks, and prefill / chunked prefill with random query and cached-prefix
+lengths.  Tolerance rtol/atol 2e-2 (bf16 output, fp32 accumulate); fp8
+pages are compared with the oracle over the dequantized pages."""
 import numpy as np
 import pytest
 import torch
@@ -124,3 +125,60 @@ def test_cascade_decode_random_configurations(dev, seed):
                                    hq, hkv, d, **kw)
     torch.cuda.synchronize()
     _close(f32(out).reshape(bsz, hq, d), want)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_prefill_random_configurations(dev, seed):
+    """Prefill and chunked prefill: dense q/k/v rows, or a cached prefix plus
+    the chunk read through block tables of a random block size and page
+    order, bf16 or fp8 pages (gathered into bf16 rows first)."""
+    from xvllm.layers.attention import prefill_attention
+
+    rng = np.random.default_rng(3000 + seed)
+    group = int(rng.choice([1, 2, 4, 8]))
+    hkv = int(rng.choice([1, 2, 8])) if group < 8 else 8
+    hq, d = group * hkv, 128
+    bsz = int(rng.integers(1, 9))
+    qlens = [int(x) for x in rng.integers(0, 400, bsz)]
+    paged = bool(rng.random() < 0.7)
+    pre = [int(x) for x in rng.integers(0, 1500, bsz)] if paged else [0] * bsz
+    if max(qlens) == 0:
+        qlens[0] = 1
+    klens = [p_ + q_ for p_, q_ in zip(pre, qlens)]
+    block = int(rng.choice([16, 32, 64, 256]))
+    layout = str(rng.choice(["nhd", "hnd"]))
+    fp8 = paged and bool(rng.random() < 0.35)
+    print(f"prefill random seed {seed}: G {group} hkv {hkv} q {qlens} k {klens} paged {paged} block {block} "
+          f"{layout} fp8 {fp8}", flush=True)
+    g = torch.Generator().manual_seed(seed)
+    cu_q = np.concatenate([[0], np.cumsum(qlens)]).astype(np.int32)
+    cu_k = np.concatenate([[0], np.cumsum(klens)]).astype(np.int32)
+    q = randn_bf16((int(cu_q[-1]), hq, d), g)
+    tq, tk = torch.from_numpy(cu_q).to(dev), torch.from_numpy(cu_k).to(dev)
+    if paged:
+        need = sum((c + block - 1) // block for c in klens)
+        kc, vc, bt, _ = make_paged(klens, need + 3, hkv, d, g, page=block)
+        kw = {}
+        if fp8:
+            ks, vs = 0.05, 0.3
+            kq = O.quantize_fp8(f32(kc), np.float32(1.0) / np.float32(ks))
+            vq = O.quantize_fp8(f32(vc), np.float32(1.0) / np.float32(vs))
+            kref, vref = O.dequantize_fp8(kq, ks), O.dequantize_fp8(vq, vs)
+            kd = torch.from_numpy(np.ascontiguousarray(kq)).view(torch.float8_e4m3fn)
+            vd = torch.from_numpy(np.ascontiguousarray(vq)).view(torch.float8_e4m3fn)
+            kw = {"max_seqlen_k": max(klens), "kv_scale": (ks, vs)}
+        else:
+            kref, vref, kd, vd = f32(kc), f32(vc), kc, vc
+        kd, vd = kd.to(dev), vd.to(dev)
+        if layout == "hnd":
+            kd, vd = kd.transpose(1, 2).contiguous().transpose(1, 2), vd.transpose(1, 2).contiguous().transpose(1, 2)
+        want = O.prefill_attention(f32(q), cu_q, cu_k, k_cache=kref, v_cache=vref, block_tables=bt.numpy())
+        out = prefill_attention(q.to(dev), None, None, tq, tk, max(qlens), hq, hkv, d, k_cache=kd, v_cache=vd,
+                                block_tables=bt.to(dev), **kw)
+    else:
+        k = randn_bf16((int(cu_k[-1]), hkv, d), g)
+        v = randn_bf16((int(cu_k[-1]), hkv, d), g)
+        want = O.prefill_attention(f32(q), cu_q, cu_k, k=f32(k), v=f32(v))
+        out = prefill_attention(q.to(dev), k.to(dev), v.to(dev), tq, tk, max(qlens), hq, hkv, d)
+    torch.cuda.synchronize()
+    _close(f32(out).reshape(-1, hq, d), want)
