@@ -110,7 +110,8 @@ struct LaneOffsets {
   int g[4];  // global byte offset of load instruction s within a page
   int g8[2];  // fp8 pages: global byte offset of load instruction s (8 rows of 128 bytes each)
   uint32_t k8[2];  // fp8 pages: LDS offsets of this lane's two K pieces (its S^T A operands)
-  uint32_t v8[2];  // fp8 pages: LDS offsets of the two V pieces this lane converts to bf16
+  uint32_t v8[2];  // fp8 pages: LDS offsets of the two pieces of a tensor this lane widens to bf16 (widen_unit_f8)
+  uint32_t vt8[4];  // fp8 pages: LDS offsets of this lane's transposed byte reads of V (O tiles 2m, 2m+1)
   uint32_t k[4];  // LDS byte offset of this lane's K A-operand chunk for MFMA step s
   uint32_t v[8];  // LDS byte offset (V half) of this lane's transposed read for O tile n
 };
@@ -134,12 +135,23 @@ XV_INLINE LaneOffsets lane_offsets(int64_t tok_stride, int lane) {
   }
   // K: lane (g, i) takes token i's values 32g .. 32g+31 (pieces 2g, 2g+1):
   // MFMA step s contracts d-chunk 4g + s (q is read in the same order).
-  // V: lane l converts token l/4's values 32(l%4) .. +31.
+  // Widening a tensor to bf16: lane l converts token l/4's values 32(l%4) .. +31.
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     o.k8[h] = (uint32_t)(i * 128 + (((2 * g + h) ^ swz8(i)) << 4));
     const int r = lane >> 2, p = 2 * (lane & 3) + h;
     o.v8[h] = (uint32_t)(kF8Half + r * 128 + ((p ^ swz8(r)) << 4));
+  }
+  // fp8 V read transposed by bytes (ds_read_b64_tr_b8: in each 16-lane group
+  // output lane i's byte j is byte i % 8 of the 8 bytes input lane 2j + i / 8
+  // addresses): input lane (g, L) addresses token 4g + (j % 4), j = L / 2, of
+  // 16-byte piece 2m + j / 4, half L % 2; output lane (g, i) then holds tokens
+  // 4g .. 4g+3 of columns 16(2m) + i (bytes 0..3) and 16(2m+1) + i (bytes
+  // 4..7): the B operands of O tiles 2m and 2m + 1.
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int j = (lane & 15) >> 1, r = 4 * g + (j & 3), piece = 2 * m + (j >> 2);
+    o.vt8[m] = (uint32_t)(kF8Half + r * 128 + ((piece ^ swz8(r)) << 4) + 8 * (lane & 1));
   }
   // V B operand of tile n: lane (g, i) supplies token 4g + i/4, columns
   // 16n + 4(i%4) .. +3 = chunk 2n + (i%4)/2, bytes 8*(i%2) of it
@@ -280,79 +292,52 @@ XV_INLINE void read_page(PageRegs& pr, const char* buf, const LaneOffsets& lo) {
 #undef XV_PAGE_OPERANDS
 }
 
-// The same operands from an fp8 page image: the lane's two K pieces become
-// its four bf16 A operands in registers (each fp8 value is exact in bf16);
-// V goes through a bf16 image in LDS (the layout read_page reads, at vimg)
-// for the transposed B-operand reads.  VM as in read_page.
-// The raw fp8 pieces of one page a lane reads: two K, two V.
-struct RawF8 {
-  u32x4_t k0, k1, v0, v1;
-};
-template <int VM, bool WAIT = true>
-XV_INLINE void read_raw_f8(RawF8& w, const char* buf, const LaneOffsets& lo) {
-  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
-#define XV_RAW_READS         \
-  "s_waitcnt vmcnt(%4)\n\t"  \
-  "ds_read_b128 %0, %5\n\t"  \
-  "ds_read_b128 %1, %6\n\t"  \
-  "ds_read_b128 %2, %7\n\t"  \
-  "ds_read_b128 %3, %8\n\t"
-#define XV_RAW_OPERANDS                                                                                     \
-  : "=&v"(w.k0), "=&v"(w.k1), "=&v"(w.v0), "=&v"(w.v1)                                                        \
-  : "n"(VM), "v"(b0 + lo.k8[0]), "v"(b0 + lo.k8[1]), "v"(b0 + lo.v8[0]), "v"(b0 + lo.v8[1])
-  if constexpr (WAIT) {
-    __asm__ __volatile__(XV_RAW_READS "s_waitcnt lgkmcnt(0)" XV_RAW_OPERANDS : "memory");
-  } else {
-    __asm__ __volatile__(XV_RAW_READS XV_RAW_OPERANDS : "memory");
-  }
-#undef XV_RAW_READS
-#undef XV_RAW_OPERANDS
+// 4 fp8 (e4m3fn) values -> 4 bf16 (exact).
+XV_INLINE short4_t fp8x4_to_bf16(uint32_t w) {
+  const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  const uint32_t a = pack_bf16x2(lo[0], lo[1]), b = pack_bf16x2(hi[0], hi[1]);
+  short4_t r;
+  r[0] = (short)(a & 0xffffu);
+  r[1] = (short)(a >> 16);
+  r[2] = (short)(b & 0xffffu);
+  r[3] = (short)(b >> 16);
+  return r;
 }
-// Operands of the page whose raw pieces are in w (already complete).
-XV_INLINE void finish_page_f8(PageRegs& pr, const RawF8& w, char* vimg, const LaneOffsets& lo, int lane) {
-  const u32x4_t k0 = w.k0, k1 = w.k1, v0 = w.v0, v1 = w.v1;
-  {
-    const int r = lane >> 2, q = lane & 3;
-    uint32_t o[2][8];
-    fp8x16_to_bf16(v0, o[0]);
-    fp8x16_to_bf16(v1, o[1]);
-    char* row = vimg + r * 256;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {  // bf16 chunk 4q + j: values 8j .. 8j+7 of the lane's 32
-      const uint32_t* w = &o[j >> 1][4 * (j & 1)];
-      *reinterpret_cast<uint4*>(row + (((4 * q + j) ^ swz(r)) << 4)) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  }
-  {
-    uint32_t o[2][8];
-    fp8x16_to_bf16(k0, o[0]);
-    fp8x16_to_bf16(k1, o[1]);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) __builtin_memcpy(&pr.kr[j], &o[j >> 1][4 * (j & 1)], 16);
-  }
-  // the transposed V reads of read_page (their offsets include the K half)
-  const uint32_t vb = (uint32_t)reinterpret_cast<uintptr_t>(vimg) - kVPageBytes;
-  __asm__ __volatile__(
-      "ds_read_b64_tr_b16 %0, %8\n\t"
-      "ds_read_b64_tr_b16 %1, %9\n\t"
-      "ds_read_b64_tr_b16 %2, %10\n\t"
-      "ds_read_b64_tr_b16 %3, %11\n\t"
-      "ds_read_b64_tr_b16 %4, %12\n\t"
-      "ds_read_b64_tr_b16 %5, %13\n\t"
-      "ds_read_b64_tr_b16 %6, %14\n\t"
-      "ds_read_b64_tr_b16 %7, %15\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(pr.vt[0]), "=&v"(pr.vt[1]), "=&v"(pr.vt[2]), "=&v"(pr.vt[3]), "=&v"(pr.vt[4]), "=&v"(pr.vt[5]),
-        "=&v"(pr.vt[6]), "=&v"(pr.vt[7])
-      : "v"(vb + lo.v[0]), "v"(vb + lo.v[1]), "v"(vb + lo.v[2]), "v"(vb + lo.v[3]), "v"(vb + lo.v[4]),
-        "v"(vb + lo.v[5]), "v"(vb + lo.v[6]), "v"(vb + lo.v[7])
-      : "memory");
-}
+
+// The operands of an fp8 page straight from its raw image: the lane's two K
+// pieces (its S^T A operands: token i's values 32g .. 32g+31, so MFMA step s
+// contracts d-chunk 4g + s) and V by four transposed byte reads, in one asm
+// block with one wait; both convert to bf16 in registers.  VM as in read_page.
 template <int VM>
-XV_INLINE void read_page_f8(PageRegs& pr, const char* buf, char* vimg, const LaneOffsets& lo, int lane) {
-  RawF8 w;
-  read_raw_f8<VM>(w, buf, lo);
-  finish_page_f8(pr, w, vimg, lo, lane);
+XV_INLINE void read_page_f8t(PageRegs& pr, const char* buf, const LaneOffsets& lo) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  const uint32_t b0 = (uint32_t)reinterpret_cast<uintptr_t>(buf);
+  u32x4_t k0, k1;
+  u32x2_t v[4];
+  __asm__ __volatile__(
+      "s_waitcnt vmcnt(%6)\n\t"
+      "ds_read_b128 %0, %7\n\t"
+      "ds_read_b128 %1, %8\n\t"
+      "ds_read_b64_tr_b8 %2, %9\n\t"
+      "ds_read_b64_tr_b8 %3, %10\n\t"
+      "ds_read_b64_tr_b8 %4, %11\n\t"
+      "ds_read_b64_tr_b8 %5, %12\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(k0), "=&v"(k1), "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+      : "n"(VM), "v"(b0 + lo.k8[0]), "v"(b0 + lo.k8[1]), "v"(b0 + lo.vt8[0]), "v"(b0 + lo.vt8[1]),
+        "v"(b0 + lo.vt8[2]), "v"(b0 + lo.vt8[3])
+      : "memory");
+  uint32_t o[2][8];
+  fp8x16_to_bf16(k0, o[0]);
+  fp8x16_to_bf16(k1, o[1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) __builtin_memcpy(&pr.kr[j], &o[j >> 1][4 * (j & 1)], 16);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    pr.vt[2 * m] = fp8x4_to_bf16(v[m][0]);
+    pr.vt[2 * m + 1] = fp8x4_to_bf16(v[m][1]);
+  }
 }
 
 // One tensor (K or V) of an fp8 page image at `raw` (its 16 rows of 128
@@ -513,14 +498,14 @@ XV_INLINE void page_math_pair(SplitState& st, const PageRegs& p0, const PageRegs
 template <bool F8> constexpr int kPageOps = F8 ? 4 : 8;
 
 template <int G, int NB, bool F8>
-XV_INLINE void process_page(SplitState& st, const char* buf, char* img, const LaneOffsets& lo,
-                            const bf16x8_t (&qb)[4], int page_tok0, int ctx, float scale_log2, int lane) {
+XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& lo, const bf16x8_t (&qb)[4],
+                            int page_tok0, int ctx, float scale_log2, int lane) {
   // The page arrived by LDS-DMA; the VMEM operations of each of the NB-1
   // pages issued after it may still be in flight: vmcnt(ops*(NB-1)) waits
   // exactly for this page.
   PageRegs pr;
   if constexpr (F8) {
-    read_page_f8<kPageOps<true> * (NB - 1)>(pr, buf, img, lo, lane);
+    read_page_f8t<kPageOps<true> * (NB - 1)>(pr, buf, lo);
   } else {
     read_page<kPageOps<false> * (NB - 1)>(pr, buf, lo);
   }
@@ -590,6 +575,9 @@ template <int G> constexpr int kNbufG = G <= 4 ? 4 : 3;
 // conversion, V image round trip, math; 93 us at config 2, 69 us with the
 // math removed); a second wave on the SIMD overlaps one wave's chain with
 // the other's, 66 us.  The buffers shrink to fit eight waves' LDS in a CU.
+// (V now reaches its B operands by transposed byte reads of the raw page,
+// without the image round trip: 66 us as well; three waves per SIMD 82 us,
+// three buffers 68 us.)
 #ifndef XV_F8_WPE
 #define XV_F8_WPE 2
 #endif
@@ -762,7 +750,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   constexpr int BUF = kBufBytesT<G, F8>;
   constexpr int QOFF = kPageBufBytes<G, F8>;  // the q slot within a page buffer
   __shared__ __attribute__((aligned(16))) char lds[NB * BUF];
-  __shared__ __attribute__((aligned(16))) char img[F8 ? kVPageBytes : 16];  // fp8 pages: the bf16 V image
   __shared__ int pref[kMaxBatch + 1];  // pages of sequences 0..b-1
   __shared__ int sl[kMaxBatch];        // cache_seqlens
   __shared__ __attribute__((aligned(16))) char idtab[2 * kIdWindow * 4];
@@ -862,7 +849,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
     } else {
       read_q<G, NB, kPageOps<F8>, F8>(qb, buf + QOFF, lane);
     }
-    process_page<G, NB, F8>(st, buf, img, offs, qb, pc.pg * kPage, pc.ctx, a.scale_log2, lane);
+    process_page<G, NB, F8>(st, buf, offs, qb, pc.pg * kPage, pc.ctx, a.scale_log2, lane);
   };
 
   static_assert(NB <= 8, "at most eight ids per lookup");
