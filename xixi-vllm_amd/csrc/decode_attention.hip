@@ -621,40 +621,91 @@ XV_INLINE void read_q(bf16x8_t (&qb)[4], const char* slot, int lane) {
 }
 
 // Write the finished segment (b, kvh): bf16 output if this wave covered the
-// whole segment, else the normalised partial and its log2-sum-exp in slot part.
-template <int G, int RR>
-XV_INLINE void finish_row(const DecodeArgs& a, const SplitState& st, float lsum, int b, int head0, bool full,
-                          int part, int lane) {
-  const int i = lane & 15, g = lane >> 4;
-  const float lh = head_of_row<G, RR>(lsum, g);
-  const float mh = head_of_row<G, RR>(st.m, g);
-  const int row = 4 * g + RR;
-  if (row >= G) return;  // rows past G are replicas
-  const float inv = a.v_scale / lh;
-  const int head = head0 + row;
-  if (full) {
-    bf16_t* o = a.out + (int64_t)b * a.out_st + (int64_t)head * kD + i;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[16 * n] = (bf16_t)f32_to_bf16(st.o[n][RR] * inv);
-  } else {
-    const int64_t wrow = ((int64_t)b * a.hq + head) * a.max_parts + part;
-    float* o = a.ws_o + wrow * kD + i;
-#pragma unroll
-    for (int n = 0; n < 8; ++n) o[16 * n] = st.o[n][RR] * inv;
-    if (i == 0) a.ws_lse[wrow] = mh + __log2f(lh);
-  }
-}
-
+// whole segment, else the normalised partial and its log2-sum-exp in slot
+// part.  The O rows go through LDS `stage` (kQSlot<G> bytes: the q slot of
+// the page buffer in hand, free once its q is in registers) and leave as
+// whole 16-byte pieces, a few store instructions per segment instead of one
+// per 16-column tile and row block.
 template <int G>
 XV_INLINE void finish_segment(const DecodeArgs& a, const SplitState& st, int b, int kvh, bool full, int part,
-                              int lane) {
+                              int lane, char* stage) {
+  const int i = lane & 15, g = lane >> 4;
   // total p-sum of head c%G over the four rows
-  float lsum = xor16_sum(st.l);
-  lsum = xor32_sum(lsum);
-  finish_row<G, 0>(a, st, lsum, b, kvh * G, full, part, lane);
-  finish_row<G, 1>(a, st, lsum, b, kvh * G, full, part, lane);
-  finish_row<G, 2>(a, st, lsum, b, kvh * G, full, part, lane);
-  finish_row<G, 3>(a, st, lsum, b, kvh * G, full, part, lane);
+  const float lsum = xor32_sum(xor16_sum(st.l));
+  float inv[4], lse[4];
+  auto row_consts = [&](auto rr_tag) {
+    constexpr int RR = decltype(rr_tag)::value;
+    const float lh = head_of_row<G, RR>(lsum, g);
+    inv[RR] = a.v_scale / lh;
+    lse[RR] = head_of_row<G, RR>(st.m, g) + __log2f(lh);
+  };
+  row_consts(std::integral_constant<int, 0>{});
+  row_consts(std::integral_constant<int, 1>{});
+  row_consts(std::integral_constant<int, 2>{});
+  row_consts(std::integral_constant<int, 3>{});
+  // the wave's own LDS writes precede its reads (rows past G are replicas: not written)
+  auto wave_sync = [] {
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    __builtin_amdgcn_wave_barrier();
+  };
+  const int head0 = kvh * G;
+  if (full) {
+    uint16_t* s16 = reinterpret_cast<uint16_t*>(stage);  // row r (head head0 + r) at r * 256 B
+#pragma unroll
+    for (int RR = 0; RR < 4; ++RR) {
+      const int row = 4 * g + RR;
+      if (row < G) {
+#pragma unroll
+        for (int nn = 0; nn < 8; ++nn) s16[row * kD + 16 * nn + i] = (uint16_t)f32_to_bf16(st.o[nn][RR] * inv[RR]);
+      }
+    }
+    wave_sync();
+    // the G heads' rows are contiguous in the output row of sequence b
+    char* dst = reinterpret_cast<char*>(a.out + (int64_t)b * a.out_st + (int64_t)head0 * kD);
+    constexpr int kBytes = G * kD * 2;
+#pragma unroll
+    for (int k = 0; k < (kBytes + 1023) / 1024; ++k) {
+      const int off = 1024 * k + 16 * lane;
+      if (off < kBytes) *reinterpret_cast<uint4*>(dst + off) = *reinterpret_cast<const uint4*>(stage + off);
+    }
+    return;
+  }
+  // fp32 partial rows (512 B each, kMaxParts apart per head), in passes of
+  // as many rows as the stage holds
+  float* s32 = reinterpret_cast<float*>(stage);
+  constexpr int kRowsPerPass = G < kQSlot<G> / (kD * 4) ? G : kQSlot<G> / (kD * 4);
+  static_assert(kRowsPerPass >= 1 && G % kRowsPerPass == 0, "whole passes of partial rows");
+  const int64_t wrow0 = ((int64_t)b * a.hq + head0) * a.max_parts + part;  // head h: + h * max_parts
+#pragma unroll
+  for (int p0 = 0; p0 < G; p0 += kRowsPerPass) {
+#pragma unroll
+    for (int RR = 0; RR < 4; ++RR) {
+      const int row = 4 * g + RR;
+      if (row >= p0 && row < p0 + kRowsPerPass) {
+#pragma unroll
+        for (int nn = 0; nn < 8; ++nn) s32[(row - p0) * kD + 16 * nn + i] = st.o[nn][RR] * inv[RR];
+      }
+    }
+    wave_sync();
+    constexpr int kBytes = kRowsPerPass * kD * 4;
+#pragma unroll
+    for (int k = 0; k < (kBytes + 1023) / 1024; ++k) {
+      const int off = 1024 * k + 16 * lane;
+      if (off < kBytes) {
+        const int r = off / (kD * 4), w = off % (kD * 4);
+        char* dst = reinterpret_cast<char*>(a.ws_o + (wrow0 + (int64_t)(p0 + r) * a.max_parts) * kD) + w;
+        *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(stage + off);
+      }
+    }
+    wave_sync();  // the stage's reads are done before the next pass writes it
+  }
+#pragma unroll
+  for (int RR = 0; RR < 4; ++RR) {
+    const int row = 4 * g + RR;
+    if (i == 0 && row < G) s32[row] = lse[RR];
+  }
+  wave_sync();
+  if (lane < G) a.ws_lse[wrow0 + (int64_t)lane * a.max_parts] = s32[lane];
 }
 
 XV_INLINE void reset(SplitState& st) {
@@ -827,24 +878,25 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   SplitState st;
   reset(st);
   bf16x8_t qb[4];
-  auto finish = [&](const Cursor& c) {
+  auto finish = [&](const Cursor& c, char* stage) {
     const int64_t seg0 = (int64_t)a.hkv * pref[c.b] + (int64_t)c.kvh * c.npb;
     // a row with a shared prefix always leaves a partial: the merge combines it with the prefix pass's
     const bool pre = a.pre_tokens != nullptr && __builtin_amdgcn_readfirstlane(a.pre_tokens[c.b]) > 0;
     const bool full = seg0 >= f0 && seg0 + c.npb <= f0 + n && !pre;
     const int part = (int)(blockIdx.x - seg0 / L);
-    finish_segment<G>(a, st, c.b, c.kvh, full, part, lane);
+    finish_segment<G>(a, st, c.b, c.kvh, full, part, lane, stage);
     if (lane == 0 && seg0 + c.npb <= f0 + n) a.ws_nparts[c.b * a.hkv + c.kvh] = full ? 1 : part + 1;
   };
   auto process = [&](int x, int slot) {
-    const char* buf = lds + slot * BUF;
+    char* buf = lds + slot * BUF;
     if (x > 0) {
       const Cursor prev = pc;
       advance(pc, pref, sl, a.hkv, a.batch, a.nsub);
       if (pc.pg == 0) {
-        finish(prev);
-        reset(st);
+        // the new segment's q first: its slot then stages the finished one
         read_q<G, NB, kPageOps<F8>, F8>(qb, buf + QOFF, lane);
+        finish(prev, buf + QOFF);
+        reset(st);
       }
     } else {
       read_q<G, NB, kPageOps<F8>, F8>(qb, buf + QOFF, lane);
@@ -884,7 +936,9 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
       if (x0 + u < n) process(x0 + u, u);
     }
   }
-  finish(pc);
+  // the last processed buffer's q slot: its q is in registers, and no DMA
+  // targets it any more (q only comes with a segment's first page)
+  finish(pc, lds + ((n - 1) % NB) * BUF + QOFF);
   XV_DECODE_TIMESTAMP(2);
 }
 
