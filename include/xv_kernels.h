@@ -76,8 +76,8 @@ int xv_store_kvcache_fp8(const void* key, int64_t key_stride_tok, int64_t key_st
  *   cache_seqlens: int32 [B]; 0 marks a padding row whose output is written as zeros
  *   out    : element (b, h, d) at b*out_stride_tok + h*D + d
  *   workspace: at least xv_paged_decode_workspace_size(...) bytes: per-segment
- *              partial counts, then fp32 partial outputs (and their
- *              log2-sum-exp) of sequences split across waves, merged by a
+ *              partial counts, then partial outputs (bf16 rows; their
+ *              log2-sum-exp in fp32) of sequences split across waves, merged by a
  *              second kernel.  No initial contents are required.  Calls
  *              sharing a workspace must be ordered on one stream.
  * Query head h reads kv head h / (Hq / Hkv).  scale multiplies q.k (1/sqrt(D) in the reference).

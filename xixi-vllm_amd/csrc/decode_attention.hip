@@ -6,8 +6,8 @@
 // number of pages and the whole grid is resident at once (no dispatch rounds,
 // no tail of late units).  A range may cover several (sequence, kv head)
 // segments; a segment cut by range boundaries yields one partial per wave,
-// merged by a second kernel through an fp32 workspace (normalised partial
-// output + log2-sum-exp).  A segment inside one range is written directly.
+// merged by a second kernel through a workspace (normalised partial output
+// in bf16 + fp32 log2-sum-exp).  The merge weights and sums in fp32.  A segment inside one range is written directly.
 // All G = Hq/Hkv query heads of a kv head are served by one pass.  Per page:
 //   K and V go HBM -> LDS by LDS-DMA, whole 256-byte rows per instruction,
 //   into a swizzled image (conflict-free reads below).
@@ -48,6 +48,7 @@ struct DecodeArgs {
   const int32_t* seqlens;
   bf16_t* out; int64_t out_st;
   float* ws_o; float* ws_lse;
+  bf16_t* ws_ob;  // the partial rows, bf16, kD per row (in ws_o's region)
   int* ws_nparts;  // partials per (sequence, kv head), written by the wave holding the segment's last page
   int batch, hq, hkv, group;
   int nsub;       // 16-token pages per cache block (block_size / 16)
@@ -621,7 +622,7 @@ XV_INLINE void read_q(bf16x8_t (&qb)[4], const char* slot, int lane) {
 }
 
 // Write the finished segment (b, kvh): bf16 output if this wave covered the
-// whole segment, else the normalised partial and its log2-sum-exp in slot
+// whole segment, else the normalised partial (bf16, as the output is) and its log2-sum-exp in slot
 // part.  The O rows go through LDS `stage` (kQSlot<G> bytes: the q slot of
 // the page buffer in hand, free once its q is in registers) and leave as
 // whole 16-byte pieces, a few store instructions per segment instead of one
@@ -670,35 +671,32 @@ XV_INLINE void finish_segment(const DecodeArgs& a, const SplitState& st, int b, 
     }
     return;
   }
-  // fp32 partial rows (512 B each, kMaxParts apart per head), in passes of
-  // as many rows as the stage holds
+  // bf16 partial rows (256 B each, max_parts rows apart per head)
+  uint16_t* s16 = reinterpret_cast<uint16_t*>(stage);
   float* s32 = reinterpret_cast<float*>(stage);
-  constexpr int kRowsPerPass = G < kQSlot<G> / (kD * 4) ? G : kQSlot<G> / (kD * 4);
-  static_assert(kRowsPerPass >= 1 && G % kRowsPerPass == 0, "whole passes of partial rows");
   const int64_t wrow0 = ((int64_t)b * a.hq + head0) * a.max_parts + part;  // head h: + h * max_parts
 #pragma unroll
-  for (int p0 = 0; p0 < G; p0 += kRowsPerPass) {
+  for (int RR = 0; RR < 4; ++RR) {
+    const int row = 4 * g + RR;
+    if (row < G) {
 #pragma unroll
-    for (int RR = 0; RR < 4; ++RR) {
-      const int row = 4 * g + RR;
-      if (row >= p0 && row < p0 + kRowsPerPass) {
-#pragma unroll
-        for (int nn = 0; nn < 8; ++nn) s32[(row - p0) * kD + 16 * nn + i] = st.o[nn][RR] * inv[RR];
-      }
+      for (int nn = 0; nn < 8; ++nn) s16[row * kD + 16 * nn + i] = (uint16_t)f32_to_bf16(st.o[nn][RR] * inv[RR]);
     }
-    wave_sync();
-    constexpr int kBytes = kRowsPerPass * kD * 4;
+  }
+  wave_sync();
+  {
+    constexpr int kBytes = G * kD * 2;
 #pragma unroll
     for (int k = 0; k < (kBytes + 1023) / 1024; ++k) {
       const int off = 1024 * k + 16 * lane;
       if (off < kBytes) {
-        const int r = off / (kD * 4), w = off % (kD * 4);
-        char* dst = reinterpret_cast<char*>(a.ws_o + (wrow0 + (int64_t)(p0 + r) * a.max_parts) * kD) + w;
+        const int r = off / (kD * 2), w = off % (kD * 2);
+        char* dst = reinterpret_cast<char*>(a.ws_ob + (wrow0 + (int64_t)r * a.max_parts) * kD) + w;
         *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(stage + off);
       }
     }
-    wave_sync();  // the stage's reads are done before the next pass writes it
   }
+  wave_sync();  // the stage's reads are done before the log2-sum-exps overwrite it
 #pragma unroll
   for (int RR = 0; RR < 4; ++RR) {
     const int row = 4 * g + RR;
@@ -1040,16 +1038,11 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
       merge_general<false>(
           n + npre,
           [&](int j, int i, float4& lo, float4& hi) {
-            if (j < n) {
-              const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
-              lo = src[0];
-              hi = src[1];
-            } else {  // prefix chunk partials are bf16
-              float f[8];
-              unpack8(load_vec8(a.pre_o + ((j - n) * cstride + prow) * kD + 8 * i), f);
-              lo = make_float4(f[0], f[1], f[2], f[3]);
-              hi = make_float4(f[4], f[5], f[6], f[7]);
-            }
+            float f[8];  // suffix and prefix chunk partials are bf16
+            unpack8(load_vec8(j < n ? a.ws_ob + (row0 + j) * kD + 8 * i : a.pre_o + ((j - n) * cstride + prow) * kD + 8 * i),
+                    f);
+            lo = make_float4(f[0], f[1], f[2], f[3]);
+            hi = make_float4(f[4], f[5], f[6], f[7]);
           },
           [&](int j) { return j < n ? a.ws_lse[row0 + j] : a.pre_lse[(j - n) * cstride + prow]; }, 0.f, orow,
           lane);
@@ -1064,7 +1057,8 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   for (int r = 0; r < kFastParts; ++r) {
     const int64_t row = row0 + min(r, a.max_parts - 1);
     lf[r] = a.ws_lse[row];
-    vf[r] = *reinterpret_cast<const float2*>(a.ws_o + row * kD + d);
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(a.ws_ob + row * kD + d);
+    vf[r] = make_float2(__uint_as_float(u << 16), __uint_as_float(u & 0xffff0000u));
   }
   const float lmine = lane < a.max_parts ? a.ws_lse[row0 + lane] : -INFINITY;
   if (ctx <= 0) {
@@ -1092,9 +1086,10 @@ __global__ __launch_bounds__(64) void merge_parts_kernel(DecodeArgs a) {
   merge_general<true>(
       n,
       [&](int j, int i, float4& lo, float4& hi) {
-        const float4* src = reinterpret_cast<const float4*>(a.ws_o + (row0 + j) * kD + 8 * i);
-        lo = src[0];
-        hi = src[1];
+        float f[8];
+        unpack8(load_vec8(a.ws_ob + (row0 + j) * kD + 8 * i), f);
+        lo = make_float4(f[0], f[1], f[2], f[3]);
+        hi = make_float4(f[4], f[5], f[6], f[7]);
       },
       [&](int j) { return a.ws_lse[row0 + j]; }, lmine, orow, lane);
 }
@@ -1381,7 +1376,8 @@ int waves_for(int group, bool f8 = false) {
 
 }  // namespace
 
-// Workspace layout: [partial counts int32, B*Hkv, padded to 256 B][partial outputs fp32][partial log2-sum-exp fp32]
+// Workspace layout: [partial counts int32, B*Hkv, padded to 256 B][partial outputs: bf16 rows of kD in a region
+// sized for fp32][partial log2-sum-exp fp32]
 size_t counter_bytes(int batch, int num_kv_heads) { return ((size_t)batch * num_kv_heads * 4 + 255) / 256 * 256; }
 
 // Workspace of one launch of `batch` <= kMaxBatch sequences; max_pages counts
@@ -1446,6 +1442,7 @@ int decode_chunk(const void* q, int64_t q_stride_tok, int64_t q_stride_head, con
   a.ws_nparts = (int*)workspace;
   a.ws_o = (float*)((char*)workspace + counter_bytes(batch, num_kv_heads));
   a.ws_lse = a.ws_o + (size_t)batch * num_q_heads * a.max_parts * kD;
+  a.ws_ob = reinterpret_cast<bf16_t*>(a.ws_o);
   a.batch = batch; a.hq = num_q_heads; a.hkv = num_kv_heads; a.group = group; a.lmin = lmin; a.nsub = nsub;
   // ranges: enough to fill the resident wave slots, never more than needed at lmin pages each
   const int64_t max_total = (int64_t)batch * num_kv_heads * max_pages;
