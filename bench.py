@@ -34,10 +34,10 @@ sys.path.insert(0, str(ROOT / "xixi-vllm_amd"))
 HBM_PEAK_GBS = 8000.0
 # HBM bytes per paged_decode_kernel launch at config 2, from rocprofv3 --pmc
 # FETCH_SIZE / WRITE_SIZE scaled by a 1 GiB copy (profiles/paged_decode_attention_config2.md):
-# 2 x 319425.9 KiB read (FETCH_SIZE counts half on this part) + 3225.4 KiB written;
-# on fp8 pages 2 x 160336.4 + 5336.7 KiB.
-MEASURED_TRAFFIC_BYTES = int((2 * 319425.9 + 3225.4) * 1024)
-MEASURED_TRAFFIC_BYTES_FP8 = int((2 * 160336.4 + 5336.7) * 1024)
+# 2 x 319019.9 KiB read (FETCH_SIZE counts half on this part) + 1722.5 KiB written;
+# on fp8 pages 2 x 160178.0 + 2831.6 KiB.
+MEASURED_TRAFFIC_BYTES = int((2 * 319019.9 + 1722.5) * 1024)
+MEASURED_TRAFFIC_BYTES_FP8 = int((2 * 160178.0 + 2831.6) * 1024)
 HQ, HKV, D, PAGE = 32, 8, 128, 16
 
 
