@@ -406,6 +406,32 @@ int xv_sample(const void* logits, int64_t logits_stride, int batch, int vocab,
               hipStream_t stream);
 
 /*
+ * Weight-streaming GEMM of a decode batch: out = x[m, k] . w[n, k]^T, m <= 64,
+ * bf16 operands, fp32 accumulate.  Replaces, for decode batches, the GEMMs
+ * of Qwen3MLP.forward (src/compute/models/qwen3.py:62-64: gate_up_proj,
+ * MergedColumnParallelLinear.forward src/compute/layers/linear.py:306, with
+ * the SiLU-and-mul after it, activation.py:6-8; down_proj,
+ * RowParallelLinear.forward linear.py:141) and o_proj (qwen3.py:115,
+ * linear.py:141); prefill and larger batches keep them on hipBLASLt.
+ *   w_packed  w in 16-row x 64-column tiles of 2 KB, row blocks outermost,
+ *             tile (nb, sg): w[16 nb + l % 16][64 sg + 8 (l / 16) + e] at
+ *             8 l + e and w[16 nb + l % 16][64 sg + 32 + 8 (l / 16) + e] at
+ *             512 + 8 l + e (l < 64, e < 8); 16-byte aligned.
+ *   x         row i at i * x_stride (a multiple of 8, >= k), 16-byte aligned.
+ *   mode 0    bf16 out[m, n], row stride out_stride, 8-byte aligned.
+ *   mode 1    fp32 partial products of K split `parts` ways: out[p][i][j] at
+ *             p * part_stride + i * out_stride + j, 16-byte aligned, strides
+ *             multiples of 4; their sum over p is the product.
+ *   mode 2    w is the gate/up weight [2I, k] (gate rows first); bf16
+ *             out[m, I] = silu(g) * u with g, u the two products rounded to bf16.
+ *   col_tiles 16-row tiles per wave (1, 2 or 4; 2 or 4 in mode 2), waves 4 or 8:
+ *             n a multiple of 16 col_tiles waves; k a multiple of 256 parts.
+ */
+int xv_dense_gemm(const void* x, int64_t x_stride, const void* w_packed, void* out, int64_t out_stride,
+                  int64_t part_stride, int m, int n, int k, int mode, int col_tiles, int waves, int parts,
+                  hipStream_t stream);
+
+/*
  * Streaming copy of `bytes` (a multiple of 16; both pointers 16-byte aligned)
  * with non-temporal 16-byte loads and stores.  No counterpart in the
  * reference: a measurement yardstick for the HBM-bound kernels above (what a

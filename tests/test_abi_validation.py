@@ -192,3 +192,46 @@ def test_fp8_model_entry_points_reject_bad_arguments(lib):
     for kw in (dict(kc=A + 4), dict(ts=1028), dict(out=U), dict(ost=512), dict(D=64), dict(ks=-1.0)):
         assert gather(**kw) == INVALID, kw
     assert gather(B=0) == 0
+
+
+def _gemm(lib, **kw):
+    a = dict(x=A, xs=4096, w=A, out=A, os=6144, ps=0, m=64, n=6144, k=4096, mode=0, ct=2, wv=4, p=1)
+    a.update(kw)
+    return lib.xv_dense_gemm(a["x"], a["xs"], a["w"], a["out"], a["os"], a["ps"], a["m"], a["n"], a["k"], a["mode"],
+                             a["ct"], a["wv"], a["p"], None)
+
+
+def test_dense_gemm_rejects_bad_arguments(lib):
+    for kw in (dict(m=65), dict(m=-1), dict(n=6144 + 16), dict(k=4096 + 64), dict(ct=3), dict(wv=2), dict(p=0),
+               dict(p=2), dict(mode=3), dict(mode=2, ct=1), dict(x=U), dict(w=U), dict(xs=4100), dict(xs=2048),
+               dict(os=6143), dict(os=1024), dict(out=A + 4), dict(mode=1, p=4, ps=64 * 6144 - 4),
+               dict(mode=1, p=4, out=A + 8, ps=64 * 6144), dict(mode=1, p=8, k=4096 + 256, ps=64 * 6144)):
+        assert _gemm(lib, **kw) == INVALID, kw
+    assert _gemm(lib, m=0) == 0  # nothing to do
+
+
+def test_pack_weight_tile_order():
+    """pack_weight against its definition, element by element with explicit
+    index arithmetic: tile (nb, sg), lane l = 16 g + r, element e."""
+    import numpy as np
+    import torch
+
+    from xvllm.layers.linear import pack_weight
+
+    n, k = 48, 192
+    w = torch.zeros((n, k), dtype=torch.bfloat16)
+    ids = np.arange(n * k).reshape(n, k)
+    wi = torch.from_numpy(ids.astype(np.int32))
+    packed = pack_weight(wi.view(n, k)).data.numpy()
+    assert packed.shape == (n * k,)
+    for nb in range(n // 16):
+        for sg in range(k // 64):
+            base = (nb * (k // 64) + sg) * 1024
+            for l in range(64):
+                r, g = l % 16, l // 16
+                for e in range(8):
+                    assert packed[base + 8 * l + e] == ids[16 * nb + r, 64 * sg + 8 * g + e]
+                    assert packed[base + 512 + 8 * l + e] == ids[16 * nb + r, 64 * sg + 32 + 8 * g + e]
+    assert sorted(packed.tolist()) == list(range(n * k))  # a permutation
+    with pytest.raises(ValueError):
+        pack_weight(w[:, :100])

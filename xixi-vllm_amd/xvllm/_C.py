@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple] = {
         i32, [vp, vp, i64, i64, i64, vp, i64, i32, vp, i32, i32, i32, i32, f32, f32, vp, vp, i64, vp]
     ),
     "xv_silu_and_mul": (i32, [vp, i64, vp, i64, i64, i32, vp]),
+    "xv_dense_gemm": (i32, [vp, i64, vp, vp, i64, i64, i32, i32, i32, i32, i32, i32, i32, vp]),
     "xv_stream_copy": (i32, [vp, vp, i64, i32, vp]),
     "xv_sampler_workspace_size": (sz, [i32, i32]),
     "xv_sample": (i32, [vp, i64, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz, vp]),

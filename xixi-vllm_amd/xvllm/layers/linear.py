@@ -80,3 +80,105 @@ def split_k_views(x: torch.Tensor, w: torch.Tensor, p: int) -> tuple[torch.Tenso
     m, k = x.shape
     n = w.shape[0]
     return x.view(m, p, k // p).transpose(0, 1), w.view(n, p, k // p).permute(1, 2, 0)
+
+
+# Output forms of xv_dense_gemm (csrc/dense_gemm.hip).
+GEMM_BF16, GEMM_PARTS, GEMM_SILU_MUL = 0, 1, 2
+
+
+class PackedWeight(NamedTuple):
+    """A [N, K] weight in the tile order the decode GEMM kernel streams:
+    16-row x 64-column tiles of 2 KB, each in the kernel's lane order (see
+    pack_weight), row blocks outermost."""
+
+    data: torch.Tensor  # bf16, N * K elements
+    n: int
+    k: int
+
+
+def pack_weight(w: torch.Tensor) -> PackedWeight:
+    """Pack w [N, K] (N % 16 == 0, K % 64 == 0) for dense_gemm: tile (nb, sg)
+    holds, for lane l = 16 g + r (r < 16, g < 4), w[16 nb + r, 64 sg + 8 g + e]
+    at 8 l + e and w[16 nb + r, 64 sg + 32 + 8 g + e] at 512 + 8 l + e."""
+    n, k = w.shape
+    if n % 16 or k % 64:
+        raise ValueError(f"pack_weight: [{n}, {k}] is not a whole number of 16 x 64 tiles")
+    t = w.reshape(n // 16, 16, k // 64, 2, 4, 8)  # [nb, r, sg, half, g, e]
+    return PackedWeight(t.permute(0, 2, 3, 4, 1, 5).contiguous().view(-1), n, k)
+
+
+def dense_gemm(x: torch.Tensor, w: PackedWeight, mode: int = GEMM_BF16, *, col_tiles: int = 4, waves: int = 4,
+               parts: int = 1):
+    """x [M, K] @ w^T on the weight-streaming gfx950 kernel (M <= 64), w packed
+    by pack_weight.
+
+    mode GEMM_BF16: bf16 [M, N].  GEMM_PARTS: PartialSums of a K split over
+    `parts` ([P, M, N] fp32).  GEMM_SILU_MUL: w is the gate/up weight [2I, K]
+    (gate rows first) and the result is bf16 silu(x w_gate^T) * (x w_up^T),
+    [M, I], the two products rounded to bf16 first as the unfused GEMM stores
+    them.  col_tiles x 16 weight rows per wave (1, 2 or 4; even for
+    GEMM_SILU_MUL), `waves` (4 or 8) waves per workgroup over the same K.
+    Raises on shapes or layouts the kernel does not take."""
+    from .. import _C
+    from .._torch_glue import ptr, require_bf16, require_cuda, stream_of
+
+    require_cuda(x)
+    require_bf16(x)
+    require_bf16(w.data)
+    m, k = x.shape
+    n = w.n
+    if x.stride(1) != 1:
+        raise ValueError("dense_gemm: x needs unit stride along K")
+    if w.k != k:
+        raise ValueError(f"dense_gemm: x {tuple(x.shape)} and w [{w.n}, {w.k}] disagree on K")
+    if mode == GEMM_PARTS:
+        out = torch.empty((parts, m, n), dtype=torch.float32, device=x.device)
+        os_, ps = n, m * n
+    else:
+        out = torch.empty((m, n // 2 if mode == GEMM_SILU_MUL else n), dtype=torch.bfloat16, device=x.device)
+        os_, ps = out.shape[1], 0
+    _C.check(
+        _C.lib().xv_dense_gemm(ptr(x), x.stride(0), ptr(w.data), ptr(out), os_, ps, m, n, k, mode, col_tiles, waves,
+                               parts, stream_of(x)),
+        "xv_dense_gemm",
+    )
+    return PartialSums(out) if mode == GEMM_PARTS else out
+
+
+# Decode batches up to this many rows take the weight-streaming kernel when
+# the model holds packed weights (pack_decode_weights); larger batches and
+# prefill stay on hipBLASLt over the [N, K] weights.
+STREAM_MAX_ROWS = 64
+
+
+def stream_parts(k: int) -> int:
+    """K slices of a split-K streamed GEMM (the most of 8, 4, 2, 1 that cut K
+    into whole 4-step rounds)."""
+    for p in (8, 4, 2, 1):
+        if k % (p * 256) == 0:
+            return p
+    return 0
+
+
+def streamable(w: torch.Tensor, mode: int) -> bool:
+    """Whether w [N, K] fits the shapes the streamed decode GEMMs use:
+    gate/up + SiLU with 2 tiles x 4 waves (2I % 128), split-K partials with
+    1 tile x 8 waves (N % 128)."""
+    n, k = w.shape
+    if mode == GEMM_SILU_MUL:
+        return n % 128 == 0 and k % 256 == 0
+    return n % 128 == 0 and stream_parts(k) > 0
+
+
+def streamed_silu_mul(x: torch.Tensor, w: PackedWeight) -> torch.Tensor:
+    """silu(x w_gate^T) * (x w_up^T) of a decode batch, bf16 [M, I]."""
+    return dense_gemm(x, w, GEMM_SILU_MUL, col_tiles=2, waves=4)
+
+
+def streamed_into_norm(x: torch.Tensor, w: PackedWeight) -> PartialSums:
+    """x @ w^T of a decode batch as split-K PartialSums for the next residual
+    add + RMSNorm: P = 4 up to 32 rows, else up to 8 (measured fastest)."""
+    p = stream_parts(w.k)
+    if x.shape[0] <= 32:
+        p = min(p, 4)
+    return dense_gemm(x, w, GEMM_PARTS, col_tiles=1, waves=8, parts=p)

@@ -47,7 +47,8 @@ class ModelRunner:
     def __init__(self, model, kv: KVPool, sampler: Sampler | None = None, *, max_num_seqs: int = 256,
                  max_num_batched_tokens: int = 8192, context_len: int = 4096, device=None,
                  enforce_eager: bool = False, sample_modes: tuple[int, ...] = (), cascade_groups: int = 0,
-                 cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16) -> None:
+                 cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16,
+                 stream_decode_gemms: bool = True) -> None:
         """`sample_modes`: sampling modes (see `sample_mode`) whose decode
         sampler graphs are recorded up front besides the all-greedy one;
         other modes are recorded at their first use.
@@ -55,8 +56,15 @@ class ModelRunner:
         whose block tables share leading pages (a prefix cache's shared
         blocks) and read those pages once per group (cascade decode);
         cascade_max_prefix_blocks bounds the shared blocks per group (default:
-        the whole table) and sizes the prefix pass."""
+        the whole table) and sizes the prefix pass.
+        `stream_decode_gemms`: pack the model's gate_up / down / o weights
+        (model.pack_decode_weights) so that decode batches of at most 64 rows
+        run them on the weight-streaming kernel; the weights must be final.
+        Packed copies an earlier runner made are kept either way (its graphs
+        read them), and every runner of the model then uses them."""
         self.model = model
+        if stream_decode_gemms and hasattr(model, "pack_decode_weights"):
+            model.pack_decode_weights()
         self.kv = kv
         self.sampler = sampler or Sampler()
         self.generator: torch.Generator | None = None  # source of the sampler's uniform draws

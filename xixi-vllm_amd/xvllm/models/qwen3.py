@@ -4,9 +4,13 @@ reference's tp=1, pp=1 case of src/compute/models/qwen3.py:44-238).
 Per layer: input RMSNorm (fused with the residual add after layer 0), fused
 qkv GEMM, per-head q/k RMSNorm + NeoX RoPE (one kernel, `xv::qk_norm_rope`),
 `vllm::attention` (KV store + paged decode / prefill), o GEMM, fused add +
-RMSNorm, gate_up GEMM, SiLU-and-mul, down GEMM.  GEMMs stay on PyTorch
-(hipBLASLt).  Weights are plain tensors (random init for the benchmarks; the
-reference's checkpoint loader is out of scope).
+RMSNorm, gate_up GEMM, SiLU-and-mul, down GEMM.  GEMMs run on PyTorch
+(hipBLASLt), except at decode batch sizes (at most 64 rows) once
+pack_decode_weights has made packed copies of gate_up, down and o: then the
+gate_up GEMM + SiLU-and-mul is one weight-streaming kernel, and down and o
+are streamed as split-K partials into the next norm.  Weights are plain
+tensors (random init for the benchmarks; the reference's checkpoint loader is
+out of scope).
 """
 from __future__ import annotations
 
@@ -18,7 +22,8 @@ from ..config import head_dim as _head_dim
 from ..config import rope_theta as _rope_theta
 from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
 from ..layers.attention import kv_cache_of, kv_scales
-from ..layers.linear import linear_into_norm
+from ..layers.linear import (GEMM_PARTS, GEMM_SILU_MUL, STREAM_MAX_ROWS, linear_into_norm, pack_weight,
+                             streamable, streamed_into_norm, streamed_silu_mul)
 from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
 
@@ -29,12 +34,22 @@ class Qwen3MLP(nn.Module):
         self.gate_up_proj = nn.Parameter(torch.empty(2 * inter, hidden))  # [gate; up] (linear.py:297-304)
         self.down_proj = nn.Parameter(torch.empty(hidden, inter))
         self.split_k = True
+        self.packed = None  # (gate_up, down) PackedWeights for decode batches
 
     def forward(self, x):
         """SiLU-MLP; the down GEMM may return PartialSums (split-K) for the
         next residual add + RMSNorm."""
+        if self.packed is not None and self.split_k and x.shape[0] <= STREAM_MAX_ROWS and x.stride(1) == 1:
+            return streamed_into_norm(streamed_silu_mul(x, self.packed[0]), self.packed[1])
         return linear_into_norm(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj,
                                 self.split_k)
+
+    def pack(self, enabled: bool = True):
+        if not enabled:
+            self.packed = None
+        elif self.packed is None and streamable(self.gate_up_proj, GEMM_SILU_MUL) and streamable(self.down_proj,
+                                                                                                   GEMM_PARTS):
+            self.packed = (pack_weight(self.gate_up_proj.data), pack_weight(self.down_proj.data))
 
 
 class Qwen3Attention(nn.Module):
@@ -53,6 +68,7 @@ class Qwen3Attention(nn.Module):
         self.attn = Attention(self.num_heads, self.head_dim, self.num_kv_heads, layer_id=layer_id)
         self.eps = cfg.rms_norm_eps
         self.split_k = True
+        self.packed_o = None  # o_proj PackedWeight for decode batches
 
     def forward(self, positions, hidden, attn: AttnInputs):
         """qkv -> q/k norm + RoPE -> attention -> o GEMM (PartialSums when
@@ -65,7 +81,15 @@ class Qwen3Attention(nn.Module):
         else:
             q, k, v = self._split_norm_rope(positions, qkv)
             o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
+        if self.packed_o is not None and self.split_k and o.shape[0] <= STREAM_MAX_ROWS and o.stride(1) == 1:
+            return streamed_into_norm(o, self.packed_o)
         return linear_into_norm(o, self.o_proj, self.split_k)
+
+    def pack(self, enabled: bool = True):
+        if not enabled:
+            self.packed_o = None
+        elif self.packed_o is None and streamable(self.o_proj, GEMM_PARTS):
+            self.packed_o = pack_weight(self.o_proj.data)
 
     def _views(self, qkv):
         t = qkv.shape[0]
@@ -143,6 +167,20 @@ class Qwen3ForCausalLM(nn.Module):
         for m in self.modules():
             if isinstance(m, (Qwen3Attention, Qwen3MLP)):
                 m.split_k = enabled
+        return self
+
+    @torch.no_grad()
+    def pack_decode_weights(self, enabled: bool = True):
+        """Packed copies of every layer's gate_up, down and o weights for the
+        weight-streaming decode GEMMs; layers that have them keep them (the
+        graphs captured over them stay valid).  enabled=False drops them: only
+        when no captured graph still uses them.  Call once the weights are
+        final: the copies do not follow later writes.  They
+        add (2 I H + I H + H Hq D) x 2 bytes per layer to the weights
+        (Qwen3-8B: 335 MB per layer, 12 GB)."""
+        for m in self.modules():
+            if isinstance(m, (Qwen3Attention, Qwen3MLP)):
+                m.pack(enabled)
         return self
 
     def compute_logits(self, hidden):
