@@ -256,7 +256,8 @@ def copy_ceiling_us(torch, dev, nbytes: int) -> float:
 
 def kernel_suite(torch, dev) -> dict:
     """Config 3 (fused elementwise/reduction set at Qwen3-8B width over 8192
-    tokens) and the sampler, each against its algorithmic HBM bytes."""
+    tokens), the sampler and the streamed decode GEMMs, each against its
+    algorithmic HBM bytes."""
     import xvllm.layers.ops  # noqa: F401
     from xvllm.kv_ops import store_kvcache
     from xvllm.layers.rotary import build_cos_sin_cache
@@ -344,6 +345,34 @@ def kernel_suite(torch, dev) -> dict:
     u = torch.rand(bsz, generator=g, device=dev)
     rec("sampler_p0.95_flat_B32", _time(torch, lambda: sample(logits, temps, tps, None, None, u, use_top_p=True), 20),
         bsz * V * 2)
+    # Decode GEMMs on the weight-streaming kernel (packed weights, 6 weight
+    # sets cycled: 0.2-1.2 GB, past the MALL) against hipBLASLt over the [N, K]
+    # weights (the unsplit GEMM + SiLU-and-mul kernel for gate_up, the split-K
+    # bmm it replaced for down / o).  Bytes: weights + x + output.
+    from xvllm.layers.linear import pack_weight, split_k_views, streamed_into_norm, streamed_silu_mul
+    import torch.nn.functional as F
+    for name, n, k in (("gate_up_silu", 2 * I, H), ("down_parts", H, I), ("o_parts", H, HQ_ * D_)):
+        ws = [rnd(n, k) for _ in range(6)]
+        pws = [pack_weight(w_) for w_ in ws]
+        for m in (8, 64):
+            x = rnd(m, k)
+            if name == "gate_up_silu":
+                fn = lambda r, x=x: streamed_silu_mul(x, pws[r % 6])
+                ref = lambda r, x=x: torch.ops.vllm.silu_and_mul(F.linear(x, ws[r % 6]))
+                ob = m * n // 2 * 2
+            else:
+                p = streamed_into_norm(x, pws[0]).parts.shape[0]
+                fn = lambda r, x=x: streamed_into_norm(x, pws[r % 6])
+                ref = lambda r, x=x, p=p: torch.bmm(*split_k_views(x, ws[r % 6], p), out_dtype=torch.float32)
+                ob = p * m * n * 4
+            for tag, f in (("", fn), ("_hipblaslt", ref)):
+                it = [0]
+
+                def step(f=f):
+                    f(it[0])
+                    it[0] += 1
+                rec(f"decode_gemm_{name}_M{m}{tag}", _time(torch, step), n * k * 2 + m * k * 2 + ob)
+        del ws, pws
     return out
 
 
