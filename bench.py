@@ -345,25 +345,27 @@ def kernel_suite(torch, dev) -> dict:
     u = torch.rand(bsz, generator=g, device=dev)
     rec("sampler_p0.95_flat_B32", _time(torch, lambda: sample(logits, temps, tps, None, None, u, use_top_p=True), 20),
         bsz * V * 2)
-    # Decode GEMMs on the weight-streaming kernel (packed weights, 6 weight
-    # sets cycled: 0.2-1.2 GB, past the MALL) against hipBLASLt over the [N, K]
+    # Decode GEMMs on the weight-streaming kernel (packed weights, enough
+    # weight sets cycled to pass 600 MB: past the 256 MB MALL, as the model's
+    # 15 GB of weights are) against hipBLASLt over the [N, K]
     # weights (the unsplit GEMM + SiLU-and-mul kernel for gate_up, the split-K
     # bmm it replaced for down / o).  Bytes: weights + x + output.
     from xvllm.layers.linear import pack_weight, split_k_views, streamed_into_norm, streamed_silu_mul
     import torch.nn.functional as F
     for name, n, k in (("gate_up_silu", 2 * I, H), ("down_parts", H, I), ("o_parts", H, HQ_ * D_)):
-        ws = [rnd(n, k) for _ in range(6)]
+        nset = max(2, -(-600_000_000 // (n * k * 2)))
+        ws = [rnd(n, k) for _ in range(nset)]
         pws = [pack_weight(w_) for w_ in ws]
         for m in (8, 64):
             x = rnd(m, k)
             if name == "gate_up_silu":
-                fn = lambda r, x=x: streamed_silu_mul(x, pws[r % 6])
-                ref = lambda r, x=x: torch.ops.vllm.silu_and_mul(F.linear(x, ws[r % 6]))
+                fn = lambda r, x=x: streamed_silu_mul(x, pws[r % nset])
+                ref = lambda r, x=x: torch.ops.vllm.silu_and_mul(F.linear(x, ws[r % nset]))
                 ob = m * n // 2 * 2
             else:
                 p = streamed_into_norm(x, pws[0]).parts.shape[0]
-                fn = lambda r, x=x: streamed_into_norm(x, pws[r % 6])
-                ref = lambda r, x=x, p=p: torch.bmm(*split_k_views(x, ws[r % 6], p), out_dtype=torch.float32)
+                fn = lambda r, x=x: streamed_into_norm(x, pws[r % nset])
+                ref = lambda r, x=x, p=p: torch.bmm(*split_k_views(x, ws[r % nset], p), out_dtype=torch.float32)
                 ob = p * m * n * 4
             for tag, f in (("", fn), ("_hipblaslt", ref)):
                 it = [0]

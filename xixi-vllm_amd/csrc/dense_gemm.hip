@@ -25,7 +25,9 @@
 // registers; both feed v_mfma_f32_16x16x32_bf16 as 8-element operands in the
 // K placement above.  The products are summed over K in another order than a
 // K-ordered loop, the same 64 per step.  Three steps are in flight while one
-// is multiplied.  Sharing x through LDS keeps its L2 traffic at
+// is multiplied.  Weights are read with non-temporal loads (each is read once
+// per decode step; the Qwen3-8B step ran 8.31 ms against 8.42 with plain
+// loads).  Sharing x through LDS keeps its L2 traffic at
 // M / (16 NT WAVES) of the weight bytes: read from L2 by every wave, x cost
 // more than the weights themselves at M 64.
 // The epilogue writes each wave's tiles in one of three forms:
@@ -115,7 +117,7 @@ __global__ __launch_bounds__(WAVES * 64) void dense_gemm_kernel(GemmArgs a) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       const bf16x8_t* q = reinterpret_cast<const bf16x8_t*>(wp[t] + (int64_t)sc * 1024);
-      wreg[u][t] = Frag{q[0], q[64]};
+      wreg[u][t] = Frag{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 64)};  // read once per step
     }
 #pragma unroll
     for (int o = 0; o < kXOps; ++o)
