@@ -170,6 +170,14 @@ def streamable(w: torch.Tensor, mode: int) -> bool:
     return n % 128 == 0 and stream_parts(k) > 0
 
 
+def stream_rows(x: torch.Tensor) -> bool:
+    """Whether activations x [M, K] can take a streamed decode GEMM: at most
+    STREAM_MAX_ROWS rows, unit stride along K, 16-byte aligned rows (other
+    layouts stay on hipBLASLt)."""
+    return (0 < x.shape[0] <= STREAM_MAX_ROWS and x.stride(1) == 1 and x.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0)
+
+
 def streamed_silu_mul(x: torch.Tensor, w: PackedWeight) -> torch.Tensor:
     """silu(x w_gate^T) * (x w_up^T) of a decode batch, bf16 [M, I]."""
     return dense_gemm(x, w, GEMM_SILU_MUL, col_tiles=2, waves=4)

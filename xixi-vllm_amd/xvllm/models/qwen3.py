@@ -22,8 +22,8 @@ from ..config import head_dim as _head_dim
 from ..config import rope_theta as _rope_theta
 from ..layers import Attention, AttnInputs, RMSNorm, RotaryEmbedding
 from ..layers.attention import kv_cache_of, kv_scales
-from ..layers.linear import (GEMM_PARTS, GEMM_SILU_MUL, STREAM_MAX_ROWS, linear_into_norm, pack_weight,
-                             streamable, streamed_into_norm, streamed_silu_mul)
+from ..layers.linear import (GEMM_PARTS, GEMM_SILU_MUL, linear_into_norm, pack_weight, stream_rows, streamable,
+                             streamed_into_norm, streamed_silu_mul)
 from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
 
@@ -39,7 +39,7 @@ class Qwen3MLP(nn.Module):
     def forward(self, x):
         """SiLU-MLP; the down GEMM may return PartialSums (split-K) for the
         next residual add + RMSNorm."""
-        if self.packed is not None and self.split_k and x.shape[0] <= STREAM_MAX_ROWS and x.stride(1) == 1:
+        if self.packed is not None and self.split_k and stream_rows(x):
             return streamed_into_norm(streamed_silu_mul(x, self.packed[0]), self.packed[1])
         return linear_into_norm(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj,
                                 self.split_k)
@@ -81,7 +81,7 @@ class Qwen3Attention(nn.Module):
         else:
             q, k, v = self._split_norm_rope(positions, qkv)
             o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
-        if self.packed_o is not None and self.split_k and o.shape[0] <= STREAM_MAX_ROWS and o.stride(1) == 1:
+        if self.packed_o is not None and self.split_k and stream_rows(o):
             return streamed_into_norm(o, self.packed_o)
         return linear_into_norm(o, self.o_proj, self.split_k)
 
