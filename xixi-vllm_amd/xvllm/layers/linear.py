@@ -1,7 +1,13 @@
-"""Dense GEMMs of the decoder on PyTorch (hipBLASLt), and a split-K form for
+"""Dense GEMMs of the decoder: PyTorch (hipBLASLt) with a split-K form for
 the two whose output goes straight into a residual add + RMSNorm (o_proj and
 down_proj, reference src/compute/models/qwen3.py:64,115 feeding the norms of
-:150,:152).
+:150,:152), and, for decode batches of at most 64 rows, the weight-streaming
+gfx950 kernel (xv_dense_gemm) over packed weight tiles: gate_up fused with
+SiLU-and-mul, down and o as split-K partials for the same norm (dense_gemm
+and the streamed_* helpers at the end of this file; measured 8-26 % faster
+than the hipBLASLt forms below at M 8 and 64, weights streamed from HBM).
+The split-K measurements below are the hipBLASLt path, which larger batches
+and models without packed weights still take.
 
 At decode batch sizes an [M, K] x [K, 4096] GEMM has few output tiles for 256
 CUs: hipBLASLt runs Qwen3-8B's o_proj (K 4096) and down_proj (K 12288) at
