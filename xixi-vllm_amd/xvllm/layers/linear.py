@@ -4,7 +4,7 @@ down_proj, reference src/compute/models/qwen3.py:64,115 feeding the norms of
 :150,:152), and, for decode batches of at most 64 rows, the weight-streaming
 gfx950 kernel (xv_dense_gemm) over packed weight tiles: gate_up fused with
 SiLU-and-mul, down and o as split-K partials for the same norm (dense_gemm
-and the streamed_* helpers at the end of this file; measured 8-26 % faster
+and the streamed_* helpers at the end of this file; measured 11-27 % faster
 than the hipBLASLt forms below at M 8 and 64, weights streamed from HBM).
 The split-K measurements below are the hipBLASLt path, which larger batches
 and models without packed weights still take.
