@@ -379,11 +379,13 @@ def kernel_suite(torch, dev) -> dict:
 
 
 def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = False, fp8: bool = False,
-               model=None):
+               model=None, stream_gemms: bool = False):
     """Qwen3-8B (36 layers, random bf16 weights ~N(0,0.02)) decode step at the
     given per-sequence contexts: hipGraph replay of the decode body + LM head +
     sampler, steady state (metadata staged once).  fp8: the KV pool in the
-    optional fp8 (e4m3fn) page format.  Returns (record, model)."""
+    optional fp8 (e4m3fn) page format.  stream_gemms: the runner's opt-in
+    weight-streaming decode GEMMs (packed copies of gate_up / down / o beside
+    the weights; their bytes are reported).  Returns (record, model)."""
     from xvllm.batch import SeqSchedule
     from xvllm.config import QWEN3_8B
     from xvllm.kv_pool import KVPool
@@ -414,7 +416,8 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     else:
         kv.kv_cache.normal_()
     max_ctx = max(ctx) + 1
-    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=max_ctx, device=dev)
+    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=max_ctx, device=dev,
+                         stream_decode_gemms=stream_gemms)
     g = torch.Generator().manual_seed(11)
     perm = torch.randperm(pool, generator=g).tolist()
     seqs, o = [], 0
@@ -445,67 +448,69 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
     roof_ms = (wbytes + kvbytes) / (HBM_PEAK_GBS * 1e9) * 1e3
     runner.destroy()
     del kv, runner
+    packed = model.packed_decode_bytes() if stream_gemms else 0
+    if stream_gemms:
+        model.pack_decode_weights(False)  # the runner's graphs are gone: drop the packed copies
     assert ids.shape[0] == bsz
     return {"batch": bsz, "mean_ctx": round(sum(ctx) / bsz, 1), "sampling": "T0.7/k50/p0.9" if sampled else "greedy",
             "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
+            "dense_gemms": ("weight-streaming kernel at <= 64 rows (opt-in), packed weight copies of "
+                            f"{packed} B beside the weights") if stream_gemms else "PyTorch / hipBLASLt",
             "ms_per_step": round(ms, 4), "tok_per_s": round(bsz / (ms * 1e-3), 1),
             "roofline_ms": round(roof_ms, 4), "roofline_tok_per_s": round(bsz / (roof_ms * 1e-3), 1),
             "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}, model
 
 
-def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bool = True, model=None,
-                   fp8: bool = False):
+def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int = 8, cascade: bool = False,
+                   model=None, fp8: bool = False):
     """Config 5: Qwen3-32B-shaped decode (64 layers, hidden 5120, 64 q / 8 kv
     heads, FFN 25600, random bf16 weights ~N(0,0.02)), batch 32 at context
-    32768; 16 requests share an 8192-token prefix, 16 are independent; top-p
-    0.95 over the 151936 vocab with seeded draws.  The requests' pages come
-    from a radix prefix cache (xvllm.prefix_cache): the first shared request
-    publishes its blocks, the other 15 match the 512 prefix blocks and reuse
-    their pages.  With `cascade` the decode reads those pages once per kv head
-    (shared-prefix pass + per-row suffix, merged by log-sum-exp); without it
-    every row streams its whole table.
+    32768; 16 requests share an 8192-token random-token prefix, 16 are
+    independent; top-p 0.95 (T 1.0) over the 151936 vocab with seeded draws.
+
+    The run goes through xvllm.serving.serve: its page ledger admits the 32
+    prompts in order, and the radix prefix cache hands the 15 later shared
+    requests the 512 prefix pages the first one published, so the timed
+    decode steps read shared pages that came from the cache.  The prompts'
+    prefill (32 x 32k tokens through 64 layers) is not run: the pool holds
+    synthetic N(0,1) K/V (`serve(prefilled=True)`), and each request decodes
+    from its last prompt token.  The timed region is `steps` whole serving
+    steps (decode graph + LM head + sampler graphs, read-back of the ids, the
+    ledger's bookkeeping) after `warmup` steps.
     The 64 layers' KV (275 GB per sequence, 243 GB of unique pages) does not
     fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
     layer i reads pool layer i % pool_layers: every layer streams the same
     bytes in the same pattern as with a full pool (what this leaves out: the
-    real memory footprint and the TLB reach of 243 GB).  fp8: the pool in the
-    optional fp8 (e4m3fn) page format, plain or cascade decode."""
-    from xvllm.batch import SeqSchedule
+    real memory footprint and the TLB reach of 243 GB).  cascade: the runner
+    reads the shared pages once per group (cascade decode).  fp8: the pool in
+    the optional fp8 (e4m3fn) page format."""
     from xvllm.config import QWEN3_32B
     from xvllm.kv_pool import KVPool
     from xvllm.model_runner import ModelRunner
     from xvllm.models import Qwen3ForCausalLM
-    from xvllm.prefix_cache import RadixPrefixCache
+    from xvllm.serving import serve
 
     cfg = QWEN3_32B
     bsz, ctx, prefix, shared = 32, 32768, 8192, 16
+    gen = warmup + steps
     npg, ppg = ctx // PAGE, prefix // PAGE
-    unique = ppg + shared * (npg - ppg) + (bsz - shared) * npg
     g = torch.Generator().manual_seed(55)
     pre_toks = torch.randint(0, cfg.vocab_size, (prefix,), generator=g).tolist()
-    cache = RadixPrefixCache(PAGE)
-    free = torch.randperm(unique, generator=g).tolist()
-    tables, hits = [], 0
+    prompts = []
     for i in range(bsz):
         own = torch.randint(0, cfg.vocab_size, (ctx - (prefix if i < shared else 0),), generator=g).tolist()
-        toks = (pre_toks + own) if i < shared else own
-        hit = cache.match(toks)
-        hits += len(hit)
-        bt = hit + [free.pop() for _ in range(npg - len(hit))]
-        held, _ = cache.insert(toks, bt)
-        assert held == bt[: len(held)]
-        tables.append((bt, toks[-1]))
-    assert hits == (shared - 1) * ppg and not free
+        prompts.append((pre_toks + own) if i < shared else own)
+    pages = bsz * ((ctx + gen + PAGE - 1) // PAGE) + 16
     torch.set_default_dtype(torch.bfloat16)
     try:
         with torch.device(dev):
             if model is None:
                 model = Qwen3ForCausalLM(cfg).random_init_(seed=0).set_split_k(SPLIT_K)
             if fp8:
-                kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.float8_e4m3fn,
+                kv = KVPool(cfg, num_blocks=pages, block_size=PAGE, device=dev, dtype=torch.float8_e4m3fn,
                             num_layers=pool_layers, k_scale=FP8_SCALE, v_scale=FP8_SCALE)
             else:
-                kv = KVPool(cfg, num_blocks=unique, block_size=PAGE, device=dev, dtype=torch.bfloat16,
+                kv = KVPool(cfg, num_blocks=pages, block_size=PAGE, device=dev, dtype=torch.bfloat16,
                             num_layers=pool_layers)
     finally:
         torch.set_default_dtype(torch.float32)
@@ -517,45 +522,41 @@ def decode_config5(torch, dev, steps: int = 8, pool_layers: int = 8, cascade: bo
     else:
         kv.kv_cache.normal_()
     casc = dict(cascade_groups=2, cascade_max_prefix_blocks=ppg, cascade_min_blocks=64) if cascade else {}
-    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx, device=dev, **casc)
+    runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx + gen, device=dev,
+                         sample_modes=(4,), **casc)
     runner.generator = torch.Generator(device=dev).manual_seed(5)
-    seqs = [SeqSchedule(seq_id=i, token_ids=[tok], num_cached_tokens=ctx - 1, block_table=bt, temperature=1.0,
-                        top_p=0.95) for i, (bt, tok) in enumerate(tables)]
-    runner.batch.build_decode(seqs, pad_to=runner.graph_runner._pad_bs(bsz))
+    seen = {}
+
+    def after_forward(r, n_p, n_d):
+        seen["cascade_rows"] = getattr(r.batch, "cascade_rows", 0)
+
+    outs, st = serve(runner, prompts, gen, sampling=dict(temperature=1.0, top_p=0.95), max_num_seqs=bsz,
+                     prefilled=True, after_forward=after_forward)
+    runner.destroy()
+    assert st.hit_tokens == (shared - 1) * prefix, st.hit_tokens
+    assert all(len(o) == gen for o in outs) and st.steps == gen
     if cascade:
-        assert runner.batch.cascade_rows == shared
-
-    def step():
-        runner.decode_hidden(bsz)
-        return runner.decode_sample(bsz)
-
-    for _ in range(2):
-        step()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        ids = step()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+        assert seen["cascade_rows"] == shared
+    t = st.step_end_s
+    ms = (t[-1] - t[warmup - 1]) / steps * 1e3
     wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
     per_tok_layer = cfg.num_key_value_heads * 128 * 2 * (1 if fp8 else 2)
-    kv_seq = bsz * ctx * cfg.num_hidden_layers * per_tok_layer
-    kv_unique = unique * PAGE * cfg.num_hidden_layers * per_tok_layer
+    mean_ctx = ctx + warmup + (steps + 1) / 2  # contexts of the timed steps (prompt + tokens so far)
+    kv_seq = int(bsz * mean_ctx * cfg.num_hidden_layers * per_tok_layer)
+    unique_tok = bsz * mean_ctx - (shared - 1) * prefix
+    kv_unique = int(unique_tok * cfg.num_hidden_layers * per_tok_layer)
     kv_read = kv_unique if cascade else kv_seq  # per-step KV bytes the decode streams
     roof_ms = (wbytes + kv_read) / (HBM_PEAK_GBS * 1e9) * 1e3
-    runner.destroy()
-    assert ids.shape[0] == bsz
     del kv
     torch.cuda.empty_cache()
     return {"model": "Qwen3-32B-shaped (64 layers, 64q/8kv, FFN 25600)", "batch": bsz, "context": ctx,
-            "shared_prefix": f"{shared} requests x {prefix} tokens (radix prefix cache)",
+            "shared_prefix": f"{shared} requests x {prefix} tokens; {st.hit_tokens} prompt tokens' pages handed out "
+                             "by the serving ledger's radix prefix cache",
             "attention": "cascade (shared blocks read once per kv head)" if cascade else "plain paged decode",
-            "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
-            "sampling": "top-p 0.95 (T 1.0)", "kv_pool_layers": pool_layers, "ms_per_step": round(ms, 3),
-            "tok_per_s": round(bsz / (ms * 1e-3), 1), "weight_bytes": wbytes, "kv_bytes_per_seq": kv_seq,
-            "kv_bytes_unique_pages": kv_unique, "kv_bytes_read_per_step": kv_read,
+            "kv_pages": "fp8 e4m3fn" if fp8 else "bf16", "path": "xvllm.serving.serve(prefilled=True)",
+            "sampling": "top-p 0.95 (T 1.0)", "kv_pool_layers": pool_layers, "timed_steps": steps,
+            "ms_per_step": round(ms, 3), "tok_per_s": round(bsz / (ms * 1e-3), 1), "weight_bytes": wbytes,
+            "kv_bytes_per_seq": kv_seq, "kv_bytes_unique_pages": kv_unique, "kv_bytes_read_per_step": kv_read,
             "roofline_ms": round(roof_ms, 3), "frac_of_roofline": round(roof_ms / ms, 4),
             "achieved_GB/s": round((wbytes + kv_read) / (ms * 1e-3) / 1e9, 1)}, model
 
@@ -624,6 +625,35 @@ def cascade_sweep(torch, dev, iters: int = 10) -> dict:
     return out
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def serving_roofline(cfg, st, wbytes: int, kv_elem: int = 2) -> dict:
+    """Roofline time of a serving run, step by step: each step reads the
+    weights once and its decode rows' KV (Sum ctx x L x Hkv x D x 2 x kv_elem
+    bytes) against 8 TB/s, plus its prefill flops (the layer GEMMs'
+    2 x params per token, causal attention's 4 x Hq x D x L per query-key
+    pair, the LM head's 2 x V x H per sampled prompt) against the 2.5 PFLOP/s
+    dense bf16 MFMA peak; summed over the steps."""
+    h, hq, hkv, d, ffn, layers = (cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, 128,
+                                  cfg.intermediate_size, cfg.num_hidden_layers)
+    layer_params = h * (hq + 2 * hkv) * d + hq * d * h + 3 * h * ffn
+    gemm_per_tok = 2 * layer_params * layers
+    attn_per_pair = 4 * hq * d * layers
+    lm_per_row = 2 * cfg.vocab_size * h
+    kv_tok = layers * hkv * d * 2 * kv_elem
+    t_bytes = t_flops = 0.0
+    for n_d, ctx_sum, n_pt, pairs, n_ps in st.step_work:
+        t_bytes += (wbytes + ctx_sum * kv_tok) / (HBM_PEAK_GBS * 1e9)
+        t_flops += (n_pt * gemm_per_tok + pairs * attn_per_pair + n_ps * lm_per_row) / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    roof = t_bytes + t_flops
+    dec = [w for w in st.step_work if w[0]]
+    return {"roofline_s": round(roof, 4), "roofline_hbm_s": round(t_bytes, 4), "roofline_mfma_s": round(t_flops, 4),
+            "frac_of_roofline": round(roof / st.wall_s, 4),
+            "mean_decode_ctx": round(sum(w[1] for w in dec) / max(1, sum(w[0] for w in dec)), 1),
+            "roofline_rule": "sum over steps of (weights + decode KV bytes) / 8 TB/s + prefill flops / 2.5 PFLOP/s"}
+
+
 def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, seed: int = 0,
               max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, model=None, fp8: bool = False) -> dict:
     """Config 4: Qwen3-8B (random bf16 weights ~N(0,0.02)) serving 256 requests
@@ -670,6 +700,8 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
     torch.cuda.empty_cache()
     out_tokens = sum(len(o) for o in outs)
     assert out_tokens == n_req * gen
+    wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
+    roof = serving_roofline(cfg, st, wbytes, kv_elem=1 if fp8 else 2)
     return {"requests": n_req, "prompt_tokens": sum(plens), "generated_tokens": out_tokens, "steps": st.steps,
             "sampling": "T0.7/k50/p0.9" if sampled else "greedy", "kv_pages": "fp8 e4m3fn" if fp8 else "bf16",
             "wall_s": round(st.wall_s, 3),
@@ -677,7 +709,9 @@ def serve_e2e(torch, dev, *, sampled: bool, n_req: int = 256, gen: int = 256, se
             "total_tok_per_s": round((out_tokens + sum(plens)) / st.wall_s, 1),
             "host_s_before_sync": round(st.host_s, 3),
             "mean_decode_batch": round(st.decode_tokens / max(1, st.steps), 1),
-            "policy": "decode-first mixed, 8192-token budget, max 256 seqs, 16-token pages"}, model
+            "prefix_cache_hit_tokens": st.hit_tokens, **roof,
+            "roofline_output_tok_per_s": round(out_tokens / roof["roofline_s"], 1),
+            "policy": "decode-first mixed, 8192-token budget, max 256 seqs, 16-token pages, radix prefix cache"}, model
 
 
 def cpu_baseline(ctx_all: list[int], budget_s: float = 12.0) -> dict:
@@ -813,7 +847,9 @@ def main() -> int:
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill attention cases")
     ap.add_argument("--no-serve", action="store_true", help="skip config 4 (256 requests, greedy and sampled)")
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
-    ap.add_argument("--config5", action="store_true", help="also run config 5 (Qwen3-32B-shaped long-context decode)")
+    ap.add_argument("--config5", action="store_true",
+                    help="also run config 5's cascade and fp8-page variants (plain bf16 config 5 runs by default)")
+    ap.add_argument("--no-config5", action="store_true", help="skip config 5 (Qwen3-32B-shaped long-context decode)")
     ap.add_argument("--config5-only", action="store_true", help="only config 5 (for profiling)")
     ap.add_argument("--cascade-only", action="store_true",
                     help="only the shared-prefix sweep: plain against cascade decode attention")
@@ -961,14 +997,17 @@ def main() -> int:
         line["decode_tok_per_s"] = line["decode_e2e"]["tok_per_s"]
         # the same step on an fp8 (e4m3fn) KV pool, the pool's optional page format
         line["decode_e2e_fp8"], model = decode_e2e(torch, dev, ctx, fp8=True, model=model)
+        # the opt-in weight-streaming decode GEMMs (12.1 GB of packed weights beside the 16.4 GB of weights)
+        line["decode_e2e_streamed_gemms"], model = decode_e2e(torch, dev, ctx, model=model, stream_gemms=True)
         del model
         torch.cuda.empty_cache()
-    if args.config5:
+    if not args.no_config5:
         torch.cuda.empty_cache()
         line["config5"], model = decode_config5(torch, dev, cascade=False)
-        line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
-        line["config5_fp8"], model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
-        line["config5_cascade_fp8"], model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
+        if args.config5:
+            line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
+            line["config5_fp8"], model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
+            line["config5_cascade_fp8"], model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
         del model
         torch.cuda.empty_cache()
     if not args.no_serve:

@@ -133,6 +133,53 @@ def test_config1_single_layer_decode(dev):
     assert np.array_equal(ids.cpu().numpy()[sure], np.argmax(logits_r, axis=1)[sure])
 
 
+@pytest.mark.parametrize("m", [1, 5, 17, 64])
+def test_config1_streamed_post_attention(dev, m):
+    """The weight-streaming decode GEMMs (packed o, gate_up + SiLU, down as
+    split-K partials into the norms) on the config-1 layer, every element
+    against the oracle's post-attention block on the same inputs, at decode
+    batches 1, 5, 17 and 64; and an in-place weight write after packing
+    raises instead of reading the stale packed copy."""
+    from xvllm.config import Qwen3Shape
+    from xvllm.layers.linear import PartialSums
+    from xvllm.models.qwen3 import Qwen3DecoderLayer, StalePackedWeights
+
+    _, _, w, _, _, _, _, _ = _layer_case(seed=m)
+    g = gen(100 + m)
+    attn = randn_bf16((m, HQ * D), g)
+    hidden = randn_bf16((m, HIDDEN), g)
+    cfg = Qwen3Shape(HIDDEN, HQ, HKV, D, FFN, 1, max_position_embeddings=4096)
+    with torch.device(dev):
+        layer = Qwen3DecoderLayer(cfg, 0).to(torch.bfloat16)
+    with torch.no_grad():
+        layer.self_attn.o_proj.copy_(w["o_proj"])
+        layer.mlp.gate_up_proj.copy_(w["gate_up_proj"])
+        layer.mlp.down_proj.copy_(w["down_proj"])
+        layer.post_attention_layernorm.weight.copy_(w["post_attention_layernorm"])
+    layer.self_attn.pack()
+    layer.mlp.pack()
+    assert layer.self_attn.packed_o is not None and layer.mlp.packed is not None
+    from xvllm.layers.linear import streamed_into_norm
+
+    with torch.no_grad():
+        a, res = attn.to(dev), hidden.to(dev).clone()
+        o = streamed_into_norm(a, layer.self_attn.packed_o)
+        assert isinstance(o, PartialSums)
+        x, res = layer.post_attention_layernorm(o, res)
+        h = layer.mlp(x)
+        assert isinstance(h, PartialSums), "the MLP did not take the streamed path"
+        h = h.materialize()
+    torch.cuda.synchronize()
+    wn = {k2: f32(v2) for k2, v2 in w.items()}
+    h_ref, r_ref = OM.post_attention(wn, f32(attn), f32(hidden), EPS)
+    _close(f32(res), r_ref)
+    _close(f32(h), h_ref)
+    with torch.no_grad():
+        layer.mlp.down_proj.mul_(1.0)  # an in-place write after packing
+        with pytest.raises(StalePackedWeights):
+            layer.mlp(x)
+
+
 def test_decode_graph_replay_matches_eager(dev):
     """A 2-layer random Qwen3-0.6B-shaped model: hipGraph replays of the decode
     body (several, with eager work and new metadata in between) equal eager runs."""

@@ -151,3 +151,51 @@ def test_config4_reduced_serving_fp8_pool(dev):
     samp = dict(temperature=0.7, top_p=0.9, top_k=50)
     s1, _ = _serve(dev, model, kv, prompts, gen, samp, 7, check=True)
     assert all(0 <= t < V for o in s1 + greedy1 for t in o)
+
+
+def test_reduced_serving_prefix_cache_reuses_pages(dev):
+    """Serving with the radix prefix cache on prompts that share prefixes
+    (reduced config 4): requests admitted after a shared prefix was published
+    reuse its pages and prefill only the rest (chunked prefill over the cached
+    pages).  Right after such a request's prefill, the K/V its block table
+    holds for every prompt position equals a fresh whole-prompt prefill into
+    spare pages, per element at the attention tolerance; greedy ids are
+    reproducible and every page ledger invariant holds after every step."""
+    from xvllm.batch import SeqSchedule
+    from xvllm.model_runner import ModelRunner
+    from xvllm.serving import serve
+
+    model, kv = _model(dev, seed=11, num_blocks=1024)
+    g = torch.Generator().manual_seed(77)
+    shared = [torch.randint(0, V, (int(n),), generator=g).tolist() for n in (160, 200, 97)]
+    prompts = []
+    for i in range(18):
+        own = torch.randint(0, V, (int(torch.randint(1, 120, (1,), generator=g)),), generator=g).tolist()
+        prompts.append(shared[i % 3] + own)
+    gen, ledger_pages, spare = 12, 512, list(range(512, 1024))
+    runner = ModelRunner(model, kv, max_num_seqs=16, max_num_batched_tokens=512, context_len=512, device=dev)
+    checked = []
+
+    def after_step(kvm, live):
+        kvm.check({r.rid: r.bt for r in live})
+        for r in live:
+            if r.hit and r.cached >= len(r.prompt) and r.rid not in [c[0] for c in checked]:
+                n = len(r.prompt)
+                sbt = spare[: (n + 15) // 16]
+                runner.run_forward([], [SeqSchedule(10_000 + r.rid, r.prompt, 0, sbt)])
+                runner.read_samples(1, 0)
+                torch.cuda.synchronize()
+                pos = torch.arange(n)
+                a = kv.kv_cache[:, :, torch.tensor(r.bt)[pos // 16], pos % 16].float().cpu().numpy()
+                b = kv.kv_cache[:, :, torch.tensor(sbt)[pos // 16], pos % 16].float().cpu().numpy()
+                bad = np.abs(a - b) > 2e-2 + 2e-2 * np.abs(b)
+                assert not bad.any(), f"request {r.rid} (hit {r.hit} of {n}): {bad.sum()} K/V elements differ"
+                checked.append((r.rid, r.hit))
+
+    outs1, st = serve(runner, prompts, gen, num_pages=ledger_pages, max_num_seqs=16, max_num_batched_tokens=512,
+                      after_step=after_step)
+    outs2, _ = serve(runner, prompts, gen, num_pages=ledger_pages, max_num_seqs=16, max_num_batched_tokens=512)
+    runner.destroy()
+    assert outs1 == outs2, "greedy serving with the prefix cache is not reproducible"
+    assert st.hit_tokens > 0 and st.prefill_tokens + st.hit_tokens == sum(len(p) for p in prompts)
+    assert len(checked) >= 3, checked

@@ -103,7 +103,7 @@ def test_split_k_decode_step_matches_unsplit(dev):
     finally:
         torch.set_default_dtype(torch.float32)
     kv.kv_cache.normal_()
-    runner = ModelRunner(model, kv, max_num_seqs=64, context_len=1024, device=dev)
+    runner = ModelRunner(model, kv, max_num_seqs=64, context_len=1024, device=dev, stream_decode_gemms=True)
     g = gen(23)
     perm = torch.randperm(64 * 40, generator=g).tolist()
     seqs, o = [], 0

@@ -510,15 +510,7 @@ XV_INLINE void process_page(SplitState& st, const char* buf, const LaneOffsets& 
   } else {
     read_page<kPageOps<false> * (NB - 1)>(pr, buf, lo);
   }
-#ifdef XV_NO_MATH
-  // timing probe: consume the operands without the MFMA/softmax work
-  float acc = 0.f;
-  for (int j = 0; j < 4; ++j) acc += (float)pr.kr[j][0];
-  for (int n = 0; n < 8; ++n) acc += (float)pr.vt[n][0];
-  st.l += acc;
-#else
   page_math<G>(st, pr, qb, page_tok0, ctx, scale_log2, lane);
-#endif
 }
 
 // Stream positions per half of the page-id table.
@@ -630,6 +622,7 @@ XV_INLINE void read_q(bf16x8_t (&qb)[4], const char* slot, int lane) {
 template <int G>
 XV_INLINE void finish_segment(const DecodeArgs& a, const SplitState& st, int b, int kvh, bool full, int part,
                               int lane, char* stage) {
+  static_assert(G * kD * 2 <= kQSlot<G>, "the q slot stages the segment's G bf16 output rows");
   const int i = lane & 15, g = lane >> 4;
   // total p-sum of head c%G over the four rows
   const float lsum = xor32_sum(xor16_sum(st.l));

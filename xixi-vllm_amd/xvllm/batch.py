@@ -144,6 +144,13 @@ class Batch:
             n = len(seqs)
             self.block_tables[:n].copy_(self._h_bt[:n], non_blocking=True)
 
+    def forget_rows(self) -> None:
+        """Drop the record of which sequence's table each host row holds, so
+        that the next build writes every row whole (a new run may reuse a
+        sequence id with another table)."""
+        self._row_sid[:] = -1
+        self._row_len[:] = -1
+
     def _check_pages(self, seq_id: int, pages: np.ndarray) -> None:
         if self.num_blocks is not None and pages.size and (pages.min() < 0 or pages.max() >= self.num_blocks):
             raise ValueError(f"sequence {seq_id}: page id outside [0, {self.num_blocks}) in its block table")

@@ -137,6 +137,9 @@ def dense_gemm(x: torch.Tensor, w: PackedWeight, mode: int = GEMM_BF16, *, col_t
         raise ValueError("dense_gemm: x needs unit stride along K")
     if w.k != k:
         raise ValueError(f"dense_gemm: x {tuple(x.shape)} and w [{w.n}, {w.k}] disagree on K")
+    if w.data.numel() != w.n * w.k or not w.data.is_contiguous() or w.n % 16 or w.k % 64:
+        raise ValueError(f"dense_gemm: packed weight holds {w.data.numel()} elements "
+                         f"(contiguous: {w.data.is_contiguous()}), not whole 16 x 64 tiles of [{w.n}, {w.k}]")
     if mode == GEMM_PARTS:
         out = torch.empty((parts, m, n), dtype=torch.float32, device=x.device)
         os_, ps = n, m * n
@@ -151,9 +154,10 @@ def dense_gemm(x: torch.Tensor, w: PackedWeight, mode: int = GEMM_BF16, *, col_t
     return PartialSums(out) if mode == GEMM_PARTS else out
 
 
-# Decode batches up to this many rows take the weight-streaming kernel when
-# the model holds packed weights (pack_decode_weights); larger batches and
-# prefill stay on hipBLASLt over the [N, K] weights.
+# Batches of up to this many rows take the weight-streaming kernel when the
+# model holds packed weights (pack_decode_weights): decode batches, and also
+# prefill chunks this short (the same products); larger batches stay on
+# hipBLASLt over the [N, K] weights.
 STREAM_MAX_ROWS = 64
 
 

@@ -48,7 +48,7 @@ class ModelRunner:
                  max_num_batched_tokens: int = 8192, context_len: int = 4096, device=None,
                  enforce_eager: bool = False, sample_modes: tuple[int, ...] = (), cascade_groups: int = 0,
                  cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16,
-                 stream_decode_gemms: bool = True) -> None:
+                 stream_decode_gemms: bool = False) -> None:
         """`sample_modes`: sampling modes (see `sample_mode`) whose decode
         sampler graphs are recorded up front besides the all-greedy one;
         other modes are recorded at their first use.
@@ -57,9 +57,13 @@ class ModelRunner:
         blocks) and read those pages once per group (cascade decode);
         cascade_max_prefix_blocks bounds the shared blocks per group (default:
         the whole table) and sizes the prefix pass.
-        `stream_decode_gemms`: pack the model's gate_up / down / o weights
+        `stream_decode_gemms` (off by default: the dense GEMMs stay on
+        PyTorch / hipBLASLt): pack the model's gate_up / down / o weights
         (model.pack_decode_weights) so that decode batches of at most 64 rows
         run them on the weight-streaming kernel; the weights must be final.
+        The packed copies take model.packed_decode_bytes() of device memory
+        (Qwen3-8B: 12.1 GB) beside the weights, which a KV pool sized before
+        this runner does not see: size it with that figure as reserve_bytes.
         Packed copies an earlier runner made are kept either way (its graphs
         read them), and every runner of the model then uses them."""
         self.model = model

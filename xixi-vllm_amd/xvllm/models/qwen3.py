@@ -28,6 +28,26 @@ from ..layers import ops as _ops  # noqa: F401  (registers the custom ops)
 from ..sampler import sample
 
 
+class StalePackedWeights(RuntimeError):
+    """A weight was written or replaced after pack_decode_weights copied it:
+    the streamed decode GEMMs would read the old values."""
+
+
+def _weight_stamp(*params) -> tuple:
+    return tuple((p._version, p.data_ptr()) for p in params)
+
+
+def _check_stamp(module, stamp: tuple, *params) -> None:
+    """Raise when a packed weight's source changed since it was packed
+    (in-place writes through the Parameter bump its version; assigning a new
+    tensor moves its data pointer).  Writes through `.data` bypass the version
+    counter and are not seen."""
+    if _weight_stamp(*params) != stamp:
+        raise StalePackedWeights(f"{type(module).__name__}: weights changed after pack_decode_weights; "
+                                 "call model.pack_decode_weights(False) then pack_decode_weights() again "
+                                 "(outside graph capture; re-capture the decode graphs)")
+
+
 class Qwen3MLP(nn.Module):
     def __init__(self, hidden: int, inter: int):
         super().__init__()
@@ -40,6 +60,7 @@ class Qwen3MLP(nn.Module):
         """SiLU-MLP; the down GEMM may return PartialSums (split-K) for the
         next residual add + RMSNorm."""
         if self.packed is not None and self.split_k and stream_rows(x):
+            _check_stamp(self, self._stamp, self.gate_up_proj, self.down_proj)
             return streamed_into_norm(streamed_silu_mul(x, self.packed[0]), self.packed[1])
         return linear_into_norm(torch.ops.vllm.silu_and_mul(F.linear(x, self.gate_up_proj)), self.down_proj,
                                 self.split_k)
@@ -50,6 +71,7 @@ class Qwen3MLP(nn.Module):
         elif self.packed is None and streamable(self.gate_up_proj, GEMM_SILU_MUL) and streamable(self.down_proj,
                                                                                                    GEMM_PARTS):
             self.packed = (pack_weight(self.gate_up_proj.data), pack_weight(self.down_proj.data))
+            self._stamp = _weight_stamp(self.gate_up_proj, self.down_proj)
 
 
 class Qwen3Attention(nn.Module):
@@ -82,6 +104,7 @@ class Qwen3Attention(nn.Module):
             q, k, v = self._split_norm_rope(positions, qkv)
             o = self.attn(q.view(q.shape[0], self.q_size), k, v, attn)
         if self.packed_o is not None and self.split_k and stream_rows(o):
+            _check_stamp(self, self._stamp, self.o_proj)
             return streamed_into_norm(o, self.packed_o)
         return linear_into_norm(o, self.o_proj, self.split_k)
 
@@ -90,6 +113,7 @@ class Qwen3Attention(nn.Module):
             self.packed_o = None
         elif self.packed_o is None and streamable(self.o_proj, GEMM_PARTS):
             self.packed_o = pack_weight(self.o_proj.data)
+            self._stamp = _weight_stamp(self.o_proj)
 
     def _views(self, qkv):
         t = qkv.shape[0]
@@ -175,13 +199,28 @@ class Qwen3ForCausalLM(nn.Module):
         weight-streaming decode GEMMs; layers that have them keep them (the
         graphs captured over them stay valid).  enabled=False drops them: only
         when no captured graph still uses them.  Call once the weights are
-        final: the copies do not follow later writes.  They
-        add (2 I H + I H + H Hq D) x 2 bytes per layer to the weights
-        (Qwen3-8B: 335 MB per layer, 12 GB)."""
+        final: the copies do not follow later writes (an eager forward raises
+        StalePackedWeights when a packed weight was written in place or
+        replaced since).  They add packed_decode_bytes() to the weights,
+        (2 I H + I H + H Hq D) x 2 bytes per layer (Qwen3-8B: 335 MB per
+        layer, 12.1 GB; the Qwen3-32B shape: 56 GB): size the KV pool after
+        packing, or pass that figure as KVPool.auto_num_blocks' reserve_bytes."""
         for m in self.modules():
             if isinstance(m, (Qwen3Attention, Qwen3MLP)):
                 m.pack(enabled)
         return self
+
+    def packed_decode_bytes(self) -> int:
+        """Bytes pack_decode_weights adds (counted for the layers whose
+        weights the streamed GEMMs take)."""
+        total = 0
+        for m in self.modules():
+            if isinstance(m, Qwen3MLP) and streamable(m.gate_up_proj, GEMM_SILU_MUL) and streamable(m.down_proj,
+                                                                                                  GEMM_PARTS):
+                total += (m.gate_up_proj.numel() + m.down_proj.numel()) * m.gate_up_proj.element_size()
+            elif isinstance(m, Qwen3Attention) and streamable(m.o_proj, GEMM_PARTS):
+                total += m.o_proj.numel() * m.o_proj.element_size()
+        return total
 
     def compute_logits(self, hidden):
         return F.linear(hidden, self.lm_head)

@@ -17,6 +17,7 @@ them.
 """
 from __future__ import annotations
 
+import heapq
 import time
 from dataclasses import dataclass, field
 
@@ -92,7 +93,11 @@ class RadixPrefixCache:
         n_blocks = max(0, (len(tokens) - 1) // self.block_size)
         if n_blocks == 0:
             return []
-        pages, _, _ = self._walk(chain_hashes(tokens, self.block_size, n_blocks), touch=True)
+        return self.match_hashes(chain_hashes(tokens, self.block_size, n_blocks))
+
+    def match_hashes(self, hashes: list[int]) -> list[int]:
+        """Page ids of the longest cached prefix of a block-hash chain."""
+        pages, _, _ = self._walk(hashes, touch=True)
         return pages
 
     # ------------------------------------------------------------ insert
@@ -113,7 +118,11 @@ class RadixPrefixCache:
         the deepest node): where the tree already caches a block, its page
         replaces the sequence's (the caller frees the duplicate)."""
         n_blocks = len(tokens) // self.block_size
-        hashes = chain_hashes(tokens, self.block_size, n_blocks)
+        return self.insert_hashes(chain_hashes(tokens, self.block_size, n_blocks), pages)
+
+    def insert_hashes(self, hashes: list[int], pages) -> tuple[list[int], "_Node"]:
+        """insert() over the blocks' chain hashes (one per page of `pages`)."""
+        n_blocks = len(hashes)
         node, i, out = self.root, 0, []
         now = time.monotonic()
         while i < n_blocks:
@@ -140,7 +149,12 @@ class RadixPrefixCache:
     def node_of(self, tokens) -> _Node:
         """The node a sequence with these (cached) tokens pins."""
         n_blocks = len(tokens) // self.block_size
-        _, node, n = self._walk(chain_hashes(tokens, self.block_size, n_blocks), touch=False)
+        return self.node_of_hashes(chain_hashes(tokens, self.block_size, n_blocks))
+
+    def node_of_hashes(self, hashes: list[int]) -> _Node:
+        """The node that ends the cached path of `hashes` (split there if the
+        path ends inside an edge); the root when nothing matches."""
+        _, node, n = self._walk(hashes, touch=False)
         if node is not self.root and n < len(node.key):
             node = self._split(node, n)
         return node
@@ -159,20 +173,36 @@ class RadixPrefixCache:
     def cached_pages(self) -> set[int]:
         return set(self._page_node)
 
+    def holds(self, page: int) -> bool:
+        return page in self._page_node
+
     # ------------------------------------------------------------ eviction
     def evict(self, n_pages: int) -> list[int]:
-        """Free unpinned leaves, least recently used first, until n_pages
-        pages are returned (or nothing more can go)."""
+        """Free unpinned leaves, least recently used first, a whole leaf at a
+        time, until n_pages pages are returned (or nothing more can go); a
+        parent left without children becomes a candidate in turn."""
         freed: list[int] = []
-        while len(freed) < n_pages:
-            leaves = [n for n in self._page_node.values() if not n.children and n.refs == 0]
-            if not leaves:
-                break
-            leaf = min(leaves, key=lambda n: n.last_use)
+        if n_pages <= 0:
+            return freed
+        heap, stack, seq = [], [self.root], 0
+        while stack:  # the tree's nodes, not its pages: a walk per call
+            n = stack.pop()
+            if n.children:
+                stack.extend(n.children.values())
+            elif n is not self.root and n.refs == 0:
+                heap.append((n.last_use, seq, n))
+                seq += 1
+        heapq.heapify(heap)
+        while len(freed) < n_pages and heap:
+            _, _, leaf = heapq.heappop(heap)
             freed.extend(leaf.pages)
             for p in leaf.pages:
                 del self._page_node[p]
-            del leaf.parent.children[leaf.key[0]]
+            parent = leaf.parent
+            del parent.children[leaf.key[0]]
+            if parent is not self.root and not parent.children and parent.refs == 0:
+                heapq.heappush(heap, (parent.last_use, seq, parent))
+                seq += 1
         return freed
 
 

@@ -1,17 +1,25 @@
 """Continuous batching over one ModelRunner on one GPU: the default step
 policy of the reference scheduler (src/control/scheduler.py:58-154) reduced
-to what drives the decode hot path.
+to what drives the decode hot path, over the page ledger and radix prefix
+cache of xvllm.kv_manager (src/data/kv.py:15-119).
 
 Each step, every running sequence decodes one token (its last sampled one);
 the rest of the token budget goes to prefill chunks of waiting prompts in
 arrival order, at most one of them partial, and a step that has no decode
 rows takes no trailing partial chunk.  A prompt's pages are taken when it is
-admitted, a decode page when its first token is written.  Generation stops
+admitted (reusing the pages of its longest cached full-block prefix, whose
+tokens are then not prefilled again), a decode page when its first token is
+written.  After each step the blocks it filled are published to the prefix
+cache (sync_prefix, scheduler.py:185); a finished sequence publishes and
+releases its pages (scheduler.py:194-205), the published ones staying cached
+for later prompts until a fresh allocation evicts them.  Generation stops
 after `gen` tokens per request (EOS is not checked).  Every id the runner
 reads back is range-checked on the host before it is fed back.
 
-This is the measurement driver of config 4, not the reference's
-Scheduler/KVManager: no preemption, no prefix cache, no stop strings.
+This is the measurement driver of configs 4 and 5, not the reference's
+Scheduler: no preemption and no stop strings.  The pool must hold the pages
+of the max_num_seqs largest requests (checked up front): a prompt that does
+not fit yet waits for running requests to finish, and none is ever preempted.
 """
 from __future__ import annotations
 
@@ -23,15 +31,23 @@ from typing import Callable
 import torch
 
 from .batch import SeqSchedule
+from .kv_manager import KVManager
 
 
-@dataclass
+@dataclass(eq=False)
 class Request:
     rid: int
     prompt: list[int]
-    out: list[int] = field(default_factory=list)
+    tokens: list[int] = field(default_factory=list)   # prompt + generated tokens
     bt: list[int] = field(default_factory=list)
     cached: int = 0
+    hit: int = 0                 # prompt tokens whose KV came from the prefix cache
+    admitted: bool = False
+    finished: bool = False
+
+    @property
+    def out(self) -> list[int]:
+        return self.tokens[len(self.prompt):]
 
 
 @dataclass
@@ -39,54 +55,96 @@ class ServeStats:
     steps: int = 0
     decode_tokens: int = 0
     prefill_tokens: int = 0
+    hit_tokens: int = 0          # prompt tokens served from the prefix cache
     host_s: float = 0.0
     wall_s: float = 0.0
+    step_end_s: list[float] = field(default_factory=list)  # end of each step since the start
+    # per step: (decode rows, sum of their context lengths incl. the new token,
+    # prefill tokens, prefill attention query-key pairs under the causal mask,
+    # prefill rows sampled)
+    step_work: list[tuple[int, int, int, int, int]] = field(default_factory=list)
 
 
 def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None = None,
           max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, num_pages: int | None = None,
-          after_forward: Callable[[object, int, int], None] | None = None) -> tuple[list[list[int]], ServeStats]:
+          prefix_cache: bool = True, prefilled: bool = False, kv_manager: KVManager | None = None,
+          after_forward: Callable[[object, int, int], None] | None = None,
+          after_step: Callable[[KVManager, list[Request]], None] | None = None
+          ) -> tuple[list[list[int]], ServeStats]:
     """Generate `gen` tokens for every prompt; returns (outputs, stats).
 
     sampling: SeqSchedule fields shared by every request (temperature,
     top_p, top_k, min_p); greedy when None.  num_pages: pages of the pool
-    handed out (default: all of the runner's pool).  after_forward(runner,
-    n_prefill, n_decode) runs after each step's launches, before its ids are
-    read back (tests use it to check the step on the device)."""
+    handed out (default: all of the runner's pool).  prefix_cache: reuse
+    cached prompt prefixes (the page ledger's radix cache); kv_manager: a
+    ledger to use (and keep) instead of a new one.
+    prefilled: the pool already holds the KV of every prompt token but the
+    last (synthetic pages for a long-context decode measurement, whose prefill
+    would dominate the run): admission allocates and matches pages as usual
+    and publishes the prompt's full blocks at once, and each request starts
+    decoding from its last prompt token; the first generated token comes from
+    that decode step.
+    after_forward(runner, n_prefill, n_decode) runs after each step's
+    launches, before its ids are read back (tests use it to check the step on
+    the device); after_step(ledger, live requests) after each step's
+    bookkeeping."""
     samp = dict(sampling or {"temperature": 0.0})
     page = runner.block_size
     pool = runner.kv.num_blocks if num_pages is None else num_pages
-    need_pages = sum((len(p) + gen + page - 1) // page for p in prompts)
-    if need_pages > pool:
-        raise ValueError(f"the requests need {need_pages} pages, the pool holds {pool}")
-    free = list(range(pool))[::-1]
-    reqs = [Request(i, list(p)) for i, p in enumerate(prompts)]
+    kvm = kv_manager or KVManager(pool, page, prefix_cache=prefix_cache)
+    if kvm.num_pages > runner.kv.num_blocks:
+        raise ValueError(f"the ledger hands out {kvm.num_pages} pages, the pool holds {runner.kv.num_blocks}")
+    # at most max_num_seqs requests hold pages at once, and every page no live
+    # request holds is free or reclaimable: admission may wait, never deadlock
+    demand = sorted(((len(p) + gen + page - 1) // page for p in prompts), reverse=True)
+    if sum(demand[:max_num_seqs]) > kvm.num_pages:
+        raise ValueError(f"{min(max_num_seqs, len(prompts))} live requests may need {sum(demand[:max_num_seqs])} "
+                         f"pages, the ledger holds {kvm.num_pages}")
+    runner.batch.forget_rows()  # block-table rows staged by an earlier run are not this run's
+    reqs = [Request(i, list(p), list(p)) for i, p in enumerate(prompts)]
     waiting = deque(reqs)
     running: deque = deque()
     st = ServeStats()
+
+    def admit(r: Request) -> bool:
+        got = kvm.allocate(r.rid, r.prompt)
+        if got is None:
+            return False
+        r.bt, r.cached = got
+        r.hit = r.cached
+        r.admitted = True
+        st.hit_tokens += r.cached
+        if prefilled:
+            r.cached = len(r.prompt) - 1
+            kvm.publish(r.rid, r.tokens, r.bt, r.cached)
+        return True
+
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     while waiting or running:
         h0 = time.perf_counter()
+        if prefilled:  # admitted requests go straight to decoding
+            while waiting and len(running) < max_num_seqs and admit(waiting[0]):
+                running.append(waiting.popleft())
         decodes, dreqs = [], []
-        for r in running:  # one token per running sequence (its last sampled token)
+        for r in running:  # one token per running sequence (its last token)
             if len(decodes) >= max_num_seqs:
                 break
             pos = r.cached
             if pos // page >= len(r.bt):
-                r.bt.append(free.pop())
-            decodes.append(SeqSchedule(r.rid, [r.out[-1]], pos, r.bt, **samp))
+                r.bt.append(kvm.append_page(r.rid))
+            decodes.append(SeqSchedule(r.rid, [r.tokens[-1]], pos, r.bt, **samp))
             dreqs.append(r)
         used = len(decodes)
         prefills, preqs = [], []
-        for r in list(waiting):
+        for r in [] if prefilled else list(waiting):
             if len(decodes) + len(prefills) >= max_num_seqs:
                 break
             remaining = max_num_batched_tokens - used
             if remaining <= 0:
                 break
-            if not r.bt:  # all of the prompt's pages at admission (the reference allocates at _try_alloc)
-                r.bt = [free.pop() for _ in range((len(r.prompt) + page - 1) // page)]
+            if not r.admitted and not admit(r):  # pages at admission (the reference's _try_alloc)
+                break
             need = len(r.prompt) - r.cached
             if remaining < need and prefills and not decodes:
                 break  # prefill-first steps take no trailing partial chunk
@@ -98,6 +156,11 @@ def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None =
             used += chunk
             if not done:
                 break  # at most one partial chunk per step
+        if not decodes and not prefills:
+            raise RuntimeError("no request can be scheduled (the pool cannot hold the next prompt)")
+        pairs = sum(c * r.cached + c * (c + 1) // 2 for r, c, _ in preqs)
+        st.step_work.append((len(decodes), sum(r.cached + 1 for r in dreqs), used - len(decodes), pairs,
+                             sum(1 for _, _, done in preqs if done)))
         n_p, n_d = runner.run_forward(decodes, prefills)
         if after_forward is not None:
             after_forward(runner, len(prefills), len(decodes))
@@ -107,17 +170,27 @@ def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None =
         st.decode_tokens += len(decodes)
         for r, tok in zip(dreqs, d_ids):
             r.cached += 1
-            r.out.append(tok)
+            r.tokens.append(tok)
         for (r, chunk, done), tok in zip(preqs, p_ids):
             r.cached += chunk
             st.prefill_tokens += chunk
             if done:
-                r.out.append(tok)
+                r.tokens.append(tok)
                 waiting.remove(r)
                 running.append(r)
-        for r in [r for r in running if len(r.out) >= gen]:
+        for r in dreqs:
+            if r.cached // page > kvm.published_blocks(r.rid):
+                kvm.publish(r.rid, r.tokens, r.bt, r.cached)
+        for r, _, _ in preqs:
+            if r.cached // page > kvm.published_blocks(r.rid):
+                kvm.publish(r.rid, r.tokens, r.bt, r.cached)
+        for r in [r for r in running if len(r.tokens) - len(r.prompt) >= gen]:
             running.remove(r)
-            free.extend(r.bt)
+            r.finished = True
+            kvm.deallocate(r.rid, r.tokens, r.bt, r.cached)
+        if after_step is not None:
+            after_step(kvm, [r for r in reqs if r.admitted and not r.finished])
+        st.step_end_s.append(time.perf_counter() - t0)
     torch.cuda.synchronize()
     st.wall_s = time.perf_counter() - t0
     return [r.out for r in reqs], st
