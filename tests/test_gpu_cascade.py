@@ -244,7 +244,9 @@ def test_cascade_decode_graphs_match_eager(dev, kv_dtype):
     else:
         kv.kv_cache.normal_()
     casc = ModelRunner(model, kv, max_num_seqs=16, context_len=1024, device=dev, cascade_groups=2,
-                       cascade_max_prefix_blocks=32, cascade_min_blocks=4)
+                       cascade_max_prefix_blocks=32, cascade_min_blocks=4, cascade_min_shared_bytes=0)
+    gated = ModelRunner(model, kv, max_num_seqs=16, context_len=1024, device=dev, cascade_groups=2,
+                        cascade_max_prefix_blocks=32, cascade_min_blocks=4)
     plain = ModelRunner(model, kv, max_num_seqs=16, context_len=1024, device=dev)
     g = gen(17)
     for step, (bs, shared) in enumerate(((9, 6), (4, 0), (13, 6))):
@@ -259,8 +261,11 @@ def test_cascade_decode_graphs_match_eager(dev, kv_dtype):
             seqs.append(SeqSchedule(seq_id=100 * step + i, token_ids=[int(torch.randint(0, 4096, (1,), generator=g))],
                                     num_cached_tokens=c - 1, block_table=btab))
         snap = kv.kv_cache.clone()
+        # the default gate: 12 shared blocks are far below the bytes where the cascade pays
+        gated.batch.build_decode(seqs, pad_to=gated.graph_runner._pad_bs(bs))
+        assert gated.batch.cascade_rows == 0 and not gated._use_cascade()
         casc.batch.build_decode(seqs, pad_to=casc.graph_runner._pad_bs(bs))
-        assert casc.batch.cascade_rows == shared
+        assert casc.batch.cascade_rows == shared and casc._use_cascade() == (shared > 0)
         h_graph = casc.decode_hidden(bs).clone()
         torch.cuda.synchronize()
         kv.kv_cache.copy_(snap)
@@ -278,4 +283,5 @@ def test_cascade_decode_graphs_match_eager(dev, kv_dtype):
         hg, hp = f32(h_graph).astype(np.float64), f32(h_plain).astype(np.float64)
         assert np.linalg.norm(hg - hp) / np.linalg.norm(hp) < 1e-2, step
     casc.destroy()
+    gated.destroy()
     plain.destroy()

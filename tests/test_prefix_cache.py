@@ -125,3 +125,30 @@ def test_cascade_groups_keep_the_largest_and_pad_the_records():
     pre, info, rows = cascade_groups(bt, sl, 16, max_rows=16, min_blocks=1, max_groups=4, max_prefix_blocks=2)
     assert info.tolist() == [[0, 3, 0, 32], [3, 2, 3, 32], [0, 0, 0, 0], [0, 0, 0, 0]]
     assert pre.tolist() == [32] * 5 + [0]
+
+
+def test_cascade_gate_takes_the_cascade_only_past_the_measured_bytes():
+    """Batch decode builds stage shared-prefix groups only when they share at
+    least the gate's bytes of KV per layer; below it the batch runs plain."""
+    import torch
+
+    from xvllm.batch import Batch, SeqSchedule
+    from xvllm.prefix_cache import CASCADE_MIN_SHARED_BYTES, cascade_pays
+
+    tok_bytes = 8 * 128 * 2 * 2  # Qwen3 kv heads x head dim x (K, V) x bf16
+    shared = [list(range(0, 32))]
+    info = np.array([[0, 4, 0, 32 * 16], [0, 0, 0, 0]], np.int32)
+    assert not cascade_pays(info, tok_bytes)
+    big = np.array([[0, 4, 0, 8192 * 2], [0, 3, 4, 8192]], np.int32)
+    assert cascade_pays(big, tok_bytes)  # 24576 tokens x 4 KB = 100 MB
+    assert not cascade_pays(np.zeros((2, 4), np.int32), tok_bytes, 0)
+    assert CASCADE_MIN_SHARED_BYTES == 64 << 20
+    for gate, want in ((None, 0), (0, 4)):
+        b = Batch(max_bs=8, max_tokens=64, max_blocks=64, vocab_size=100, device=torch.device("cpu"), block_size=16,
+                  num_blocks=512, cascade_groups=2, cascade_min_blocks=4, cascade_token_bytes=tok_bytes,
+                  cascade_min_shared_bytes=gate)
+        seqs = [SeqSchedule(i, [1], 40 * 16 - 1, shared[0] + list(range(100 + 10 * i, 108 + 10 * i)))
+                for i in range(4)]
+        b.build_decode(seqs)
+        assert b.cascade_rows == want
+        assert int(b.cascade.prefix_tokens[:4].sum()) == (4 * 32 * 16 if want else 0)

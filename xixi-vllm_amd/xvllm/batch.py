@@ -50,14 +50,18 @@ class Batch:
     def __init__(self, *, max_bs: int, max_tokens: int, max_blocks: int, vocab_size: int,
                  device: torch.device, block_size: int, num_blocks: int | None = None,
                  cascade_groups: int = 0, cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16,
-                 cascade_max_rows: int = 16) -> None:
+                 cascade_max_rows: int = 16, cascade_token_bytes: int = 0,
+                 cascade_min_shared_bytes: int | None = None) -> None:
         """`num_blocks`: pages in the KV pool; when given, every page id and
         slot staged for the device is checked against it on the host (a bad
         one raises ValueError instead of reaching a kernel).
         `cascade_groups` > 0: decode builds also stage the batch's
         shared-prefix groups (at most that many, of at most cascade_max_rows
         rows, prefixes of cascade_min_blocks .. cascade_max_prefix_blocks
-        blocks) for the cascade decode."""
+        blocks) for the cascade decode, when they share at least
+        cascade_min_shared_bytes of KV per layer (prefix tokens x
+        cascade_token_bytes; default prefix_cache.CASCADE_MIN_SHARED_BYTES);
+        otherwise the build stages no groups and cascade_rows is 0."""
         self.num_blocks = num_blocks
         self.max_bs, self.max_tokens, self.max_blocks = max_bs, max_tokens, max_blocks
         self.vocab_size, self.device, self.block_size = vocab_size, device, block_size
@@ -101,13 +105,17 @@ class Batch:
         self.cascade = None
         self._casc_cfg = (cascade_groups, cascade_max_prefix_blocks or max_blocks, cascade_min_blocks,
                           cascade_max_rows)
+        from .prefix_cache import CASCADE_MIN_SHARED_BYTES
+
+        self._casc_gate = (cascade_token_bytes, CASCADE_MIN_SHARED_BYTES if cascade_min_shared_bytes is None
+                           else cascade_min_shared_bytes)
+        self.cascade_rows = 0  # rows in shared-prefix groups in the last decode build
         if cascade_groups > 0:
             from .layers.attention import CascadePlan
 
             self.cascade = CascadePlan(gpu((max_bs,), torch.int32), gpu((cascade_groups, 4), torch.int32),
                                        gpu((max_bs,), torch.int32), cascade_groups, self._casc_cfg[1])
             self._h_casc = _pinned((2 * max_bs + 4 * cascade_groups,), torch.int32, pin=pin)
-            self.cascade_rows = 0  # rows in shared-prefix groups in the last decode build
 
     def _wait_staging(self) -> None:
         if self._h2d_pending:
@@ -216,11 +224,13 @@ class Batch:
         self._staged()
 
     def _stage_cascade(self, n: int, seqlens: np.ndarray, rows: int) -> None:
-        from .prefix_cache import cascade_groups
+        from .prefix_cache import cascade_groups, cascade_pays
 
         groups, max_pre, min_blocks, max_rows = self._casc_cfg
         pre, info, grp_rows = cascade_groups(self._bt_np[:n], seqlens, self.block_size, max_rows=max_rows,
                                              min_blocks=min_blocks, max_groups=groups, max_prefix_blocks=max_pre)
+        if len(grp_rows) and not cascade_pays(info, *self._casc_gate):
+            pre[:], info[:], grp_rows = 0, 0, grp_rows[:0]  # the plain decode is faster for this batch
         h = self._h_casc.numpy()
         mb, ng = self.max_bs, len(grp_rows)
         h[:rows] = 0

@@ -15,6 +15,7 @@ import torch
 
 from . import _C
 from .batch import Batch, SeqSchedule
+from .config import head_dim as _head_dim
 from .cuda_graph import HipGraphRunner
 from .kv_pool import KVPool
 from .layers.attention import AttnInputs, AttnMetadata, attention_context
@@ -48,7 +49,7 @@ class ModelRunner:
                  max_num_batched_tokens: int = 8192, context_len: int = 4096, device=None,
                  enforce_eager: bool = False, sample_modes: tuple[int, ...] = (), cascade_groups: int = 0,
                  cascade_max_prefix_blocks: int = 0, cascade_min_blocks: int = 16,
-                 stream_decode_gemms: bool = False) -> None:
+                 cascade_min_shared_bytes: int | None = None, stream_decode_gemms: bool = False) -> None:
         """`sample_modes`: sampling modes (see `sample_mode`) whose decode
         sampler graphs are recorded up front besides the all-greedy one;
         other modes are recorded at their first use.
@@ -56,7 +57,12 @@ class ModelRunner:
         whose block tables share leading pages (a prefix cache's shared
         blocks) and read those pages once per group (cascade decode);
         cascade_max_prefix_blocks bounds the shared blocks per group (default:
-        the whole table) and sizes the prefix pass.
+        the whole table) and sizes the prefix pass.  A step takes the cascade
+        only when its groups share at least cascade_min_shared_bytes of KV
+        per layer (default prefix_cache.CASCADE_MIN_SHARED_BYTES, the measured
+        point below which the plain decode is faster); the runner records a
+        plain and a cascade decode graph per bucket and replays the one the
+        staged batch selects.
         `stream_decode_gemms` (off by default: the dense GEMMs stay on
         PyTorch / hipBLASLt): pack the model's gate_up / down / o weights
         (model.pack_decode_weights) so that decode batches of at most 64 rows
@@ -88,7 +94,9 @@ class ModelRunner:
                            max_blocks=max_blocks, vocab_size=cfg.vocab_size, device=self.device,
                            block_size=self.block_size, num_blocks=kv.num_blocks, cascade_groups=cascade_groups,
                            cascade_max_prefix_blocks=cascade_max_prefix_blocks, cascade_min_blocks=cascade_min_blocks,
-                           cascade_max_rows=max(1, 128 // (cfg.num_attention_heads // cfg.num_key_value_heads)))
+                           cascade_max_rows=max(1, 128 // (cfg.num_attention_heads // cfg.num_key_value_heads)),
+                           cascade_token_bytes=cfg.num_key_value_heads * _head_dim(cfg) * 2 * kv.dtype.itemsize,
+                           cascade_min_shared_bytes=cascade_min_shared_bytes)
         self.vocab_size = cfg.vocab_size
         act_dtype = torch.bfloat16 if kv.dtype == torch.float8_e4m3fn else kv.dtype  # activations stay bf16
         self._decode_out = torch.zeros(self.max_bs, self.hidden_size, dtype=act_dtype, device=self.device)
@@ -98,26 +106,39 @@ class ModelRunner:
         self._copy_event = torch.cuda.Event()
         self._sample_cpu = torch.empty(self.max_bs * 2, dtype=torch.int64, pin_memory=True)
         self.graph_runner: HipGraphRunner | None = None
+        self.cascade_graph_runner: HipGraphRunner | None = None
         self._sample_graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
         if not enforce_eager:
             # every workspace a graph will hold is allocated before the first capture
             reserve_workspace(self.device, self.max_bs, cfg.vocab_size)
             self.graph_runner = HipGraphRunner(HipGraphRunner.make_bs_list(self.max_bs), self.device)
             with torch.inference_mode():
-                self.graph_runner.capture(self._decode_body)
+                self.graph_runner.capture(lambda bs: self._decode_body(bs, cascade=False))
+                if self.batch.cascade is not None:
+                    self.cascade_graph_runner = HipGraphRunner(self.graph_runner.bs_list, self.device)
+                    self.cascade_graph_runner.capture(lambda bs: self._decode_body(bs, cascade=True))
                 for mode in dict.fromkeys((_C.XV_SAMPLE_ALL_GREEDY, *sample_modes)):
                     for bs in reversed(self.graph_runner.bs_list):
                         self._sample_graph(bs, mode)
 
     # ------------------------------------------------------------ decode
-    def _decode_attn(self, bs: int) -> AttnInputs:
+    def _use_cascade(self) -> bool:
+        """Whether the staged decode batch has shared-prefix groups worth the
+        cascade decode (the batch build applies the measured gate)."""
+        return self.batch.cascade is not None and self.batch.cascade_rows > 0
+
+    def _decode_attn(self, bs: int, cascade: bool) -> AttnInputs:
         return AttnInputs(slot_mapping=self.batch.slot_mapping[:bs], is_prefill=False,
                           cache_seqlens=self.batch.cache_seqlens[:bs], block_tables=self.batch.block_tables[:bs],
-                          cascade=self.batch.cascade)
+                          cascade=self.batch.cascade if cascade else None)
 
-    def _decode_body(self, bs: int) -> torch.Tensor:
+    def _decode_body(self, bs: int, cascade: bool | None = None) -> torch.Tensor:
+        """The decode forward over the staged batch; cascade None: as the
+        staged batch selects."""
+        if cascade is None:
+            cascade = self._use_cascade()
         with attention_context(self._meta):
-            out = self.model(self.batch.input_ids[:bs], self.batch.positions[:bs], self._decode_attn(bs))
+            out = self.model(self.batch.input_ids[:bs], self.batch.positions[:bs], self._decode_attn(bs, cascade))
         self._decode_out[:bs] = out
         return self._decode_out[:bs]
 
@@ -125,7 +146,8 @@ class ModelRunner:
     def decode_hidden(self, bs: int) -> torch.Tensor:
         """Final hidden states of the decode batch whose metadata is staged."""
         if self.graph_runner is not None and bs <= self.max_bs:
-            hidden, _ = self.graph_runner.replay(bs)
+            runner = self.cascade_graph_runner if self._use_cascade() else self.graph_runner
+            hidden, _ = runner.replay(bs)
             return hidden[:bs]
         return self._decode_body(bs)
 
@@ -256,3 +278,6 @@ class ModelRunner:
         if self.graph_runner is not None:
             self.graph_runner.destroy()
             self.graph_runner = None
+        if self.cascade_graph_runner is not None:
+            self.cascade_graph_runner.destroy()
+            self.cascade_graph_runner = None

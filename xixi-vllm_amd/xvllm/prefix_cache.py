@@ -206,6 +206,27 @@ class RadixPrefixCache:
         return freed
 
 
+# Shared bytes per layer (sum over a batch's groups of prefix tokens x kv bytes
+# per token) above which the cascade decode pays.  Measured on MI355X at the
+# Qwen3-32B attention shape (64 q / 8 kv heads, B 32 x 32768 tokens, us per
+# layer, plain -> cascade): 33.5 MB shared (8192 tokens, bf16) 592 -> 598 at
+# 16 rows and 525 -> 548 at 32 rows; 100 MB shared (24576 tokens) 493 -> 470
+# and 426 -> 248; 133 MB (32512 tokens) 410 -> 99.  Below about 64 MB the plain
+# decode's repeat reads of the shared pages are served by the 256 MB
+# last-level cache, and the cascade's prefix pass (20-75 us) and second merge
+# cost more than they save; fp8 pages (16.7 MB at 8192 tokens) lose inside
+# the model step as well (296 -> 298 us per layer at config 5).
+CASCADE_MIN_SHARED_BYTES = 64 << 20
+
+
+def cascade_pays(group_info: np.ndarray, token_bytes: int, min_shared_bytes: int = CASCADE_MIN_SHARED_BYTES) -> bool:
+    """Whether a batch's shared-prefix groups (cascade_groups' group_info)
+    share enough KV per layer for the cascade decode to beat the plain one."""
+    info = np.asarray(group_info)
+    live = info[:, 1] > 1
+    return bool(live.any()) and int(info[live, 3].astype(np.int64).sum()) * token_bytes >= min_shared_bytes
+
+
 def cascade_groups(block_tables: np.ndarray, seqlens: np.ndarray, block_size: int, *, max_rows: int,
                    min_blocks: int, max_groups: int, max_prefix_blocks: int):
     """Shared-prefix groups of a decode batch from its block tables.
