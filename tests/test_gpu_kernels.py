@@ -648,6 +648,40 @@ def test_sampler_one_workspace_sampled_and_greedy_calls_interleaved(dev):
         assert torch.equal(got, want), (bs, kind)
 
 
+def test_sampler_large_batches_bitexact(dev):
+    """Sampled batches of 129-256 rows (past the multi-workgroup chain's 128:
+    one workgroup per row): seeded top-k / top-p / min-p mixes with greedy
+    rows, flat and tied rows and NaN entries, equal to the C oracle on every
+    row."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    rng = np.random.default_rng(4242)
+    for case, (b, flags, kind) in enumerate([(129, 4, "flat"), (200, 2 | 4, "normal"), (256, 4 | 8, "ties"),
+                                             (256, 2 | 4 | 8, "normal"), (160, 0, "wide"), (256, 4, "massive")]):
+        v = 151936
+        std = {"flat": 0.05, "normal": 1.0, "wide": 4.0, "ties": 1.0, "massive": 1.0}[kind]
+        x = rng.standard_normal((b, v)).astype(np.float32) * std
+        if kind == "ties":
+            x = np.round(x * 4) / 4
+        if kind == "massive":
+            x = np.round(x) / 2
+        x[rng.random((b, v)) < 0.0005] = np.nan
+        logits = torch.from_numpy(x).to(torch.bfloat16)
+        temps = torch.from_numpy(rng.uniform(0.3, 1.5, b).astype(np.float32))
+        temps[torch.from_numpy(rng.random(b) < 0.2)] = 0.0
+        tps = torch.from_numpy(rng.uniform(0.3, 0.99, b).astype(np.float32))
+        tks = torch.from_numpy(rng.integers(1, 3000, b).astype(np.int32))
+        mps = torch.from_numpy(rng.uniform(0.0, 0.3, b).astype(np.float32))
+        u = torch.from_numpy(rng.random(b).astype(np.float32))
+        want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                        mps.numpy(), u.numpy(), flags)
+        print(f"large-batch case {case}: b {b} flags {flags} {kind}", flush=True)
+        got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev),
+                     use_top_k=bool(flags & 2), use_top_p=bool(flags & 4), use_min_p=bool(flags & 8))
+        assert np.array_equal(got.cpu().numpy(), want), (case, np.nonzero(got.cpu().numpy() != want)[0][:8])
+
+
 def test_sampler_randomized_configurations_bitexact(dev):
     """40 seeded random configurations (batch 1-40, vocabularies 1003 / 4099 /
     32000 / 151936, any mix of top-k / top-p / min-p, temperatures with some

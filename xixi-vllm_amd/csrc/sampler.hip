@@ -178,18 +178,6 @@ struct FastShared {
   int ncand;
 };
 
-XV_INLINE uint32_t wave_max_u(uint32_t x) {
-  for (int o = 32; o > 0; o >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, o));
-  return x;
-}
-XV_INLINE uint32_t wave_min_u(uint32_t x) {
-  for (int o = 32; o > 0; o >>= 1) x = min(x, (uint32_t)__shfl_xor((int)x, o));
-  return x;
-}
-XV_INLINE float wave_maxf(float x) {
-  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o));
-  return x;
-}
 // x[lane ^ S] in registers, no LDS round trip: DPP within a 16-lane row for
 // S = 1, 2 (quad_perm), 8 (row_ror:8) and 4 (row_ror:4 for lanes with bit 2
 // set, row_ror:12 for the others: row_ror:n reads lane (i - n) mod 16), the
@@ -223,6 +211,49 @@ XV_INLINE unsigned long long xor_lane64(unsigned long long x, int s) {  // s a c
     default: return xor_lane64<32>(x);
   }
 }
+// Wave-wide reductions through the register permutes above (the shuffles
+// they replace each took an LDS round trip, two for 64-bit values).
+XV_INLINE uint32_t wave_max_u(uint32_t x) {
+  x = max(x, xor_lane<1>(x));
+  x = max(x, xor_lane<2>(x));
+  x = max(x, xor_lane<4>(x));
+  x = max(x, xor_lane<8>(x));
+  x = max(x, xor_lane<16>(x));
+  return max(x, xor_lane<32>(x));
+}
+XV_INLINE uint32_t wave_min_u(uint32_t x) {
+  x = min(x, xor_lane<1>(x));
+  x = min(x, xor_lane<2>(x));
+  x = min(x, xor_lane<4>(x));
+  x = min(x, xor_lane<8>(x));
+  x = min(x, xor_lane<16>(x));
+  return min(x, xor_lane<32>(x));
+}
+XV_INLINE float wave_maxf(float x) {
+  x = fmaxf(x, __uint_as_float(xor_lane<1>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xor_lane<2>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xor_lane<4>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xor_lane<8>(__float_as_uint(x))));
+  x = fmaxf(x, __uint_as_float(xor_lane<16>(__float_as_uint(x))));
+  return fmaxf(x, __uint_as_float(xor_lane<32>(__float_as_uint(x))));
+}
+XV_INLINE int64_t wave_min_l(int64_t x) {
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) {
+    const int64_t y = (int64_t)xor_lane64(x, sh);
+    x = y < x ? y : x;
+  }
+  return x;
+}
+XV_INLINE unsigned long long wave_max_ull(unsigned long long x) {
+#pragma unroll
+  for (int sh = 1; sh < 64; sh <<= 1) {
+    const unsigned long long y = xor_lane64(x, sh);
+    x = y > x ? y : x;
+  }
+  return x;
+}
+
 // x[63 - lane]: row_mirror (lane i of a row reads lane 15 - i), then the row swaps
 XV_INLINE unsigned long long reverse_lanes64(unsigned long long x) {
   const uint32_t lo = dpp_u<0x140>((uint32_t)x), hi = dpp_u<0x140>((uint32_t)(x >> 32));
@@ -302,11 +333,7 @@ XV_INLINE int64_t block_sum_l(Shared& s, int64_t x) {
 // Exclusive prefix sum over the block (thread order); *total gets the block sum.
 XV_INLINE int64_t block_excl_scan(Shared& s, int64_t x, int64_t* total) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  int64_t inc = x;
-  for (int o = 1; o < 64; o <<= 1) {
-    int64_t y = __shfl_up(inc, o);
-    if (lane >= o) inc += y;
-  }
+  const int64_t inc = wave_incl_scan_l(x);
   __syncthreads();
   if (lane == 63) s.red_l[w] = inc;
   __syncthreads();
@@ -565,10 +592,7 @@ XV_INLINE void general_boundary(Shared& s, const bf16_t* row, int V, bool vec_ok
 }
 
 XV_INLINE int64_t block_min_l(Shared& s, int64_t x) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t y = __shfl_xor(x, o);
-    x = y < x ? y : x;
-  }
+  x = wave_min_l(x);
   const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) s.red_l[w] = x;
@@ -1249,10 +1273,7 @@ XV_INLINE uint32_t seg_min_u(SegRed& r, uint32_t x) {
   return m;
 }
 XV_INLINE unsigned long long seg_max_ull(SegRed& r, unsigned long long x) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long y = __shfl_xor(x, o);
-    x = y > x ? y : x;
-  }
+  x = wave_max_ull(x);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) r.u[threadIdx.x >> 6] = x;
   __syncthreads();
@@ -1270,10 +1291,7 @@ XV_INLINE int64_t seg_sum_l(SegRed& r, int64_t x) {
   return m;
 }
 XV_INLINE int64_t seg_min_l(SegRed& r, int64_t x) {
-  for (int o = 32; o > 0; o >>= 1) {
-    const int64_t y = __shfl_xor(x, o);
-    x = y < x ? y : x;
-  }
+  x = wave_min_l(x);
   __syncthreads();
   if ((threadIdx.x & 63) == 0) r.l[threadIdx.x >> 6] = x;
   __syncthreads();
@@ -1284,10 +1302,7 @@ XV_INLINE int64_t seg_min_l(SegRed& r, int64_t x) {
 // Inclusive prefix sum over the workgroup (thread order).
 XV_INLINE int64_t seg_incl_scan(SegRed& r, int64_t x) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  for (int o = 1; o < 64; o <<= 1) {
-    const int64_t y = __shfl_up(x, o);
-    if (lane >= o) x += y;
-  }
+  x = wave_incl_scan_l(x);
   __syncthreads();
   if (lane == 63) r.l[w] = x;
   __syncthreads();
