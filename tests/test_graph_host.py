@@ -148,3 +148,27 @@ def test_read_samples_rejects_out_of_range_ids():
         r._sample_cpu = torch.tensor([5, bad, 0, 3], dtype=torch.int64)
         with pytest.raises(SampledIdOutOfRange):
             r.read_samples(2, 2)
+
+
+def test_cached_workspaces_are_plain_tensors_after_inference_mode():
+    """A per-device workspace first grown inside torch.inference_mode (the
+    runner's decode) is a plain tensor: callers outside inference mode can
+    still write to it (a test that fills it with NaN patterns does)."""
+    import torch
+
+    from xvllm.layers import attention as A
+    from xvllm import sampler as Sm
+
+    dev = torch.device("cpu")
+    for fn, store in ((A.decode_workspace, A._WORKSPACE), (Sm._workspace, Sm._WORKSPACE)):
+        key = (dev.type, dev.index)
+        saved = store.pop(key, None)
+        try:
+            with torch.inference_mode():
+                ws = fn(dev, 4096)
+            assert not ws.is_inference()
+            ws.fill_(255)
+        finally:
+            store.pop(key, None)
+            if saved is not None:
+                store[key] = saved

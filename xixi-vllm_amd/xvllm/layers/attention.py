@@ -105,7 +105,8 @@ def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED.append(ws)
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+        with torch.inference_mode(False):  # a plain tensor: later callers outside inference mode may use it
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws
 
@@ -226,7 +227,8 @@ def cascade_decode_attention(
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED.append(ws)  # a recorded graph may still hold it
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=q.device)
+        with torch.inference_mode(False):  # a plain tensor: later callers outside inference mode may use it
+            ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=q.device)
         _CASCADE_WS[key] = ws
     scale = 1.0 / math.sqrt(head_dim) if softmax_scale is None else softmax_scale
     args = (

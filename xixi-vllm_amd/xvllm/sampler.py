@@ -42,7 +42,8 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED.append(ws)
-        ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
+        with torch.inference_mode(False):  # a plain tensor: later callers outside inference mode may use it
+            ws = torch.zeros(max(nbytes, 4096), dtype=torch.uint8, device=device)
         _WORKSPACE[key] = ws
     return ws
 
