@@ -461,7 +461,7 @@ def decode_e2e(torch, dev, ctx: list[int], steps: int = 20, sampled: bool = Fals
             "frac_of_roofline": round(roof_ms / ms, 4), "weight_bytes": wbytes, "kv_bytes": kvbytes}, model
 
 
-def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int = 8, cascade: bool = False,
+def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int = 8, attention: str = "gated",
                    model=None, fp8: bool = False):
     """Config 5: Qwen3-32B-shaped decode (64 layers, hidden 5120, 64 q / 8 kv
     heads, FFN 25600, random bf16 weights ~N(0,0.02)), batch 32 at context
@@ -481,9 +481,12 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
     fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
     layer i reads pool layer i % pool_layers: every layer streams the same
     bytes in the same pattern as with a full pool (what this leaves out: the
-    real memory footprint and the TLB reach of 243 GB).  cascade: the runner
-    reads the shared pages once per group (cascade decode).  fp8: the pool in
-    the optional fp8 (e4m3fn) page format."""
+    real memory footprint and the TLB reach of 243 GB).  attention: "gated"
+    is the runner as served (cascade groups staged, the measured gate of
+    xvllm.prefix_cache choosing cascade or plain decode per step: the 8192
+    shared tokens pass it), "plain" a runner without cascade groups,
+    "cascade" the cascade forced.  fp8: the pool in the optional fp8
+    (e4m3fn) page format."""
     from xvllm.config import QWEN3_32B
     from xvllm.kv_pool import KVPool
     from xvllm.model_runner import ModelRunner
@@ -521,10 +524,12 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
                 view.copy_((torch.randn(view.shape, device=dev) / FP8_SCALE).to(torch.float8_e4m3fn))
     else:
         kv.kv_cache.normal_()
-    # the cascade variant forces the cascade (the runner's default gate keeps
-    # config 5's 8192-token prefix on the plain decode: measured faster)
-    casc = dict(cascade_groups=2, cascade_max_prefix_blocks=ppg, cascade_min_blocks=64,
-                cascade_min_shared_bytes=0) if cascade else {}
+    if attention not in ("gated", "plain", "cascade"):
+        raise ValueError(f"attention {attention!r}")
+    casc = {} if attention == "plain" else dict(cascade_groups=2, cascade_max_prefix_blocks=ppg,
+                                                cascade_min_blocks=64)
+    if attention == "cascade":
+        casc["cascade_min_shared_bytes"] = 0
     runner = ModelRunner(model, kv, max_num_seqs=bsz, context_len=ctx + gen, device=dev,
                          sample_modes=(4,), **casc)
     runner.generator = torch.Generator(device=dev).manual_seed(5)
@@ -538,8 +543,9 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
     runner.destroy()
     assert st.hit_tokens == (shared - 1) * prefix, st.hit_tokens
     assert all(len(o) == gen for o in outs) and st.steps == gen
-    if cascade:
-        assert seen["cascade_rows"] == shared
+    cascade = seen["cascade_rows"] > 0
+    if attention != "plain":  # 8192 shared tokens (32 / 16 MiB per layer) pass the gate
+        assert seen["cascade_rows"] == shared, seen
     t = st.step_end_s
     ms = (t[-1] - t[warmup - 1]) / steps * 1e3
     wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
@@ -555,7 +561,8 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
     return {"model": "Qwen3-32B-shaped (64 layers, 64q/8kv, FFN 25600)", "batch": bsz, "context": ctx,
             "shared_prefix": f"{shared} requests x {prefix} tokens; {st.hit_tokens} prompt tokens' pages handed out "
                              "by the serving ledger's radix prefix cache",
-            "attention": "cascade (shared blocks read once per kv head)" if cascade else "plain paged decode",
+            "attention": ("cascade (shared blocks read once per kv head)" if cascade else "plain paged decode")
+                         + (", chosen by the runner's gate" if attention == "gated" else ", forced"),
             "kv_pages": "fp8 e4m3fn" if fp8 else "bf16", "path": "xvllm.serving.serve(prefilled=True)",
             "sampling": "top-p 0.95 (T 1.0)", "kv_pool_layers": pool_layers, "timed_steps": steps,
             "ms_per_step": round(ms, 3), "tok_per_s": round(bsz / (ms * 1e-3), 1), "weight_bytes": wbytes,
@@ -567,22 +574,30 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
 def cascade_sweep(torch, dev, iters: int = 10) -> dict:
     """Shared-prefix decode attention alone, plain against cascade, at the
     Qwen3-32B attention shape (64 q / 8 kv heads, head-major 16-token pages),
-    B 32 x 32768 tokens: `rows` requests share the first `prefix` tokens (the
-    same pages), the rest of the KV is per request.  Two layers of KV are
-    cycled so that a call does not find the previous call's pages in the
-    last-level cache.  us per call (one layer), bf16 and fp8 pages."""
+    B 32 at 32768 and at 32777 tokens: `rows` requests share the first
+    `prefix` tokens (the same pages), the rest of the KV is per request.  At
+    32768 tokens (2048 whole pages per row) the plain decode's stream-K ranges
+    start every row's prefix at the same moment, so the rows' reads of a
+    shared page arrive together and the last-level cache serves the repeats;
+    one more page (32777, as a serving run's contexts fall) shifts the rows
+    against each other.  Two layers of KV are cycled so that a call does not
+    find the previous call's pages in the last-level cache.  us per call (one
+    layer), bf16 and fp8 pages."""
     import numpy as np
 
     from xvllm.layers.attention import CascadePlan, cascade_decode_attention, paged_decode_attention
     from xvllm.prefix_cache import cascade_groups
 
-    hq, hkv, d, ctx, bsz = 64, 8, 128, 32768, 32
+    hq, hkv, d, bsz = 64, 8, 128, 32
     g = torch.Generator(device=dev).manual_seed(3)
     q = torch.randn((bsz, hq * d), generator=g, device=dev).to(torch.bfloat16)
-    sl = torch.full((bsz,), ctx, dtype=torch.int32, device=dev)
     out = {}
-    for rows, prefix in ((16, 8192), (32, 8192), (16, 24576), (32, 24576), (32, ctx - 256)):
-        npg, ppg = ctx // PAGE, prefix // PAGE
+    cases = [(ctx, rows, prefix) for ctx in (32768, 32777)
+             for rows, prefix in ((16, 2048), (32, 2048), (16, 4096), (32, 4096), (16, 8192), (32, 8192),
+                                  (16, 24576), (32, 24576), (32, 32512))]
+    for ctx, rows, prefix in cases:
+        sl = torch.full((bsz,), ctx, dtype=torch.int32, device=dev)
+        npg, ppg = (ctx + PAGE - 1) // PAGE, prefix // PAGE
         unique = ppg + rows * (npg - ppg) + (bsz - rows) * npg
         perm = torch.randperm(unique, generator=torch.Generator().manual_seed(1)).to(torch.int32)
         bt = torch.empty((bsz, npg), dtype=torch.int32)
@@ -624,7 +639,7 @@ def cascade_sweep(torch, dev, iters: int = 10) -> dict:
                 rec[f"{'fp8' if fp8 else 'bf16'}_{name}_us"] = round(e0.elapsed_time(e1) / (2 * iters) * 1e3, 1)
             del caches
             torch.cuda.empty_cache()
-        out[f"rows{rows}_prefix{prefix}"] = rec
+        out[f"ctx{ctx}_rows{rows}_prefix{prefix}"] = rec
     return out
 
 
@@ -851,7 +866,8 @@ def main() -> int:
     ap.add_argument("--no-serve", action="store_true", help="skip config 4 (256 requests, greedy and sampled)")
     ap.add_argument("--serve-only", action="store_true", help="only config 4 (for profiling)")
     ap.add_argument("--config5", action="store_true",
-                    help="also run config 5's cascade and fp8-page variants (plain bf16 config 5 runs by default)")
+                    help="also run config 5 with the plain decode forced and on fp8 pages (the runner as served, "
+                         "its gate choosing the decode, runs by default)")
     ap.add_argument("--no-config5", action="store_true", help="skip config 5 (Qwen3-32B-shaped long-context decode)")
     ap.add_argument("--config5-only", action="store_true", help="only config 5 (for profiling)")
     ap.add_argument("--cascade-only", action="store_true",
@@ -893,11 +909,11 @@ def main() -> int:
         print(json.dumps({"decode_e2e": rec, "decode_e2e_fp8": rec8}))
         return 0
     if args.config5_only:
-        c5, model = decode_config5(torch, dev, cascade=False)
-        c5c, model = decode_config5(torch, dev, cascade=True, model=model)
-        c58, model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
-        c58c, model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
-        print(json.dumps({"config5": c5, "config5_cascade": c5c, "config5_fp8": c58, "config5_cascade_fp8": c58c}))
+        c5, model = decode_config5(torch, dev)
+        c5p, model = decode_config5(torch, dev, attention="plain", model=model)
+        c58, model = decode_config5(torch, dev, model=model, fp8=True)
+        c58p, model = decode_config5(torch, dev, attention="plain", model=model, fp8=True)
+        print(json.dumps({"config5": c5, "config5_plain": c5p, "config5_fp8": c58, "config5_plain_fp8": c58p}))
         return 0
     if args.cascade_only:
         print(json.dumps({"cascade_sweep": cascade_sweep(torch, dev)}))
@@ -1006,11 +1022,11 @@ def main() -> int:
         torch.cuda.empty_cache()
     if not args.no_config5:
         torch.cuda.empty_cache()
-        line["config5"], model = decode_config5(torch, dev, cascade=False)
+        line["config5"], model = decode_config5(torch, dev)
         if args.config5:
-            line["config5_cascade"], model = decode_config5(torch, dev, cascade=True, model=model)
-            line["config5_fp8"], model = decode_config5(torch, dev, cascade=False, model=model, fp8=True)
-            line["config5_cascade_fp8"], model = decode_config5(torch, dev, cascade=True, model=model, fp8=True)
+            line["config5_plain"], model = decode_config5(torch, dev, attention="plain", model=model)
+            line["config5_fp8"], model = decode_config5(torch, dev, model=model, fp8=True)
+            line["config5_plain_fp8"], model = decode_config5(torch, dev, attention="plain", model=model, fp8=True)
         del model
         torch.cuda.empty_cache()
     if not args.no_serve:

@@ -142,7 +142,7 @@ def test_cascade_gate_takes_the_cascade_only_past_the_measured_bytes():
     big = np.array([[0, 4, 0, 8192 * 2], [0, 3, 4, 8192]], np.int32)
     assert cascade_pays(big, tok_bytes)  # 24576 tokens x 4 KB = 100 MB
     assert not cascade_pays(np.zeros((2, 4), np.int32), tok_bytes, 0)
-    assert CASCADE_MIN_SHARED_BYTES == 64 << 20
+    assert CASCADE_MIN_SHARED_BYTES == 8 << 20
     for gate, want in ((None, 0), (0, 4)):
         b = Batch(max_bs=8, max_tokens=64, max_blocks=64, vocab_size=100, device=torch.device("cpu"), block_size=16,
                   num_blocks=512, cascade_groups=2, cascade_min_blocks=4, cascade_token_bytes=tok_bytes,

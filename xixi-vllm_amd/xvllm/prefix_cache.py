@@ -207,16 +207,19 @@ class RadixPrefixCache:
 
 
 # Shared bytes per layer (sum over a batch's groups of prefix tokens x kv bytes
-# per token) above which the cascade decode pays.  Measured on MI355X at the
-# Qwen3-32B attention shape (64 q / 8 kv heads, B 32 x 32768 tokens, us per
-# layer, plain -> cascade): 33.5 MB shared (8192 tokens, bf16) 592 -> 598 at
-# 16 rows and 525 -> 548 at 32 rows; 100 MB shared (24576 tokens) 493 -> 470
-# and 426 -> 248; 133 MB (32512 tokens) 410 -> 99.  Below about 64 MB the plain
-# decode's repeat reads of the shared pages are served by the 256 MB
-# last-level cache, and the cascade's prefix pass (20-75 us) and second merge
-# cost more than they save; fp8 pages (16.7 MB at 8192 tokens) lose inside
-# the model step as well (296 -> 298 us per layer at config 5).
-CASCADE_MIN_SHARED_BYTES = 64 << 20
+# per token) from which the cascade decode pays.  Measured on MI355X at the
+# Qwen3-32B attention shape (64 q / 8 kv heads, B 32 rows of 32777 tokens, us
+# per layer, plain -> cascade, bf16 pages): 16 rows sharing 2048 tokens
+# (8 MiB) 670 -> 665, 4096 tokens 663 -> 644, 8192 tokens 661 -> 614, 24576
+# tokens 677 -> 473; fp8 pages: 2048 tokens (4 MiB) 362 -> 365, 4096 tokens
+# (8 MiB) 360 -> 354, 8192 tokens 361 -> 339.  Below 8 MiB the prefix pass
+# and the second merge cost what the saved reads give back.  (At exactly
+# 32768 tokens, 2048 whole pages per row, the plain decode's stream-K ranges
+# start every row's prefix together and the last-level cache serves the
+# rows' repeat reads of a shared page: plain then wins up to 8192 shared
+# tokens, 607 against 620 at 16 rows.  One more token breaks that alignment,
+# and serving contexts are almost never so aligned.)
+CASCADE_MIN_SHARED_BYTES = 8 << 20
 
 
 def cascade_pays(group_info: np.ndarray, token_bytes: int, min_shared_bytes: int = CASCADE_MIN_SHARED_BYTES) -> bool:
