@@ -56,6 +56,31 @@ def test_decode_rows_and_bucket_padding():
     assert (bt[5:8] == -1).all()
 
 
+def test_decode_inputs_fed_from_the_previous_steps_ids():
+    """Rows with src_row >= 0 take their input id from the previous step's
+    sampled ids (a device tensor) by a gather, clamped into [0, vocab); the
+    other rows keep their host ids; a source row past the previous step's ids
+    or a missing previous step raises."""
+    import dataclasses
+
+    import pytest
+
+    g = gen(84)
+    b = _batch()
+    seqs = _seqs(g, 6, 200, decode=True)
+    prev = torch.tensor([11, 22, V + 5, 44, -3, 66], dtype=torch.int64)  # two ids a bad sampler could leave
+    src = [3, -1, 0, 2, -1, 4]
+    fed = [dataclasses.replace(s, token_ids=[0] if r >= 0 else s.token_ids, src_row=r) for s, r in zip(seqs, src)]
+    b.build_decode(fed, prev_ids=prev)
+    want = [min(max(int(prev[r]), 0), V - 1) if r >= 0 else s.token_ids[-1] for s, r in zip(seqs, src)]
+    assert b.input_ids[:6].tolist() == want
+    assert b.input_ids[3] == V - 1 and b.input_ids[5] == 0  # clamped
+    with pytest.raises(ValueError, match="previous step"):
+        b.build_decode(fed)
+    with pytest.raises(ValueError, match="source row"):
+        b.build_decode(fed, prev_ids=prev[:3])
+
+
 def test_block_table_rows_grow_append_only_and_follow_new_owners():
     g = gen(82)
     b = _batch()

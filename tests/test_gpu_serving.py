@@ -98,7 +98,7 @@ def test_decode_sampler_graphs_match_oracle(dev):
     runner.destroy()
 
 
-def _serve(dev, model, kv, prompts, gen, sampling, seed, check):
+def _serve(dev, model, kv, prompts, gen, sampling, seed, check, overlap=True):
     from xvllm.model_runner import ModelRunner
     from xvllm.serving import serve
 
@@ -110,7 +110,7 @@ def _serve(dev, model, kv, prompts, gen, sampling, seed, check):
             if n_d:
                 _oracle_check(r, n_d)
     outs, st = serve(runner, prompts, gen, sampling=sampling, max_num_seqs=16, max_num_batched_tokens=512,
-                     after_forward=hook)
+                     overlap=overlap, after_forward=hook)
     runner.destroy()
     return outs, st
 
@@ -133,6 +133,31 @@ def test_config4_reduced_serving(dev):
     assert s1 == s2, "seeded sampled serving is not reproducible"
     assert all(0 <= t < V for o in s1 + greedy1 for t in o)
     assert s1 != greedy1
+
+
+def test_overlapped_serving_equals_one_step_at_a_time(dev):
+    """The serving loop with one step in flight (decode inputs fed from the
+    previous step's ids on the device, read-back and bookkeeping trailing by
+    a step) gives the same greedy and seeded sampled ids as the loop that
+    reads every step back before scheduling the next, on the same workload
+    (random prompts: no shared prefixes, so both loops schedule the same
+    steps); the overlapped sampled steps equal the oracle on the device's
+    logits."""
+    model, kv = _model(dev, seed=11, num_blocks=1024)
+    g = torch.Generator().manual_seed(405)
+    prompts = [torch.randint(0, V, (int(n),), generator=g).tolist() for n in torch.randint(16, 301, (24,), generator=g)]
+    gen = 20
+    print("overlap vs one step at a time: greedy", flush=True)
+    a, st_a = _serve(dev, model, kv, prompts, gen, None, 0, check=False, overlap=True)
+    b, st_b = _serve(dev, model, kv, prompts, gen, None, 0, check=False, overlap=False)
+    assert st_a.step_work == st_b.step_work, "the two loops scheduled different steps"
+    assert a == b, "overlapped greedy serving differs from the one-step-at-a-time loop"
+    print("overlap vs one step at a time: sampled, oracle-checked", flush=True)
+    samp = dict(temperature=0.7, top_p=0.9, top_k=50)
+    s1, _ = _serve(dev, model, kv, prompts, gen, samp, 7, check=True, overlap=True)
+    s2, _ = _serve(dev, model, kv, prompts, gen, samp, 7, check=False, overlap=False)
+    assert s1 == s2, "overlapped sampled serving differs from the one-step-at-a-time loop"
+    assert all(len(o) == gen for o in a + s1)
 
 
 def test_config4_reduced_serving_fp8_pool(dev):
@@ -192,9 +217,11 @@ def test_reduced_serving_prefix_cache_reuses_pages(dev):
                 assert not bad.any(), f"request {r.rid} (hit {r.hit} of {n}): {bad.sum()} K/V elements differ"
                 checked.append((r.rid, r.hit))
 
+    # the hook launches prefills of its own: one step at a time (no step in flight)
     outs1, st = serve(runner, prompts, gen, num_pages=ledger_pages, max_num_seqs=16, max_num_batched_tokens=512,
-                      after_step=after_step)
-    outs2, _ = serve(runner, prompts, gen, num_pages=ledger_pages, max_num_seqs=16, max_num_batched_tokens=512)
+                      overlap=False, after_step=after_step)
+    outs2, _ = serve(runner, prompts, gen, num_pages=ledger_pages, max_num_seqs=16, max_num_batched_tokens=512,
+                     overlap=False)
     runner.destroy()
     assert outs1 == outs2, "greedy serving with the prefix cache is not reproducible"
     assert st.hit_tokens > 0 and st.prefill_tokens + st.hit_tokens == sum(len(p) for p in prompts)

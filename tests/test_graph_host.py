@@ -139,13 +139,21 @@ def test_read_samples_rejects_out_of_range_ids():
         def synchronize(self):
             pass
 
+    from collections import deque
+
     r = ModelRunner.__new__(ModelRunner)
-    r._copy_event = Ev()
     r.vocab_size = 1000
-    r._sample_cpu = torch.tensor([5, 999, 0, 3], dtype=torch.int64)
+    r._readback = [(torch.tensor([5, 999, 0, 3], dtype=torch.int64), Ev()), (torch.zeros(4, dtype=torch.int64), Ev())]
+    r._pending = deque([(0, 1, 3)])
     assert r.read_samples(1, 3) == ([3], [5, 999, 0])
+    with pytest.raises(RuntimeError, match="no launched step"):
+        r.read_samples(1, 3)
+    r._pending = deque([(0, 1, 3)])
+    with pytest.raises(ValueError, match="oldest waiting step"):
+        r.read_samples(2, 2)
     for bad in (1000, -1, 1 << 40):
-        r._sample_cpu = torch.tensor([5, bad, 0, 3], dtype=torch.int64)
+        r._readback[1] = (torch.tensor([5, bad, 0, 3], dtype=torch.int64), Ev())
+        r._pending = deque([(1, 2, 2)])
         with pytest.raises(SampledIdOutOfRange):
             r.read_samples(2, 2)
 

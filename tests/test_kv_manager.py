@@ -12,6 +12,8 @@
   with the prefix cache equal those without it while fewer tokens are
   prefilled.
 """
+from collections import deque
+
 import numpy as np
 import pytest
 import torch
@@ -148,7 +150,9 @@ class FakeRunner:
         self.slots = np.full(num_pages * block_size, -1, np.int64)
         self.vocab = vocab
         self.ctx = {}   # seq id -> tokens whose KV it has written
-        self._ids = None
+        self._pending = deque()  # (prefill ids, decode ids) of launched steps not read back
+        self._last = []          # the last launched step's ids, decode rows first (the device's copy)
+        self.launched_steps = 0
 
     def _check_and_write(self, s, new_tokens):
         bs = self.block_size
@@ -168,13 +172,18 @@ class FakeRunner:
         return int(sum((i + 1) * t for i, t in enumerate(ctx)) % self.vocab)
 
     def run_forward(self, decodes, prefills):
-        d = [self._check_and_write(s, s.token_ids) for s in decodes]
+        # a device-fed decode input is the previous launched step's id of that row
+        d = [self._check_and_write(s, [self._last[s.src_row]] if s.src_row >= 0 else s.token_ids) for s in decodes]
         p = [self._check_and_write(s, s.token_ids) for s in prefills]
-        self._ids = (p, d)
+        self._pending.append((p, d))
+        self._last = d + p
+        self.launched_steps += 1
         return len(p), len(d)
 
     def read_samples(self, n_p, n_d):
-        return self._ids
+        p, d = self._pending.popleft()
+        assert (len(p), len(d)) == (n_p, n_d)
+        return p, d
 
 
 def _workload(seed, n_req=24, vocab=1000):
@@ -211,8 +220,9 @@ def _live_check(kvm, live):
     kvm.check({r.rid: r.bt for r in live})
 
 
+@pytest.mark.parametrize("overlap", [False, True])
 @pytest.mark.parametrize("seed", [0, 1, 2])
-def test_serve_with_prefix_cache_matches_without(monkeypatch, seed):
+def test_serve_with_prefix_cache_matches_without(monkeypatch, seed, overlap):
     from xvllm import serving
 
     monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
@@ -224,7 +234,7 @@ def test_serve_with_prefix_cache_matches_without(monkeypatch, seed):
         runner = FakeRunner(pages, BS)
         _recording(monkeypatch, runner)
         outs[pc] = serving.serve(runner, prompts, gen, max_num_seqs=6, max_num_batched_tokens=40,
-                                 prefix_cache=pc, after_step=_live_check)
+                                 prefix_cache=pc, overlap=overlap, after_step=_live_check)
     assert outs[True][0] == outs[False][0]
     assert all(len(o) == gen for o in outs[True][0])
     st_on, st_off = outs[True][1], outs[False][1]
@@ -232,8 +242,9 @@ def test_serve_with_prefix_cache_matches_without(monkeypatch, seed):
     assert st_on.prefill_tokens + st_on.hit_tokens == st_off.prefill_tokens
 
 
+@pytest.mark.parametrize("overlap", [False, True])
 @pytest.mark.parametrize("prefix_cache", [False, True])
-def test_serve_under_page_pressure(monkeypatch, prefix_cache):
+def test_serve_under_page_pressure(monkeypatch, prefix_cache, overlap):
     """A pool only as large as the pages of the max_num_seqs largest
     requests: prompts wait for pages, cached pages are evicted for later
     prompts, no live page is ever reused, and the outputs equal those of a
@@ -259,13 +270,63 @@ def test_serve_under_page_pressure(monkeypatch, prefix_cache):
     runner = FakeRunner(small, BS)
     _recording(monkeypatch, runner)
     outs, st = serving.serve(runner, prompts, gen, max_num_seqs=seqs, max_num_batched_tokens=32,
-                             prefix_cache=prefix_cache, after_step=_live_check)
+                             prefix_cache=prefix_cache, overlap=overlap, after_step=_live_check)
     big = FakeRunner(sum(demand), BS)
     _recording(monkeypatch, big)
-    want, _ = serving.serve(big, prompts, gen, max_num_seqs=seqs, max_num_batched_tokens=32, prefix_cache=False)
+    want, _ = serving.serve(big, prompts, gen, max_num_seqs=seqs, max_num_batched_tokens=32, prefix_cache=False,
+                            overlap=False)
     assert outs == want
     if prefix_cache:
         assert evicted, "the run never had to evict a cached page"
         assert st.hit_tokens > 0
     with pytest.raises(ValueError, match="live requests may need"):
         serving.serve(FakeRunner(small - 1, BS), prompts, gen, max_num_seqs=seqs)
+
+
+@pytest.mark.parametrize("prefilled", [False, True])
+def test_overlapped_serving_keeps_one_step_in_flight(monkeypatch, prefilled):
+    """With overlap, every step after the first is launched before the
+    previous one is read back, decode inputs after a prefill or decode come
+    from the device (src_row), and the outputs equal the one-step-at-a-time
+    loop's."""
+    from xvllm import serving
+
+    monkeypatch.setattr(torch.cuda, "synchronize", lambda *a, **k: None)
+    prompts = _workload(3, n_req=20)
+    gen = 6
+    pages = sum((len(p) + gen + BS - 1) // BS for p in prompts)
+    runs = {}
+    for overlap in (False, True):
+        runner = FakeRunner(pages, BS)
+        _recording(monkeypatch, runner)
+        if prefilled:  # the pool "holds" every prompt token but the last
+            orig = runner._check_and_write
+
+            def fill_then_check(s, toks, runner=runner, orig=orig):
+                if s.seq_id not in runner.ctx:
+                    bt = np.asarray(s.block_table, np.int64)
+                    pos = np.arange(s.num_cached_tokens)
+                    prompt = runner._hit_tokens[s.seq_id]
+                    runner.slots[bt[pos // BS] * BS + pos % BS] = prompt[: s.num_cached_tokens]
+                    runner.ctx[s.seq_id] = list(prompt[: s.num_cached_tokens])
+                return orig(s, toks)
+
+            runner._check_and_write = fill_then_check
+        depth, fed = [], []
+        orig_run = runner.run_forward
+
+        def spy(decodes, prefills, runner=runner, orig_run=orig_run, depth=depth, fed=fed):
+            depth.append(len(runner._pending))
+            fed.extend(s.src_row >= 0 for s in decodes)
+            return orig_run(decodes, prefills)
+
+        runner.run_forward = spy
+        outs, st = serving.serve(runner, prompts, gen, max_num_seqs=8, max_num_batched_tokens=48, overlap=overlap,
+                                 prefilled=prefilled, after_step=_live_check)
+        runs[overlap] = (outs, st, depth, fed)
+    assert runs[True][0] == runs[False][0]
+    assert all(len(o) == gen for o in runs[True][0])
+    _, st, depth, fed = runs[True]
+    assert depth[0] == 0 and all(d == 1 for d in depth[1:]), depth
+    assert sum(fed) == st.decode_tokens - (len(prompts) if prefilled else 0)
+    assert max(runs[False][2]) == 0 and not any(runs[False][3])

@@ -30,6 +30,9 @@ class SeqSchedule:
     top_k: int | None = None
     min_p: float | None = None
     need_sample: bool = True
+    # decode rows only: when >= 0, the input id is row src_row of the previous
+    # step's sampled ids, still on the device (token_ids is then a placeholder)
+    src_row: int = -1
 
 
 def slots_for_range(block_table, start: int, end: int, block_size: int) -> np.ndarray:
@@ -92,6 +95,8 @@ class Batch:
         self._h_bt = _pinned((max_bs, max_blocks), torch.int32, -1, pin=pin)
         self._h_samp = _pinned((4, max_bs), torch.float32, pin=pin)
         self._h_topk = _pinned((max_bs,), torch.int32, pin=pin)
+        self._h_feed = _pinned((2, max_bs), torch.int64, pin=pin)  # (batch row, source row) of device-fed ids
+        self._feed = gpu((2, max_bs), torch.int64)
         self._bt_np = self._h_bt.numpy()
         self._row_len = np.full(max_bs, -1, dtype=np.int64)   # entries of each host row in sync
         self._row_sid = np.full(max_bs, -1, dtype=np.int64)   # sequence that owns the row
@@ -189,12 +194,25 @@ class Batch:
         self.max_top_k = int(k.max()) if self.use_top_k else 0
 
     # ------------------------------------------------------------ decode
-    def build_decode(self, seqs: list[SeqSchedule], *, pad_to: int | None = None) -> None:
+    def build_decode(self, seqs: list[SeqSchedule], *, pad_to: int | None = None,
+                     prev_ids: torch.Tensor | None = None) -> None:
+        """Stage a decode batch.  Rows with src_row >= 0 take their input id
+        from prev_ids[src_row] (the previous step's sampled ids, on the
+        device) by a gather on the current stream, clamped into [0, vocab) so
+        that an id the host has not yet checked can never index past the
+        embedding; the host checks every id when it reads them back."""
         n = len(seqs)
         self._wait_staging()
         self._sync_block_tables(seqs)
         pos = np.fromiter((s.num_cached_tokens for s in seqs), np.int64, n)
-        ids = np.fromiter((s.token_ids[-1] for s in seqs), np.int64, n)
+        src = np.fromiter((s.src_row for s in seqs), np.int64, n)
+        fed = src >= 0
+        ids = np.fromiter((0 if s.src_row >= 0 else s.token_ids[-1] for s in seqs), np.int64, n)
+        if fed.any():
+            if prev_ids is None:
+                raise ValueError("decode rows take ids from the previous step, but it left none on the device")
+            if int(src.max()) >= prev_ids.numel():
+                raise ValueError(f"source row {int(src.max())} past the previous step's {prev_ids.numel()} ids")
         short = pos // self.block_size >= self._row_len[:n]
         if short.any() or (pos < 0).any():
             i = int(np.argmax(short | (pos < 0)))
@@ -211,6 +229,14 @@ class Batch:
         self.positions[:n].copy_(self._h_pos[:n], non_blocking=True)
         self.slot_mapping[:n].copy_(self._h_slot[:n], non_blocking=True)
         self.cache_seqlens[:n].copy_(self._h_csl[:n], non_blocking=True)
+        if fed.any():
+            rows = np.nonzero(fed)[0]
+            k = rows.size
+            feed = self._h_feed.numpy()
+            feed[0, :k], feed[1, :k] = rows, src[rows]
+            self._feed[:, :k].copy_(self._h_feed[:, :k], non_blocking=True)
+            got = prev_ids.view(-1).index_select(0, self._feed[1, :k]).clamp_(0, self.vocab_size - 1)
+            self.input_ids.index_copy_(0, self._feed[0, :k], got)
         self._sync_sampling(seqs)
         if self.cascade is not None:
             self._stage_cascade(n, pos + 1, pad_to or n)

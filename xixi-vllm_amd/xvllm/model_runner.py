@@ -11,6 +11,8 @@ batches it was recorded for.  Sampling parameters and the uniform draws are
 static buffers written before the replay."""
 from __future__ import annotations
 
+from collections import deque
+
 import torch
 
 from . import _C
@@ -103,8 +105,14 @@ class ModelRunner:
         self._decode_ids = torch.zeros(self.max_bs, dtype=torch.int64, device=self.device)
         self._uniforms = torch.zeros(self.max_bs, dtype=torch.float32, device=self.device)
         self._copy_stream = torch.cuda.Stream(device=self.device)
-        self._copy_event = torch.cuda.Event()
-        self._sample_cpu = torch.empty(self.max_bs * 2, dtype=torch.int64, pin_memory=True)
+        # two read-back slots (pinned ids + the event of their copy): a step's
+        # ids may still wait to be read while the next step is launched
+        self._readback = [(torch.empty(self.max_bs * 2, dtype=torch.int64, pin_memory=True), torch.cuda.Event())
+                          for _ in range(2)]
+        self._readback_next = 0
+        self._pending: deque = deque()  # (slot, n_p, n_d) of launched steps not read back yet
+        self._last_ids: torch.Tensor | None = None  # the last launched step's sampled ids, on the device
+        self.launched_steps = 0  # steps staged for read-back so far (device-fed inputs name the last one)
         self.graph_runner: HipGraphRunner | None = None
         self.cascade_graph_runner: HipGraphRunner | None = None
         self._sample_graphs: dict[tuple[int, int], torch.cuda.CUDAGraph] = {}
@@ -154,7 +162,7 @@ class ModelRunner:
     def _run_decode(self, seqs: list[SeqSchedule]) -> torch.Tensor:
         bs = len(seqs)
         pad_to = self.graph_runner._pad_bs(bs) if self.graph_runner is not None and bs <= self.max_bs else None
-        self.batch.build_decode(seqs, pad_to=pad_to)
+        self.batch.build_decode(seqs, pad_to=pad_to, prev_ids=self._last_ids)
         if pad_to is None:
             return self._sample_logits(self.decode_hidden(bs), bs)
         self.decode_hidden(bs)
@@ -240,33 +248,50 @@ class ModelRunner:
 
     def _stage_samples(self, p, d) -> tuple[int, int]:
         """Queue this step's sampled ids for the host: decode rows first, then
-        prefill rows, joined on the device and moved by one non-blocking copy
-        on the side stream, so the next step's launches do not wait for it."""
+        prefill rows, joined on the device (kept as the next step's source of
+        device-fed decode inputs) and moved by one non-blocking copy on the
+        side stream into a free read-back slot, so the next step's launches
+        do not wait for it.  At most two steps may wait to be read back."""
         n_d = 0 if d is None else d.numel()
         n_p = 0 if p is None else p.numel()
+        if len(self._pending) >= len(self._readback):
+            raise RuntimeError("two steps' ids are already waiting to be read back")
+        slot = self._readback_next
+        self._readback_next = (slot + 1) % len(self._readback)
+        cpu, event = self._readback[slot]
         side = self._copy_stream
         ids = None
         if n_d + n_p:
-            if self._sample_cpu.numel() < n_d + n_p:
-                self._sample_cpu = torch.empty(n_d + n_p, dtype=torch.int64, pin_memory=True)
+            if cpu.numel() < n_d + n_p:
+                cpu = torch.empty(n_d + n_p, dtype=torch.int64, pin_memory=True)
+                self._readback[slot] = (cpu, event)
             ids = torch.cat([t.view(-1) for t in (d, p) if t is not None])
         # the copy may start only after everything that produces `ids`,
         # the join included, has run on the compute stream
         side.wait_stream(torch.cuda.current_stream())
         if ids is not None:
             with torch.cuda.stream(side):
-                self._sample_cpu[: n_d + n_p].copy_(ids, non_blocking=True)
+                cpu[: n_d + n_p].copy_(ids, non_blocking=True)
             ids.record_stream(side)  # made on the compute stream, read on the side stream
-        self._copy_event.record(side)
+        event.record(side)
+        self._last_ids = ids
+        self._pending.append((slot, n_p, n_d))
+        self.launched_steps += 1
         return n_p, n_d
 
     def read_samples(self, n_p: int, n_d: int) -> tuple[list[int], list[int]]:
-        """(prefill ids, decode ids) of the step staged last.  Every id is
-        checked against [0, vocab) on the host before it is returned, so a
-        wrong id raises here instead of faulting the next step's embedding
-        gather when it is fed back."""
-        self._copy_event.synchronize()
-        ids = self._sample_cpu[: n_d + n_p].tolist()
+        """(prefill ids, decode ids) of the oldest launched step not read back
+        yet.  Every id is checked against [0, vocab) on the host before it is
+        returned; a wrong id raises here (the device-fed decode inputs of a
+        step launched meanwhile were clamped into range)."""
+        if not self._pending:
+            raise RuntimeError("no launched step is waiting to be read back")
+        slot, pp, dd = self._pending.popleft()
+        if (pp, dd) != (n_p, n_d):
+            raise ValueError(f"the oldest waiting step has {dd} decode + {pp} prefill rows, not {n_d} + {n_p}")
+        cpu, event = self._readback[slot]
+        event.synchronize()
+        ids = cpu[: n_d + n_p].tolist()
         bad = [(i, t) for i, t in enumerate(ids) if not 0 <= t < self.vocab_size]
         if bad:
             raise SampledIdOutOfRange(f"{len(bad)} sampled ids outside [0, {self.vocab_size}): "
