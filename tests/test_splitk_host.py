@@ -25,11 +25,21 @@ def test_split_views_sum_to_the_product(m, n, k, p):
 
 
 def test_split_table():
-    # Qwen3-8B o_proj (K 4096) and down_proj (K 12288) at decode batches
-    assert [split_factor(m, 4096, 4096) for m in (1, 8, 16, 32, 64, 128, 256)] == [4, 4, 4, 1, 1, 8, 1]
+    from xvllm.layers.linear import SPLIT_BUCKETS, SPLIT_TABLE, split_rule
+
+    # measured shapes: the entry of the smallest bucket holding m rows
+    assert [split_factor(m, 4096, 4096) for m in (1, 8, 16, 32, 64, 128, 256)] == [4, 4, 4, 1, 2, 2, 4]
     assert [split_factor(m, 4096, 12288) for m in (8, 16, 32, 64, 128, 256, 512)] == [1, 1, 4, 4, 8, 8, 1]
+    assert [split_factor(m, 5120, 8192) for m in (1, 32, 33, 48, 200)] == [1, 1, 8, 8, 4]
+    assert [split_factor(m, 5120, 25600) for m in (1, 32, 64, 96)] == [2, 2, 8, 4]
+    for (n, k), row in SPLIT_TABLE.items():
+        assert len(row) == len(SPLIT_BUCKETS)
+        assert all(p in (1, 2, 4, 8) and k % (p * 64) == 0 for p in row)  # the norm sums at most 8 partials
+    # other shapes: the rule
+    assert [split_factor(m, 4096, 8192) for m in (16, 32, 128)] == [split_rule(m, 4096, 8192) for m in (16, 32, 128)]
     # prefill-sized M, wide outputs and short K never split
     assert split_factor(8192, 4096, 12288) == 1
     assert split_factor(64, 24576, 4096) == 1
     assert split_factor(64, 1024, 3072) == 1
     assert split_factor(128, 4096, 4352) == 1  # K not a multiple of 8 x 64
+    assert split_factor(0, 4096, 4096) == 1

@@ -1,13 +1,13 @@
 """Dense GEMMs of the decoder: PyTorch (hipBLASLt) with a split-K form for
 the two whose output goes straight into a residual add + RMSNorm (o_proj and
 down_proj, reference src/compute/models/qwen3.py:64,115 feeding the norms of
-:150,:152), and, for decode batches of at most 64 rows, the weight-streaming
-gfx950 kernel (xv_dense_gemm) over packed weight tiles: gate_up fused with
-SiLU-and-mul, down and o as split-K partials for the same norm (dense_gemm
-and the streamed_* helpers at the end of this file; measured 11-27 % faster
-than the hipBLASLt forms below at M 8 and 64, weights streamed from HBM).
-The split-K measurements below are the hipBLASLt path, which larger batches
-and models without packed weights still take.
+:150,:152), and, opt-in for decode batches of at most 64 rows of a model with
+packed weights, the weight-streaming gfx950 kernel (xv_dense_gemm) over
+packed weight tiles: gate_up fused with SiLU-and-mul, down and o as split-K
+partials for the same norm (dense_gemm and the streamed_* helpers at the end
+of this file; measured 11-27 % faster than the hipBLASLt forms below at M 8
+and 64, weights streamed from HBM).  The split-K measurements below are the
+hipBLASLt path, the default.
 
 At decode batch sizes an [M, K] x [K, 4096] GEMM has few output tiles for 256
 CUs: hipBLASLt runs Qwen3-8B's o_proj (K 4096) and down_proj (K 12288) at
@@ -19,8 +19,10 @@ unsplit GEMM would have written) and continues as fused_add_rmsnorm.  The
 partials cost P x M x N x 4 bytes of extra reads in the norm, which the
 table below charges against the GEMM's gain.
 
-Measured on MI355X, graph replay, more than 1 GB of weights cycled so that
-none is served from the 256 MB last-level cache (us; unsplit -> split):
+The split per shape and batch size is SPLIT_TABLE, measured for the Qwen3-8B
+and Qwen3-32B weights; the first measurements, which set split_rule for other
+shapes (MI355X, graph replay, more than 1 GB of weights cycled so that none is
+served from the 256 MB last-level cache; us, unsplit -> split):
 
     down_proj  M 32: 28.2 -> 22.6 (P 4)   M 64: 37.5 -> 25.0 (P 4)
                M 128: 66.2 -> 27.3 (P 8)  M 256: 54.4 -> 36.0 (P 8)
@@ -38,6 +40,7 @@ layer at the largest serving batches.
 """
 from __future__ import annotations
 
+import bisect
 from typing import NamedTuple
 
 import torch
@@ -56,8 +59,27 @@ class PartialSums(NamedTuple):
         return self.parts.sum(0).to(torch.bfloat16)
 
 
-def split_factor(m: int, n: int, k: int) -> int:
-    """K slices for an [m, k] x [k, n] GEMM feeding a norm (1: no split)."""
+# The fastest K split per decode graph bucket (SPLIT_BUCKETS) for the o_proj
+# and down_proj weights of Qwen3-8B ([4096, 4096], [4096, 12288]) and
+# Qwen3-32B ([5120, 8192], [5120, 25600]), measured on MI355X by
+# `python -m xvllm.layers.split_tune` (the GEMM plus the norm that sums its
+# partials, graph replay, weights cycled past the last-level cache).
+# hipBLASLt's kernel choice makes the best split jump between neighbouring
+# sizes, so the table is taken as measured.  At Qwen3-32B's M 32 it runs
+# o_proj unsplit (27.6 us against 54.2 at P 4) and down_proj at P 2 (80.1
+# against 89.1 us).  Other shapes use split_rule.
+SPLIT_BUCKETS = (1, 2, 4, 8, 16, 32, 48, 64, 80, 96, 112, 128, 144, 160, 176, 192, 208, 224, 240, 256)
+SPLIT_TABLE = {
+    (4096, 4096): (4, 4, 4, 4, 4, 1, 1, 2, 2, 2, 2, 2, 2, 4, 2, 4, 2, 4, 2, 4),
+    (4096, 12288): (1, 1, 1, 1, 1, 4, 4, 4, 4, 4, 8, 8, 8, 8, 8, 8, 8, 8, 8, 8),
+    (5120, 8192): (1, 1, 1, 1, 1, 1, 8, 8, 1, 2, 4, 2, 2, 8, 2, 8, 4, 8, 4, 8),
+    (5120, 25600): (2, 2, 2, 2, 2, 2, 8, 8, 8, 4, 8, 8, 8, 8, 8, 8, 4, 8, 8, 8),
+}
+
+
+def split_rule(m: int, n: int, k: int) -> int:
+    """K slices for a shape outside SPLIT_TABLE (the Qwen3-8B measurements
+    above, generalised by K)."""
     if n > 8192 or k % (8 * 64):
         return 1
     if k >= 8192:
@@ -65,6 +87,18 @@ def split_factor(m: int, n: int, k: int) -> int:
     if k >= 4096:
         return 4 if m <= 16 else 8 if 96 <= m <= 192 else 1
     return 1
+
+
+def split_factor(m: int, n: int, k: int) -> int:
+    """K slices for an [m, k] x [k, n] GEMM feeding a norm (1: no split):
+    SPLIT_TABLE's entry for the smallest bucket of at least m rows, else
+    split_rule; above 256 rows, 1."""
+    if m < 1 or m > SPLIT_BUCKETS[-1]:
+        return 1
+    row = SPLIT_TABLE.get((n, k))
+    if row is None:
+        return split_rule(m, n, k)
+    return row[bisect.bisect_left(SPLIT_BUCKETS, m)]
 
 
 def linear_into_norm(x: torch.Tensor, w: torch.Tensor, split: bool = True):
