@@ -476,7 +476,9 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
     synthetic N(0,1) K/V (`serve(prefilled=True)`), and each request decodes
     from its last prompt token.  The timed region is `steps` whole serving
     steps (decode graph + LM head + sampler graphs, read-back of the ids, the
-    ledger's bookkeeping) after `warmup` steps.
+    ledger's bookkeeping; one step in flight) after `warmup` steps, timed on
+    the device's timeline between events recorded after each step's launches
+    (idle time between steps included).
     The 64 layers' KV (275 GB per sequence, 243 GB of unique pages) does not
     fit beside the 64 GB of weights, so the pool holds `pool_layers` layers and
     layer i reads pool layer i % pool_layers: every layer streams the same
@@ -539,15 +541,19 @@ def decode_config5(torch, dev, steps: int = 8, warmup: int = 2, pool_layers: int
         seen["cascade_rows"] = getattr(r.batch, "cascade_rows", 0)
 
     outs, st = serve(runner, prompts, gen, sampling=dict(temperature=1.0, top_p=0.95), max_num_seqs=bsz,
-                     prefilled=True, after_forward=after_forward)
+                     prefilled=True, timing_events=True, after_forward=after_forward)
     runner.destroy()
     assert st.hit_tokens == (shared - 1) * prefix, st.hit_tokens
     assert all(len(o) == gen for o in outs) and st.steps == gen
     cascade = seen["cascade_rows"] > 0
     if attention != "plain":  # 8192 shared tokens (32 / 16 MiB per layer) pass the gate
         assert seen["cascade_rows"] == shared, seen
-    t = st.step_end_s
-    ms = (t[-1] - t[warmup - 1]) / steps * 1e3
+    # device timeline from the end of the last warm-up step's launches to the
+    # end of the last step's: the host's read-back clock would count the final
+    # step's release of every request's pages (~15 ms of host bookkeeping), and
+    # a slow host (a profiler's) could shift its starting point
+    ev = st.step_events
+    ms = ev[warmup - 1].elapsed_time(ev[-1]) / steps
     wbytes = sum(p.numel() for n, p in model.named_parameters() if "embed_tokens" not in n) * 2
     per_tok_layer = cfg.num_key_value_heads * 128 * 2 * (1 if fp8 else 2)
     mean_ctx = ctx + warmup + (steps + 1) / 2  # contexts of the timed steps (prompt + tokens so far)

@@ -72,6 +72,9 @@ class ServeStats:
     host_s: float = 0.0          # host time scheduling and launching steps
     wall_s: float = 0.0
     step_end_s: list[float] = field(default_factory=list)  # when each step's ids were read back, since the start
+    # a timing event recorded on the compute stream after each step's launches
+    # (device-timeline step times: elapsed_time between two of them)
+    step_events: list = field(default_factory=list)
     # per step: (decode rows, sum of their context lengths incl. the new token,
     # prefill tokens, prefill attention query-key pairs under the causal mask,
     # prefill rows sampled)
@@ -90,7 +93,8 @@ class _Step:
 def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None = None,
           max_num_seqs: int = 256, max_num_batched_tokens: int = 8192, num_pages: int | None = None,
           prefix_cache: bool = True, prefilled: bool = False, kv_manager: KVManager | None = None,
-          overlap: bool = True, after_forward: Callable[[object, int, int], None] | None = None,
+          overlap: bool = True, timing_events: bool = False,
+          after_forward: Callable[[object, int, int], None] | None = None,
           after_step: Callable[[KVManager, list[Request]], None] | None = None
           ) -> tuple[list[list[int]], ServeStats]:
     """Generate `gen` tokens for every prompt; returns (outputs, stats).
@@ -100,7 +104,10 @@ def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None =
     handed out (default: all of the runner's pool).  prefix_cache: reuse
     cached prompt prefixes (the page ledger's radix cache); kv_manager: a
     ledger to use (and keep) instead of a new one.  overlap: keep one step in
-    flight (module docstring).
+    flight (module docstring).  timing_events: record a timing event after
+    each step's launches (ServeStats.step_events), so that step times can be
+    read on the device's timeline, which a slow host (a profiler's) cannot
+    shorten the way it can shift read-back times.
     prefilled: the pool already holds the KV of every prompt token but the
     last (synthetic pages for a long-context decode measurement, whose prefill
     would dominate the run): admission allocates and matches pages as usual
@@ -196,6 +203,10 @@ def serve(runner, prompts: list[list[int]], gen: int, *, sampling: dict | None =
                              sum(1 for _, _, done in preqs if done)))
         n_p, n_d = runner.run_forward(decodes, prefills)
         launched_at = runner.launched_steps
+        if timing_events:
+            ev = torch.cuda.Event(enable_timing=True)
+            ev.record()
+            st.step_events.append(ev)
         step = _Step(serial, n_p, n_d, dreqs, preqs)
         # what the launched step writes and samples (its ids arrive later)
         for row, r in enumerate(dreqs):
