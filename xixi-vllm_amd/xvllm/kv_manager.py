@@ -193,15 +193,20 @@ class KVManager:
         self._hashes.pop(seq_id, None)
         self._prompt_chain.pop(seq_id, None)
         self._stopped.discard(seq_id)
-        for p in block_table:
-            self.ref[p] -= 1
-            if self.ref[p] < 0:
-                raise AssertionError(f"page {p} released more often than it was taken")
-            if self.ref[p] == 0:
-                if self.cache is not None and self.cache.holds(p):
-                    self.cached.add(p)
-                else:
-                    self.free.append(p)
+        bt = np.asarray(block_table, np.int64)
+        if bt.size == 0:
+            return
+        np.subtract.at(self.ref, bt, 1)  # a table lists a page once, but count repeats right anyway
+        if (self.ref[bt] < 0).any():
+            p = int(bt[np.argmax(self.ref[bt] < 0)])
+            raise AssertionError(f"page {p} released more often than it was taken")
+        released = dict.fromkeys(bt[self.ref[bt] == 0].tolist())  # in table order, once each
+        if self.cache is None:
+            self.free.extend(released)
+            return
+        held = self.cache.held(released)
+        self.cached |= held
+        self.free.extend(p for p in released if p not in held)
 
     # ------------------------------------------------------------ checks
     def check(self, live_tables: dict[int, list[int]] | None = None) -> None:

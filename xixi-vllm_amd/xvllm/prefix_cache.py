@@ -176,6 +176,10 @@ class RadixPrefixCache:
     def holds(self, page: int) -> bool:
         return page in self._page_node
 
+    def held(self, pages) -> set[int]:
+        """The pages of `pages` the tree holds."""
+        return self._page_node.keys() & set(pages)
+
     # ------------------------------------------------------------ eviction
     def evict(self, n_pages: int) -> list[int]:
         """Free unpinned leaves, least recently used first, a whole leaf at a
