@@ -1,7 +1,8 @@
 """Split-K o_proj / down_proj feeding the residual add + RMSNorm, on the GPU:
 the partial-sum norm kernel equals fused_add_rmsnorm on the bf16 sum of the
 partials bit for bit, the split GEMM + norm equals the unsplit chain within
-the bf16 tolerance at Qwen3-8B widths and decode batch sizes, and a decode
+the bf16 tolerance at the Qwen3-8B and -32B o_proj / down_proj shapes and
+decode batch sizes (every split the measured table picks there), and a decode
 step of a Qwen3-8B-width model (graphs, two layers) agrees with split-K off."""
 
 import numpy as np
@@ -58,8 +59,8 @@ def test_parts_norm_rejects_bad_arguments(dev):
         torch.ops.xv.fused_add_rmsnorm_parts(torch.zeros((9, 4, 4096), device=dev), r, w, 1e-6)
 
 
-@pytest.mark.parametrize("m", [8, 64, 128, 256])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 12288)])
+@pytest.mark.parametrize("m,n,k", [(m, n, k) for n, k in ((4096, 4096), (4096, 12288)) for m in (8, 64, 128, 256)]
+                         + [(m, n, k) for n, k in ((5120, 8192), (5120, 25600)) for m in (8, 32, 48, 96, 200)])
 def test_split_linear_into_norm_matches_unsplit(dev, m, n, k):
     from xvllm.layers.layernorm import RMSNorm
     from xvllm.layers.linear import PartialSums, linear_into_norm, split_factor
