@@ -950,15 +950,11 @@ XV_INLINE void merge_general(int n, PV part_vals, PL part_lse, float lse_lane, b
   const float la = lane < n ? (HAVE_LANE ? lse_lane : part_lse(lane)) : -INFINITY;
   const float lb = 64 + lane < n ? part_lse(64 + lane) : -INFINITY;
   const float lc = 128 + lane < n ? part_lse(128 + lane) : -INFINITY;
-  float mx = fmaxf(la, fmaxf(lb, lc));
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  const float mx = wave_max(fmaxf(la, fmaxf(lb, lc)));
   const float wa = lane < n ? __builtin_amdgcn_exp2f(la - mx) : 0.f;
   const float wb = 64 + lane < n ? __builtin_amdgcn_exp2f(lb - mx) : 0.f;
   const float wc = 128 + lane < n ? __builtin_amdgcn_exp2f(lc - mx) : 0.f;
-  float den = wa + wb + wc;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
+  const float den = wave_sum(wa + wb + wc);
   const int g = lane >> 4, i = lane & 15;  // group g: partials g, g + 4, ...; dims 8i .. 8i + 7
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   auto load = [&](float4 (&v)[8][2], int j0) {
@@ -968,14 +964,20 @@ XV_INLINE void merge_general(int n, PV part_vals, PL part_lse, float lse_lane, b
     }
   };
   auto fold = [&](const float4 (&v)[8][2], int j0) {
+    // partial j's weight sits in lane j mod 64 of the register of its
+    // 64-block; a batch (32 partials from j0, a multiple of 32) lies in one
+    // block, and group g's partial of step k is j0 + 4k + g: four lane reads
+    // into scalars, one per group
+    const float wsrc = j0 < 64 ? wa : j0 < 128 ? wb : wc;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-      // partial j's weight sits in lane j mod 64, in the register of its
-      // 64-block; j differs between groups, so fetch all three and pick
       const int j = j0 + 4 * k + g;
-      const int jj = j & 63;
-      const float w_a = __shfl(wa, jj), w_b = __shfl(wb, jj), w_c = __shfl(wc, jj);
-      const float w = j < n ? (j < 64 ? w_a : j < 128 ? w_b : w_c) : 0.f;
+      const int s0 = (j0 + 4 * k) & 63;
+      const float w0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), s0));
+      const float w1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), s0 + 1));
+      const float w2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), s0 + 2));
+      const float w3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(wsrc), s0 + 3));
+      const float w = j < n ? (g == 0 ? w0 : g == 1 ? w1 : g == 2 ? w2 : w3) : 0.f;
       acc[0] += w * v[k][0].x; acc[1] += w * v[k][0].y; acc[2] += w * v[k][0].z; acc[3] += w * v[k][0].w;
       acc[4] += w * v[k][1].x; acc[5] += w * v[k][1].y; acc[6] += w * v[k][1].z; acc[7] += w * v[k][1].w;
     }
@@ -991,10 +993,7 @@ XV_INLINE void merge_general(int n, PV part_vals, PL part_lse, float lse_lane, b
     }
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    acc[e] += __shfl_xor(acc[e], 16);
-    acc[e] += __shfl_xor(acc[e], 32);
-  }
+  for (int e = 0; e < 8; ++e) acc[e] = xor32_sum(xor16_sum(acc[e]));
   if (g == 0) {
     const float inv = 1.0f / den;
     uint32_t* o = reinterpret_cast<uint32_t*>(orow + 8 * i);

@@ -121,18 +121,8 @@ template <int N>
 XV_INLINE float row_bcast(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + N, 0xf, 0xf, false));
 }
-// Full wave64 reductions (result valid in every lane).
-XV_INLINE float wave_sum(float x) {
-  x = row16_sum(x);
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
-}
-XV_INLINE float wave_max(float x) {
-  x = row16_max(x);
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
-}
+// Full wave64 reductions (result valid in every lane), all in registers.
+XV_INLINE float wave_sum(float x) { return xor32_sum(xor16_sum(row16_sum(x))); }
+XV_INLINE float wave_max(float x) { return xor32_max(xor16_max(row16_max(x))); }
 
 #define XV_CHECK_LAUNCH() do { hipError_t e_ = hipGetLastError(); if (e_ != hipSuccess) return (int)e_; } while (0)
