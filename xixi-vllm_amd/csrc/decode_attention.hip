@@ -815,12 +815,11 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
       pref[b + 1] = carry + inc;
       sl[b] = ctx;
     }
-    carry += __shfl(inc, 63);
+    carry += __builtin_amdgcn_readlane(inc, 63);
   }
   if (lane == 0) pref[0] = 0;
   __syncthreads();  // single wave: orders the LDS writes before the reads
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) max_np = max(max_np, __shfl_xor(max_np, m));
+  max_np = (int)wave_max((float)max_np);  // page counts are exact in fp32 (below 2^24)
   const int64_t total = (int64_t)a.hkv * carry;
   const int L = range_pages(a, total, max_np);
   const int64_t f0 = (int64_t)blockIdx.x * L;
