@@ -1092,12 +1092,7 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
       }
     }
   }
-  unsigned long long best = greedy_word(fm, bid, nid);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long y = __shfl_xor(best, o);
-    best = y > best ? y : best;
-  }
+  unsigned long long best = wave_max_ull(greedy_word(fm, bid, nid));
   __shared__ unsigned long long wbest[kGreedyThreads / 64];
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
   __syncthreads();
