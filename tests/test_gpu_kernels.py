@@ -372,6 +372,36 @@ def test_sampler_bitexact(dev, name, b, v, flags, temp, top_p, top_k, min_p, tie
     assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
 
 
+@pytest.mark.parametrize("b", [32, 64])
+def test_sampler_chain_cut_cases_bitexact(dev, b):
+    """The multi-workgroup path's cut on its own cases, against the C oracle:
+    near-flat rows whose top-p cut splits a tie group of one key (under and
+    over the 512 ids the per-key cut ranks itself; the sort takes the larger),
+    wide rows, min-p cuts and both together, seeded uniforms, B 32 and 64."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    rng = np.random.default_rng(77 + b)
+    v = 151936
+    for case, (std, temp, top_p, min_p, flags) in enumerate([
+            (0.05, 1.0, 0.95, 0.0, 4), (0.002, 1.0, 0.9, 0.0, 4), (0.01, 0.7, 0.6, 0.0, 4),
+            (1.0, 1.0, 0.9, 0.0, 4), (3.0, 0.8, 0.99, 0.0, 4), (0.05, 1.0, 1.0, 0.97, 8),
+            (0.3, 1.0, 1.0, 0.5, 8), (0.02, 1.0, 0.8, 0.99, 4 | 8), (1.0, 0.5, 0.7, 0.01, 4 | 8)]):
+        x = (rng.standard_normal((b, v)) * std).astype(np.float32)
+        logits = torch.from_numpy(x).to(torch.bfloat16)
+        temps = torch.full((b,), temp)
+        tps = torch.from_numpy(np.clip(rng.normal(top_p, 0.02, b), 0.05, 1.0).astype(np.float32)) \
+            if top_p < 1.0 else torch.ones(b)
+        mps = torch.full((b,), min_p)
+        u = torch.from_numpy(rng.random(b).astype(np.float32))
+        want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), None,
+                        mps.numpy(), u.numpy(), flags)
+        print(f"chain cut case {case}: std {std} T {temp} p {top_p} min_p {min_p} B {b}", flush=True)
+        got = sample(logits.to(dev), temps.to(dev), tps.to(dev), None, mps.to(dev), u.to(dev),
+                     use_top_p=bool(flags & 4), use_min_p=bool(flags & 8))
+        assert np.array_equal(got.cpu().numpy(), want), (case, np.nonzero(got.cpu().numpy() != want)[0][:8])
+
+
 def test_sampler_nan_rows_paths_agree(dev):
     """Rows with NaN logits (some, all) and a row of equal logits: the
     multi-workgroup path gives the ids of the one-workgroup path."""

@@ -3,7 +3,7 @@
 // arithmetic below: one 1024-thread workgroup per row (sample_kernel), the
 // all-greedy argmax over several workgroups per row (greedy_segment_kernel),
 // the sampled path over several workgroups per row for batches of up to
-// kSegMaxBatch rows (the seg_* / row_* chain), and for calls whose every
+// kSegMaxBatch rows (seg_stats / seg_hist / row_finish), and for calls whose every
 // top_k is at most 64 a two-launch top-k path (seg_topk / row_topk); all give
 // the same ids.
 //
@@ -158,6 +158,7 @@ struct Shared {
   uint32_t red_u[kWaves];
   float red_f[kWaves];
   int64_t red_l[kWaves];
+  int64_t red_l2[kWaves];
   uint32_t cnt[256];
   unsigned long long mass[256];
   // broadcast slots
@@ -344,6 +345,32 @@ XV_INLINE int64_t block_excl_scan(Shared& s, int64_t x, int64_t* total) {
   }
   *total = tot;
   return before + inc - x;
+}
+
+// Two exclusive prefix sums over the block at once (one pair of barriers).
+XV_INLINE void block_excl_scan2(Shared& s, int64_t x, int64_t y, int64_t* ex, int64_t* ey, int64_t* tx,
+                                int64_t* ty) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t ix = wave_incl_scan_l(x), iy = wave_incl_scan_l(y);
+  __syncthreads();
+  if (lane == 63) {
+    s.red_l[w] = ix;
+    s.red_l2[w] = iy;
+  }
+  __syncthreads();
+  int64_t bx = 0, by = 0, sx = 0, sy = 0;
+  for (int i = 0; i < kWaves; ++i) {
+    if (i < w) {
+      bx += s.red_l[i];
+      by += s.red_l2[i];
+    }
+    sx += s.red_l[i];
+    sy += s.red_l2[i];
+  }
+  *ex = bx + ix - x;
+  *ey = by + iy - y;
+  *tx = sx;
+  *ty = sy;
 }
 
 struct Boundary {
@@ -1123,24 +1150,25 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
 // Sampled rows over several workgroups per row (batches given a workspace).
 //
 // A row is cut into R segments of whole 8-id vectors, one kSegThreads
-// workgroup each, and the one-workgroup algorithm above runs as a chain of
+// workgroup each, and the one-workgroup algorithm above runs as three
 // launches (a launch boundary makes one kernel's global writes visible to the
 // next, across XCDs):
 //   1. seg_stats:  per segment, the largest and smallest key and the greedy best;
 //   2. seg_hist:   per segment, bucket counts and masses, the min-p key, and the
 //                  segment's total mass (its kept mass when the row has no cut);
-//   3. row_plan:   per row, the summed histograms give the bucket(s) holding the
-//                  cut-offs (greedy and all-NaN rows finish here);
-//   4. seg_gather: the candidates of those buckets, appended to the row's list;
-//   5. row_cut:    per row, the sorted list gives the exact cut and the kept
-//                  mass (top-k rows draw from the list and finish); a row whose
-//                  buckets hold more candidates than LDS runs sample_row.  Each
-//                  segment's kept mass follows without another pass over the
-//                  logits: its masses of the buckets before the cut's bucket
-//                  (every candidate there is kept) plus its candidates in the
-//                  sorted list up to the cut (exact integer sums of the same
-//                  per-candidate masses);
-//   6. row_draw:   per row, the segment holding floor(u * M), then the id in it.
+//   3. row_finish: per row, one 1024-thread workgroup: the summed histograms
+//                  give the bucket(s) holding the cut-offs (greedy and all-NaN
+//                  rows finish here); the workgroup gathers those buckets'
+//                  candidates from the row into LDS, makes the exact cut (by
+//                  per-key counts, or a sort) and the kept mass (top-k rows
+//                  draw from the list and finish), then draws: the segment
+//                  holding floor(u * M), then the id in it.  A row whose
+//                  buckets hold more candidates than LDS runs sample_row.
+//                  Each segment's kept mass follows without another pass over
+//                  the logits: its masses of the buckets before the cut's
+//                  bucket (every candidate there is kept) plus its candidates
+//                  up to the cut (exact integer sums of the same per-candidate
+//                  masses).
 // Buckets, masses, cuts and the draw are those of the one-workgroup path, so
 // the ids are identical to it.
 
@@ -1167,7 +1195,6 @@ struct __attribute__((aligned(128))) RowPlan {
   int use_k;           // the list is the top-k candidates (draw from the list)
   int cut_p, cut_m;    // the top-p / min-p cut falls in the gathered bucket
   uint32_t kminp;      // min-p key (0xffffffff: none)
-  uint32_t cand_count; // appended by seg_gather
   uint32_t key_cut;
   uint32_t klo, khi;   // keys of buckets lo..hi: exactly [klo, khi]
   float zmax, inv_t, bs;
@@ -1184,7 +1211,6 @@ struct SegArgs {
   const float* min_ps;
   const float* uniforms;
   int64_t* out_ids;
-  RowPlan* plans;               // [B]
   uint32_t* seg_kmax;           // [B * R]
   uint32_t* seg_kmin;           // [B * R]
   uint32_t* seg_minp;           // [B * R]
@@ -1428,187 +1454,13 @@ __global__ __launch_bounds__(kSegThreads) void seg_hist_kernel(SegArgs a) {
   if (t == kBuckets - 1) { c += (uint32_t)far_c; m += (unsigned long long)far_m; }
   a.seg_cnt[o + t] = c;
   if (!p.use_k) a.seg_mass[o + t] = m;  // top-k rows take their masses from the list
-  // the segment's total mass: its kept mass if the row has no cut (row_cut
-  // replaces it for rows it cuts; top-k rows never reach the draw)
+  // the segment's total mass: its kept mass if the row has no cut (rows with
+  // a cut take theirs from the cut; top-k rows never reach the draw)
   const int64_t total = seg_sum_l(red, p.use_k ? 0 : (int64_t)m);
   if (t == 0) {
     a.seg_minp[b * a.R + r] = kminp;
     a.seg_kept[b * a.R + r] = total;
   }
-}
-
-// One thread per bucket (kSegThreads == kBuckets).
-__global__ __launch_bounds__(kSegThreads) void row_plan_kernel(SegArgs a) {
-  static_assert(kSegThreads == kBuckets, "one thread per bucket");
-  __shared__ SegRed red;
-  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63;
-  RowPlan& plan = a.plans[b];
-  // Every load the plan can need goes out before any is used: one memory
-  // round trip instead of one per dependent step.  Segment indices past R
-  // reload segment R-1 (no branch between the loads) and are masked below;
-  // entries a row's path did not write this call are loaded and ignored.
-  uint32_t c_all[kMaxSegs];
-  unsigned long long m_all[kMaxSegs];
-#pragma unroll
-  for (int j = 0; j < kMaxSegs; ++j) {
-    const int64_t o = ((int64_t)b * a.R + min(j, a.R - 1)) * kBuckets + t;
-    c_all[j] = a.seg_cnt[o];
-    m_all[j] = a.seg_mass[o];
-  }
-  const int sl = min(lane, a.R - 1);
-  const uint32_t kmax_l = a.seg_kmax[b * a.R + sl], kmin_l = a.seg_kmin[b * a.R + sl];
-  const uint32_t minp_l = a.seg_minp[b * a.R + sl];
-  const unsigned long long best_l = a.seg_best[b * a.R + min(t, a.R - 1)];
-  const RowParams p = row_params(a, b);
-  if (p.greedy) {
-    unsigned long long best = t < a.R ? best_l : 0ull;
-    best = seg_max_ull(red, best);
-    if (t == 0) {
-      a.out_ids[b] = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
-      plan.status = kPlanDone;
-    }
-    return;
-  }
-  const RowConsts rc = row_consts_of(lane < a.R ? kmax_l : 0u, lane < a.R ? kmin_l : 0xffffffffu, p.temp);
-  if (rc.kmax == 0) {  // every logit NaN: nothing has mass
-    if (t == 0) {
-      a.out_ids[b] = 0;
-      plan.status = kPlanDone;
-    }
-    return;
-  }
-  int64_t cnt = 0, mass = 0;
-#pragma unroll
-  for (int j = 0; j < kMaxSegs; ++j)
-    if (j < a.R) {
-      cnt += c_all[j];
-      mass += p.use_k ? 0 : (int64_t)m_all[j];
-    }
-  const uint32_t kminp = wave_min_u(lane < a.R ? minp_l : 0xffffffffu);
-  const int64_t cnt_incl = seg_incl_scan(red, cnt);
-  const int64_t mass_incl = seg_incl_scan(red, mass);
-  const int64_t total = seg_sum_l(red, mass);
-  int status = kPlanDraw, lo = 0, hi = 0, cut_p = 0, cut_m = 0;
-  int64_t thr = 0, mp_before = 0, m_before = 0;
-  if (p.use_k) {
-    // rank k-1 lies in the first bucket whose inclusive count reaches k
-    const int bk = (int)seg_min_l(red, cnt_incl >= p.top_k ? t : kBuckets);
-    __syncthreads();
-    if (t == bk) red.l[0] = cnt_incl;  // candidates in buckets 0..bk
-    __syncthreads();
-    const int64_t upto = bk < kBuckets ? red.l[0] : 0;
-    status = (bk >= kBuckets - 1 || upto > kMaxCand) ? kPlanFallback : kPlanGather;
-    lo = 0;
-    hi = bk;
-  } else if (p.use_p || p.use_m) {
-    int bp = kBuckets;
-    if (p.use_p) {
-      thr = (int64_t)floor((double)p.top_p * (double)total);
-      bp = (int)seg_min_l(red, mass_incl > thr ? t : kBuckets);
-    }
-    int bm = kBuckets;
-    if (p.use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), rc.inv_t, rc.zmax), rc.bs);
-    const int bf = min(bp, bm);
-    if (bf < kBuckets) {
-      __syncthreads();
-      if (t == bf) {
-        red.l[0] = cnt;
-        red.l[1] = mass_incl - mass;  // mass of the buckets before bf
-      }
-      __syncthreads();
-      const int64_t nbf = red.l[0];
-      m_before = red.l[1];
-      mp_before = m_before;
-      status = nbf > kMaxCand ? kPlanFallback : kPlanGather;
-      lo = hi = bf;
-      cut_p = bp == bf;
-      cut_m = bm == bf;
-    }
-  }
-  if (t == 0) {
-    if (status == kPlanGather) {
-      // Buckets fall as keys rise over the keys of non-NaN values, [1, 0xff80]
-      // (+inf), so buckets lo..hi hold exactly the keys of an interval; find
-      // its ends with the same bucket function.
-      constexpr uint32_t kInfKey = 0xff80u;
-      auto bkt = [&](uint32_t k) { return bucket_of(log2_ratio(key_to_bits(k), rc.inv_t, rc.zmax), rc.bs); };
-      uint32_t l = 1, h = kInfKey;  // smallest key with bucket <= hi
-      if (bkt(kInfKey) > hi) {
-        l = kInfKey + 1;  // empty (cannot happen: the plan's buckets are non-empty)
-      } else {
-        while (l < h) {
-          const uint32_t m = (l + h) >> 1;
-          if (bkt(m) <= hi) h = m; else l = m + 1;
-        }
-      }
-      plan.klo = l;
-      l = 1; h = kInfKey;             // largest key with bucket >= lo
-      if (bkt(1) < lo) {
-        plan.khi = 0u;  // empty (cannot happen: the plan's buckets are non-empty)
-      } else {
-        while (l < h) {
-          const uint32_t m = (l + h + 1) >> 1;
-          if (bkt(m) >= lo) l = m; else h = m - 1;
-        }
-        plan.khi = l;
-      }
-    }
-    plan.status = status;
-    plan.lo = lo;
-    plan.hi = hi;
-    plan.use_k = p.use_k;
-    plan.cut_p = cut_p;
-    plan.cut_m = cut_m;
-    plan.kminp = kminp;
-    plan.cand_count = 0;
-    plan.zmax = rc.zmax;
-    plan.inv_t = rc.inv_t;
-    plan.bs = rc.bs;
-    plan.thr = thr;
-    plan.mp_before = mp_before;
-    plan.m_before = m_before;
-    plan.key_cut = 1u;  // no cut: every candidate kept
-    plan.id_cut = kTieAll;
-    plan.M = total;
-  }
-}
-
-// Two passes over the segment (the second from L2): count the candidates of
-// the plan's key interval, reserve their slots in the row's list with one atomic per
-// workgroup, then write them.  No LDS staging, so occupancy stays high.
-__global__ __launch_bounds__(kSegThreads) void seg_gather_kernel(SegArgs a) {
-  __shared__ SegRed red;
-  __shared__ uint32_t base_lds;
-  const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x;
-  const RowPlan plan = a.plans[b];  // read fields in one round trip (the count is reserved through a.plans)
-  if (plan.status != kPlanGather) return;
-  const uint32_t klo = plan.klo, khi = plan.khi;
-  const bf16_t* row = a.logits + (int64_t)b * a.stride;
-  const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
-  const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
-  auto in_plan = [&](uint32_t bits) {
-    const uint32_t key = order_key(bits);  // 0 (NaN) is below klo >= 1
-    return key >= klo && key <= khi;
-  };
-  int64_t mine = 0;
-  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) { mine += in_plan(bits); });
-  const int64_t incl = seg_incl_scan(red, mine);
-  __syncthreads();
-  if (t == kSegThreads - 1) {
-    base_lds = incl ? __hip_atomic_fetch_add(&a.plans[b].cand_count, (uint32_t)incl, __ATOMIC_RELAXED,
-                                             __HIP_MEMORY_SCOPE_AGENT)
-                    : 0u;
-  }
-  __syncthreads();
-  if (mine == 0) return;
-  int64_t slot = (int64_t)base_lds + incl - mine;
-  unsigned long long* dst = a.cand + (int64_t)b * a.cand_stride;
-  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int id) {
-    if (!in_plan(bits)) return;
-    if (slot < kMaxCand)
-      dst[slot] = ((unsigned long long)order_key(bits) << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
-    ++slot;
-  });
 }
 
 // List operations on at most 64 candidates held one per lane, by one wave
@@ -1633,11 +1485,11 @@ XV_INLINE int64_t wave_first(bool pred, int64_t none) {
   return m ? (int64_t)__builtin_ctzll(m) : none;
 }
 
-// row_cut for a list of n <= 64 candidates, wave 0 alone: the same cut, kept
+// The cut of a list of n <= 64 candidates, wave 0 alone: the same cut, kept
 // mass and draw as the workgroup list functions.
 // c: this lane's candidate (0 past n), in any order.
-// segk: per segment, the kept mass of the buckets before the cut's (rows
-// without top-k; the list's part is added here and the sums written out).
+// segk: per segment in LDS, the kept mass of the buckets before the cut's
+// (rows without top-k; the list's part is added here).
 XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
                                  unsigned long long c, unsigned long long* segk) {
   const int lane = threadIdx.x & 63;
@@ -1686,8 +1538,6 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
   }
   // each segment's kept mass: its earlier buckets plus its listed candidates up to the cut
   if (lane <= jcut) atomicAdd(&segk[cand_id(c) / a.seg_len], (unsigned long long)q);
-  __builtin_amdgcn_wave_barrier();  // the wave's LDS operations stay in order
-  if (lane < a.R) a.seg_kept[b * a.R + lane] = (int64_t)segk[lane];
   if (lane == 0) {
     plan.key_cut = cand_key(edge);
     plan.id_cut = cand_id(edge);
@@ -1696,107 +1546,145 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
   }
 }
 
-XV_INLINE void row_cut_wave(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
-                            unsigned long long* segk) {
-  const int lane = threadIdx.x & 63;
-  row_cut_wave_list(a, plan, p, b, n, lane < n ? a.cand[(int64_t)b * a.cand_stride + lane] : 0ull, segk);
-}
-
-__global__ __launch_bounds__(kThreads) void row_cut_kernel(SegArgs a) {
-  __shared__ Shared s;
-  __shared__ FastShared fs;
-  const int b = blockIdx.x, t = threadIdx.x;
-  RowPlan& plan = a.plans[b];
-  int status = plan.status;
-  // a gathered list is never empty (the cut's bucket holds its own boundary
-  // candidate); should it be, the one-workgroup path takes the row
-  if (status == kPlanGather && plan.cand_count == 0u) status = kPlanFallback;
-  if (status == kPlanFallback) {
-    sample_row(s, fs, b, a.logits, a.stride, a.V, a.temps, a.top_ps, a.top_ks, a.min_ps, a.uniforms,
-               a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
-    __syncthreads();
-    if (t == 0) plan.status = kPlanDone;
-    return;
-  }
-  if (status != kPlanGather) return;
-  const RowParams p = row_params(a, b);
+// The cut of a gathered bucket list of a row without top-k, by per-key counts
+// instead of a sort.  A candidate's mass depends on its key alone and the
+// list's order is key descending, ties by ascending id, so a prefix of the
+// list is a key plus the number of that key's lowest ids, and the mass before
+// a key is a sum of count x mass over the keys above it.  Bin j of the count
+// array holds key khi - j.  Returns false, having written nothing, when the
+// keys span more bins than the array holds or the cut splits a tie group of
+// more than kTieRank ids (the sort then takes the list); the result is the
+// sort's in every other case.
+constexpr int kKeyBins = kWaves * kBuckets;  // the per-wave histograms' LDS, unused here
+constexpr int kTieRank = 512;
+XV_INLINE bool row_cut_by_keys(const SegArgs& a, RowPlan& plan, Shared& s, FastShared& fs, int b, int n,
+                               uint32_t* tie_ids, unsigned long long* segk) {
+  const int t = threadIdx.x;
+  const uint32_t klo = plan.klo, khi = plan.khi;
+  if (khi < klo || khi - klo >= (uint32_t)kKeyBins) return false;
+  const int K = (int)(khi - klo) + 1;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
-  const int n = (int)min(plan.cand_count, (uint32_t)kMaxCand);
-  // Rows without top-k: per segment, the mass of the buckets before the cut's
-  // bucket, all of whose candidates are kept (the list's part is added
-  // below).  Those masses and a long list load in the same memory round trip.
-  __shared__ unsigned long long segk[kMaxSegs];
-  constexpr int kPer = kMaxSegs * kBuckets / kThreads;
-  static_assert(kPer * kThreads == kMaxSegs * kBuckets, "segment x bucket entries per thread");
-  const bool per_seg = !plan.use_k;
-  const int lo = plan.lo, nlo = per_seg ? a.R * lo : 0;
-  unsigned long long pm[kPer];
-#pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int idx = t + k * kThreads, r = idx / max(lo, 1);
-    pm[k] = idx < nlo ? a.seg_mass[((int64_t)b * a.R + r) * kBuckets + (idx - r * lo)] : 0ull;
-  }
-  if (n > 64) {
-    const unsigned long long* src = a.cand + (int64_t)b * a.cand_stride;
-    for (int i = t; i < n; i += kThreads) fs.cand[i] = src[i];
-  }
-  if (per_seg) {
-    if (t < kMaxSegs) segk[t] = 0ull;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int idx = t + k * kThreads;
-      if (idx < nlo) atomicAdd(&segk[idx / lo], pm[k]);
-    }
-  }
+  uint32_t* kcnt = &fs.wcnt[0][0];
+  for (int j = t; j < K; j += kThreads) kcnt[j] = 0u;
   __syncthreads();
-  if (n <= 64) {
-    if (t < 64) row_cut_wave(a, plan, p, b, n, segk);
-    return;
-  }
-  sort_cand_desc(fs, n);
-  int64_t jcut;
-  if (plan.use_k) {
-    // the list is every candidate down to rank k-1 (as topk_boundary)
-    const int64_t total_k = list_mass_prefix(s, fs, n, p.top_k, inv_t, zmax);
-    jcut = (int64_t)p.top_k - 1;
-    if (p.use_p) {
-      const int64_t thr = (int64_t)floor((double)p.top_p * (double)total_k);
-      jcut = min(jcut, list_first_exceed(s, fs, n, 0, thr, inv_t, zmax));
+  for (int i = t; i < n; i += kThreads) atomicAdd(&kcnt[khi - cand_key(fs.cand[i])], 1u);
+  __syncthreads();
+  constexpr int kPerT = kKeyBins / kThreads;  // consecutive bins of one thread
+  static_assert(kPerT * kThreads == kKeyBins, "bins per thread");
+  const int j0 = t * kPerT;
+  uint32_t c[kPerT];
+  int64_t m[kPerT];
+  int64_t local = 0;
+  int64_t first = kTieAll, last = -1;  // present bins of this thread
+#pragma unroll
+  for (int k = 0; k < kPerT; ++k) {
+    const int j = j0 + k;
+    c[k] = j < K ? kcnt[j] : 0u;
+    m[k] = c[k] ? mass_of(exp_of(key_to_bits(khi - (uint32_t)j), inv_t, zmax)) : 0;
+    local += (int64_t)c[k] * m[k];
+    if (c[k]) {
+      first = first < j ? first : j;
+      last = j;
     }
+  }
+  int64_t list_mass;  // unused
+  const int64_t before = block_excl_scan(s, local, &list_mass);  // mass of the bins before this thread's
+  // cut position (bin << 32 | ties kept): kTieAll keeps the whole list, -1 only its first candidate
+  int64_t pos = kTieAll;
+  if (plan.cut_p) {  // first candidate whose inclusive mass (after the earlier buckets') exceeds thr
+    const int64_t thr = plan.thr;
+    int64_t cum = plan.mp_before + before, found = kTieAll;
+#pragma unroll
+    for (int k = 0; k < kPerT; ++k) {
+      const int64_t w = (int64_t)c[k] * m[k];
+      if (found == kTieAll && c[k] && cum + w > thr) {
+        int64_t i = m[k] > 0 ? (thr - cum) / m[k] + 1 : 1;
+        i = i < 1 ? 1 : (i > (int64_t)c[k] ? (int64_t)c[k] : i);
+        found = ((int64_t)(j0 + k) << 32) | i;
+      }
+      cum += w;
+    }
+    pos = block_min_l(s, found);
+  }
+  if (plan.cut_m) {  // the candidates with key >= kminp, a prefix of the list
     const uint32_t kminp = plan.kminp;
-    if (p.use_m && kminp != 0xffffffffu && kminp >= cand_key(fs.cand[n - 1]))
-      jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
-  } else {
-    // the list is the bucket of the earliest cut (as fast_boundary)
-    jcut = kTieAll;
-    if (plan.cut_p) jcut = min(jcut, list_first_exceed(s, fs, n, plan.mp_before, plan.thr, inv_t, zmax));
-    if (plan.cut_m) jcut = min(jcut, list_count_ge(s, fs, n, plan.kminp) - 1);
-  }
-  if (jcut >= n) jcut = n - 1;
-  if (jcut < 0) jcut = 0;
-  const unsigned long long edge = fs.cand[jcut];
-  if (plan.use_k) {
-    const int64_t M = list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
-    const float u = a.uniforms ? a.uniforms[b] : 0.5f;
-    const int64_t found = list_draw(s, fs, (int)jcut + 1, inv_t, zmax, draw_point(u, M));
-    if (t == 0) {
-      a.out_ids[b] = found == kTieAll ? 0 : found;
-      plan.status = kPlanDone;
+    int64_t lastm = -1;
+    if (kminp <= khi) {
+      const int64_t jm = (int64_t)(khi - kminp);
+#pragma unroll
+      for (int k = 0; k < kPerT; ++k)
+        if (c[k] && j0 + k <= jm) lastm = ((int64_t)(j0 + k) << 32) | c[k];
     }
-    return;
+    lastm = -block_min_l(s, -lastm);
+    pos = lastm < pos ? lastm : pos;
   }
-  const int64_t M = plan.m_before + list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
-  for (int i = t; i <= jcut; i += kThreads)
-    atomicAdd(&segk[cand_id(fs.cand[i]) / a.seg_len], (unsigned long long)cand_mass(fs.cand[i], inv_t, zmax));
+  int jc;
+  int64_t ic;
+  if (pos == kTieAll) {  // (uniform branches: the block reductions run on every thread)
+    jc = (int)-block_min_l(s, -last);
+    ic = kTieAll;
+  } else if (pos < 0) {
+    jc = (int)block_min_l(s, first);
+    ic = 1;
+  } else {
+    jc = (int)(pos >> 32);
+    ic = pos & 0xffffffffll;
+  }
+  const uint32_t key_cut = khi - (uint32_t)jc;
+  const int64_t cnt_c = kcnt[jc];
+  if (ic >= cnt_c) ic = kTieAll;
+  int64_t id_cut = kTieAll;
+  if (ic != kTieAll) {
+    // the ic-th smallest id of key_cut: each of its ids counts the smaller ones
+    if (cnt_c > kTieRank) return false;
+    __syncthreads();
+    if (t == 0) fs.ncand = 0;
+    __syncthreads();
+    for (int i = t; i < n; i += kThreads) {
+      const unsigned long long e = fs.cand[i];
+      if (cand_key(e) == key_cut) tie_ids[atomicAdd(&fs.ncand, 1)] = (uint32_t)cand_id(e);
+    }
+    __syncthreads();
+    const int nt = fs.ncand, nt4 = (nt + 3) & ~3;
+    if (t >= nt && t < nt4) tie_ids[t] = 0xffffffffu;
+    __syncthreads();
+    if (t < nt) {
+      const uint32_t mine = tie_ids[t];
+      const uint4* v = reinterpret_cast<const uint4*>(tie_ids);
+      int rank = 0;
+      for (int q = 0; q < nt4 / 4; ++q) {
+        const uint4 x = v[q];
+        rank += (x.x < mine) + (x.y < mine) + (x.z < mine) + (x.w < mine);
+      }
+      if (rank == ic - 1) s.b_id = mine;
+    }
+    __syncthreads();
+    id_cut = s.b_id;
+  }
+  // kept mass of the list: the bins before jc, and ic (or all) ties of jc
+  if (jc >= j0 && jc < j0 + kPerT) {
+    int64_t kept = plan.m_before + before;
+#pragma unroll
+    for (int k = 0; k < kPerT; ++k)
+      if (j0 + k < jc) kept += (int64_t)c[k] * m[k];
+      else if (j0 + k == jc) kept += (ic == kTieAll ? (int64_t)c[k] : ic) * m[k];
+    s.b_total = kept;
+  }
+  for (int i = t; i < n; i += kThreads) {
+    const unsigned long long e = fs.cand[i];
+    const uint32_t key = cand_key(e);
+    const int64_t id = cand_id(e);
+    if (key > key_cut || (key == key_cut && id <= id_cut))
+      atomicAdd(&segk[id / a.seg_len], (unsigned long long)cand_mass(e, inv_t, zmax));
+  }
   __syncthreads();
-  if (t < a.R) a.seg_kept[b * a.R + t] = (int64_t)segk[t];
   if (t == 0) {
-    plan.key_cut = cand_key(edge);
-    plan.id_cut = cand_id(edge);
-    plan.M = M;
+    plan.key_cut = key_cut;
+    plan.id_cut = id_cut;
+    plan.M = s.b_total;
     plan.status = kPlanDraw;
   }
+  return true;
 }
 
 // ---------------------------------------------------------------------------
@@ -2054,86 +1942,415 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
   row_cut_wave_list(a, pl, p, b, n, c, nullptr);  // top-k: drawn from the list, no per-segment masses
 }
 
+
+// ---------------------------------------------------------------------------
+// Per row, after seg_stats and seg_hist, in one launch (row_finish_kernel):
+// the plan (the bucket or buckets holding the cut-offs, from the summed
+// segment histograms), the candidates of those buckets gathered from the row
+// by this workgroup, the cut, and the draw.
+
+constexpr uint32_t kInfKey = 0xff80u;  // +inf: the keys of non-NaN values are [1, kInfKey]
+
+// Smallest key in [1, kInfKey] at which pred holds (pred is false below some
+// key and true from it on), kInfKey + 1 if it holds at none.  Each round
+// probes 64 keys at once, so three or four rounds cover the key range; every
+// lane of the calling wave returns the result.
+template <typename P>
+XV_INLINE uint32_t wave_first_key(P&& pred) {
+  const uint32_t lane = threadIdx.x & 63;
+  uint32_t l = 1, h = kInfKey + 1;  // the result is in [l, h]: pred holds at h, or h is past the keys
+  while (l < h) {
+    const uint32_t span = h - l, step = (span + 63) / 64;
+    const uint32_t k = l + lane * step;
+    const unsigned long long m = __ballot(k < h && pred(k));
+    if (m) {
+      const uint32_t i = (uint32_t)__builtin_ctzll(m);
+      h = l + i * step;
+      if (i) l = h - step + 1;  // the probe before it failed
+    } else {
+      l += ((span + step - 1) / step - 1) * step + 1;  // past the last probe below h
+    }
+  }
+  return l;
+}
+
+// Append every id of the row whose key lies in [klo, khi] (klo >= 1) to
+// fs.cand as (key << 32) | ~id; fs.ncand counts them, also past kMaxCand.
+// The key transform and the range test run on two logits per 32-bit word (the
+// key of raw bits b is b ^ 0xffff for a negative b, else b ^ 0x8000; a
+// saturating subtract leaves 0 exactly for the keys in range), so a vector
+// without a hit costs a few instructions, and a wave with no hit in a vector
+// skips the per-id work.  Ids with a hit are checked exactly (a NaN's key is
+// 0 there).  The loads of a step go out together: every lane loads whole
+// vectors (vectors past the row's last whole one reload it and are masked),
+// and the ids past the last whole vector are taken one by one at the end.
+constexpr int kGatherChunk = 10;  // 16-byte loads in flight per thread (more spill registers)
+XV_INLINE void gather_key_range(FastShared& fs, const bf16_t* row, int V, bool vec_ok, uint32_t klo,
+                                uint32_t khi) {
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  auto append = [&](uint32_t bits, int id) {
+    const uint32_t key = order_key(bits);
+    if (key >= klo && key <= khi) {
+      const int slot = atomicAdd(&fs.ncand, 1);
+      if (slot < kMaxCand)
+        fs.cand[slot] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
+    }
+  };
+  const int t = threadIdx.x;
+  const int nfull = vec_ok ? V / 8 : 0;  // a row not 16-byte aligned goes id by id
+  const u16x2 lo2 = {(unsigned short)klo, (unsigned short)klo};
+  const u16x2 sp2 = {(unsigned short)(khi - klo), (unsigned short)(khi - klo)};
+  const u16x2 top2 = {(unsigned short)0x8000u, (unsigned short)0x8000u};
+  for (int c0 = 0; c0 < nfull; c0 += kGatherChunk * kThreads) {
+    uint32_t wv[kGatherChunk][4];
+#pragma unroll
+    for (int v = 0; v < kGatherChunk; ++v) {
+      const int vi = c0 + v * kThreads + t;
+      const Vec8 x = load_vec8(row + 8u * (uint32_t)min(vi, nfull - 1));
+#pragma unroll
+      for (int k = 0; k < 4; ++k) wv[v][k] = x.w[k];
+    }
+#pragma unroll
+    for (int v = 0; v < kGatherChunk; ++v) {
+      const int vi = c0 + v * kThreads + t;
+      uint32_t z[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const u16x2 w2 = __builtin_bit_cast(u16x2, wv[v][k]);
+        const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
+        z[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat((u16x2)((w2 ^ (sg | top2)) - lo2), sp2));
+      }
+      const u16x2 m2 = __builtin_elementwise_min(
+          __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[0]), __builtin_bit_cast(u16x2, z[1])),
+          __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[2]), __builtin_bit_cast(u16x2, z[3])));
+      if (vi < nfull && (m2.x == 0 || m2.y == 0)) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+          if (((z[k >> 1] >> (16 * (k & 1))) & 0xffffu) == 0u)
+            append((wv[v][k >> 1] >> (16 * (k & 1))) & 0xffffu, vi * 8 + k);
+      }
+    }
+  }
+  for (int id = nfull * 8 + t; id < V; id += kThreads) append((uint32_t)row[id], id);
+}
+
 XV_INLINE int64_t kept_mass_of(uint32_t bits, int id, uint32_t key_cut, int64_t id_cut, float inv_t, float zmax) {
   const uint32_t key = order_key(bits);
   const bool kept = key && (key > key_cut || (key == key_cut && (int64_t)id <= id_cut));
   return kept ? mass_of(exp_of(bits, inv_t, zmax)) : 0;
 }
 
-__global__ __launch_bounds__(kSegThreads) void row_draw_kernel(SegArgs a) {
-  __shared__ SegRed red;
-  __shared__ int64_t pick;
-  const int b = blockIdx.x, t = threadIdx.x;
-  // the segment masses and the draw load beside the plan (one round trip)
-  const int64_t sm_l = a.seg_kept[b * a.R + min(t, a.R - 1)];
+// The draw of a row whose cut is made: the segment holding floor(u * M) by
+// the segments' kept masses, then in that segment, in id order, the first kept
+// id whose inclusive mass exceeds the rest of the draw point.  Each thread
+// takes a run of consecutive ids of the segment.
+constexpr int kDrawRegs = 16;  // ids per thread whose masses the draw keeps in registers
+XV_INLINE void row_draw(const SegArgs& a, Shared& s, const RowPlan& lp, const unsigned long long* segk, int b) {
+  const int t = threadIdx.x, lane = t & 63;
   const float u = a.uniforms ? a.uniforms[b] : 0.5f;
-  const RowPlan plan = a.plans[b];  // every field in one round trip
-  if (plan.status != kPlanDraw) return;
-  const uint32_t key_cut = plan.key_cut;
-  const int64_t id_cut = plan.id_cut;
-  const float inv_t = plan.inv_t, zmax = plan.zmax;
-  const int64_t rdraw = draw_point(u, plan.M);
-  // the segment holding rdraw: inclusive sums of the segment masses
-  const int64_t sm = t < a.R ? sm_l : 0;
-  const int64_t incl = seg_incl_scan(red, sm);
-  const int r = (int)seg_min_l(red, (t < a.R && rdraw < incl) ? t : kMaxSegs);
+  const int64_t rdraw = draw_point(u, lp.M);
+  // every wave finds the segment itself: R <= 64, one segment per lane
+  const int64_t sm = lane < a.R ? (int64_t)segk[lane] : 0;
+  const int64_t incl = wave_incl_scan_l(sm);
+  const int r = (int)wave_first(lane < a.R && rdraw < incl, kMaxSegs);
   if (r >= a.R) {  // no kept mass (cannot happen for a row with a finite logit)
     if (t == 0) a.out_ids[b] = 0;
     return;
   }
-  __syncthreads();
-  if (t == r) pick = incl - sm;  // mass of the segments before r
-  __syncthreads();
-  const int64_t rr = rdraw - pick;
-  // inside segment r, in id order: thread t owns [beg + t*C, beg + t*C + C)
+  const int64_t rr = rdraw - (__shfl(incl, r) - (int64_t)segk[r]);
+  const uint32_t key_cut = lp.key_cut;
+  const int64_t id_cut = lp.id_cut;
+  const float inv_t = lp.inv_t, zmax = lp.zmax;
   const bf16_t* row = a.logits + (int64_t)b * a.stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
   const int beg = r * a.seg_len, end = min(a.V, beg + a.seg_len);
-  const int C = ((end - beg + kSegThreads - 1) / kSegThreads + 7) / 8 * 8;
+  const int C = ((end - beg + kThreads - 1) / kThreads + 7) / 8 * 8;
   const int i0 = min(end, beg + t * C), i1 = min(end, i0 + C);
-  auto scan_range = [&](auto&& f) {
-    for (int i = i0; i < i1; i += 8 * kSegChunk) {
-      uint32_t bits[kSegChunk][8];
+  if (C <= kDrawRegs) {
+    // the thread's masses stay in registers for the second step
+    int64_t q[kDrawRegs];
 #pragma unroll
-      for (int v = 0; v < kSegChunk; ++v)
-        if (i + 8 * v < i1) load8(row, i1, i + 8 * v, vec_ok, bits[v]);  // i0 and C are multiples of 8
+    for (int v = 0; v < kDrawRegs / 8; ++v) {
+      uint32_t bits[8];
+      const int base = i0 + 8 * v;
+      if (base < i1) load8(row, i1, base, vec_ok, bits);  // i0 and C are multiples of 8
 #pragma unroll
-      for (int v = 0; v < kSegChunk; ++v)
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (i + 8 * v + k < i1) f(bits[v][k], i + 8 * v + k);
+      for (int k = 0; k < 8; ++k)
+        q[8 * v + k] = base + k < i1 ? kept_mass_of(bits[k], base + k, key_cut, id_cut, inv_t, zmax) : 0;
     }
-  };
-  int64_t mine = 0;
-  scan_range([&](uint32_t bits, int id) { mine += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax); });
-  const int64_t cum_incl = seg_incl_scan(red, mine);
-  int64_t cum = cum_incl - mine;
-  __syncthreads();
-  if (t == 0) pick = -1;
-  __syncthreads();
-  if (cum <= rr && rr < cum_incl) {
-    int64_t found = -1;
-    scan_range([&](uint32_t bits, int id) {
-      if (found >= 0) return;
-      cum += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax);
-      if (cum > rr) found = id;
-    });
-    pick = found;
+    int64_t mine = 0;
+#pragma unroll
+    for (int k = 0; k < kDrawRegs; ++k) mine += q[k];
+    int64_t seg_total;
+    int64_t cum = block_excl_scan(s, mine, &seg_total);
+    __syncthreads();
+    if (t == 0) s.b_id = -1;
+    __syncthreads();
+    if (cum <= rr && rr < cum + mine) {
+      int found = -1;
+#pragma unroll
+      for (int k = 0; k < kDrawRegs; ++k) {
+        cum += q[k];
+        if (found < 0 && cum > rr) found = i0 + k;
+      }
+      s.b_id = found;
+    }
+  } else {
+    auto scan_range = [&](auto&& f) {
+      for (int i = i0; i < i1; i += 8 * kSegChunk) {
+        uint32_t bits[kSegChunk][8];
+#pragma unroll
+        for (int v = 0; v < kSegChunk; ++v)
+          if (i + 8 * v < i1) load8(row, i1, i + 8 * v, vec_ok, bits[v]);
+#pragma unroll
+        for (int v = 0; v < kSegChunk; ++v)
+#pragma unroll
+          for (int k = 0; k < 8; ++k)
+            if (i + 8 * v + k < i1) f(bits[v][k], i + 8 * v + k);
+      }
+    };
+    int64_t mine = 0;
+    scan_range([&](uint32_t bits, int id) { mine += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax); });
+    int64_t seg_total;
+    int64_t cum = block_excl_scan(s, mine, &seg_total);
+    __syncthreads();
+    if (t == 0) s.b_id = -1;
+    __syncthreads();
+    if (cum <= rr && rr < cum + mine) {
+      int64_t found = -1;
+      scan_range([&](uint32_t bits, int id) {
+        if (found >= 0) return;
+        cum += kept_mass_of(bits, id, key_cut, id_cut, inv_t, zmax);
+        if (cum > rr) found = id;
+      });
+      s.b_id = found;
+    }
   }
   __syncthreads();
-  if (t == 0) a.out_ids[b] = pick >= 0 ? pick : 0;
+  if (t == 0) a.out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
 }
 
+__global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
+  __shared__ Shared s;
+  __shared__ FastShared fs;
+  __shared__ RowPlan lp;
+  __shared__ unsigned long long segk[kMaxSegs];
+  __shared__ __attribute__((aligned(16))) uint32_t tie_ids[kTieRank];
+  const int b = blockIdx.x, t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const RowParams p = row_params(a, b);
+  if (p.greedy) {  // the best of the segments' best words (torch.argmax order)
+    if (w == 0) {
+      const unsigned long long best = wave_max_ull(lane < a.R ? a.seg_best[b * a.R + lane] : 0ull);
+      if (lane == 0) a.out_ids[b] = best ? (int64_t)(0xffffffffu - (uint32_t)best) : 0;
+    }
+    return;
+  }
+  // Every load the plan needs goes out before any is used: the row's segment
+  // statistics, and of bucket t % kBuckets the histogram entries of segments
+  // t / kBuckets + kGroups * j.  Segment indices past R reload segment R - 1
+  // (no branch between the loads) and are masked below.
+  constexpr int kGroups = kThreads / kBuckets, kSegPerGroup = kMaxSegs / kGroups;
+  static_assert(kGroups * kBuckets == kThreads && kSegPerGroup * kGroups == kMaxSegs, "bucket x segment layout");
+  const int bt = t & (kBuckets - 1), g = t / kBuckets;
+  uint32_t hc[kSegPerGroup];
+  unsigned long long hm[kSegPerGroup];
+#pragma unroll
+  for (int j = 0; j < kSegPerGroup; ++j) {
+    const int64_t o = ((int64_t)b * a.R + min(g + kGroups * j, a.R - 1)) * kBuckets + bt;
+    hc[j] = a.seg_cnt[o];
+    hm[j] = p.use_k ? 0ull : a.seg_mass[o];  // top-k rows take their masses from the list
+  }
+  const int sl = min(lane, a.R - 1);
+  const uint32_t kmax_l = a.seg_kmax[b * a.R + sl], kmin_l = a.seg_kmin[b * a.R + sl];
+  const uint32_t minp_l = a.seg_minp[b * a.R + sl];
+  const RowConsts rc = row_consts_of(lane < a.R ? kmax_l : 0u, lane < a.R ? kmin_l : 0xffffffffu, p.temp);
+  if (rc.kmax == 0) {  // every logit NaN: nothing has mass
+    if (t == 0) a.out_ids[b] = 0;
+    return;
+  }
+  const uint32_t kminp = wave_min_u(lane < a.R ? minp_l : 0xffffffffu);
+  if (t < kBuckets) {
+    s.cnt[t] = 0u;
+    s.mass[t] = 0ull;
+  }
+  if (t < kMaxSegs) segk[t] = 0ull;
+  __syncthreads();
+  {
+    uint32_t c = 0;
+    unsigned long long m = 0;
+#pragma unroll
+    for (int j = 0; j < kSegPerGroup; ++j)
+      if (g + kGroups * j < a.R) {
+        c += hc[j];
+        m += hm[j];
+      }
+    atomicAdd(&s.cnt[bt], c);
+    if (!p.use_k) atomicAdd(&s.mass[bt], m);
+  }
+  __syncthreads();
+  const int64_t cnt = t < kBuckets ? (int64_t)s.cnt[t] : 0;
+  const int64_t mass = (t < kBuckets && !p.use_k) ? (int64_t)s.mass[t] : 0;
+  int64_t cnt_excl, mass_excl, cnt_all, total;
+  block_excl_scan2(s, cnt, mass, &cnt_excl, &mass_excl, &cnt_all, &total);
+  const int64_t cnt_incl = cnt_excl + cnt, mass_incl = mass_excl + mass;
+  int status = kPlanDraw, lo = 0, hi = 0, cut_p = 0, cut_m = 0;
+  int64_t thr = 0, m_before = 0;
+  if (p.use_k) {
+    // rank k-1 lies in the first bucket whose inclusive count reaches k
+    const int bk = (int)block_min_l(s, (t < kBuckets && cnt_incl >= p.top_k) ? t : kBuckets);
+    __syncthreads();
+    if (t == bk) s.b_long[0] = cnt_incl;  // candidates in buckets 0..bk
+    __syncthreads();
+    const int64_t upto = bk < kBuckets ? s.b_long[0] : 0;
+    status = (bk >= kBuckets - 1 || upto > kMaxCand) ? kPlanFallback : kPlanGather;
+    hi = bk;
+  } else if (p.use_p || p.use_m) {
+    int bp = kBuckets;
+    if (p.use_p) {
+      thr = (int64_t)floor((double)p.top_p * (double)total);
+      bp = (int)block_min_l(s, (t < kBuckets && mass_incl > thr) ? t : kBuckets);
+    }
+    int bm = kBuckets;
+    if (p.use_m && kminp != 0xffffffffu) bm = bucket_of(log2_ratio(key_to_bits(kminp), rc.inv_t, rc.zmax), rc.bs);
+    const int bf = min(bp, bm);
+    if (bf < kBuckets) {
+      __syncthreads();
+      if (t == bf) {
+        s.b_long[0] = cnt;
+        s.b_long[1] = mass_incl - mass;  // mass of the buckets before bf
+      }
+      __syncthreads();
+      m_before = s.b_long[1];
+      status = s.b_long[0] > kMaxCand ? kPlanFallback : kPlanGather;
+      lo = hi = bf;
+      cut_p = bp == bf;
+      cut_m = bm == bf;
+    }
+  }
+  bool fallback = status == kPlanFallback;  // the boundary does not fit in LDS
+  if (t == 0) {
+    lp.status = status;
+    lp.lo = lo;
+    lp.hi = hi;
+    lp.use_k = p.use_k;
+    lp.cut_p = cut_p;
+    lp.cut_m = cut_m;
+    lp.kminp = kminp;
+    lp.zmax = rc.zmax;
+    lp.inv_t = rc.inv_t;
+    lp.bs = rc.bs;
+    lp.thr = thr;
+    lp.mp_before = m_before;
+    lp.m_before = m_before;
+    lp.key_cut = 1u;  // no cut: every candidate kept
+    lp.id_cut = kTieAll;
+    lp.M = total;
+    fs.ncand = 0;
+  }
+  if (fallback) {
+  } else if (status == kPlanDraw) {  // no cut: the segments' total masses are their kept masses
+    if (t < a.R) segk[t] = (unsigned long long)a.seg_kept[b * a.R + t];
+  } else {
+    // Buckets fall as keys rise over the keys of non-NaN values, so buckets
+    // lo..hi hold exactly the keys of an interval: its ends by the same bucket
+    // function.
+    auto bkt = [&](uint32_t k) { return bucket_of(log2_ratio(key_to_bits(k), rc.inv_t, rc.zmax), rc.bs); };
+    if (w == 0) {
+      const uint32_t klo = wave_first_key([&](uint32_t k) { return bkt(k) <= hi; });
+      if (lane == 0) lp.klo = klo;
+    } else if (w == 1) {
+      const uint32_t kend = wave_first_key([&](uint32_t k) { return bkt(k) < lo; });
+      if (lane == 0) lp.khi = kend - 1;
+    }
+    // rows without top-k: each segment's mass of the buckets before lo (all
+    // of whose candidates are kept; the list's part is added by the cut)
+    if (!p.use_k) {
+#pragma unroll
+      for (int j = 0; j < kSegPerGroup; ++j) {
+        const int r = g + kGroups * j;
+        const int64_t v = wave_sum_l((r < a.R && bt < lo) ? (int64_t)hm[j] : 0);
+        if (lane == 0 && r < a.R) atomicAdd(&segk[r], (unsigned long long)v);
+      }
+    }
+  }
+  __syncthreads();
+  if (status == kPlanGather) {
+    const bf16_t* row = a.logits + (int64_t)b * a.stride;
+    const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
+    const uint32_t klo = lp.klo, khi = lp.khi;
+    if (klo <= khi) gather_key_range(fs, row, a.V, vec_ok, klo, khi);
+    __syncthreads();
+    const int n = fs.ncand;
+    // the cut's bucket holds its own boundary candidate, and the histograms
+    // counted the list; should either fail, the one-workgroup path takes the row
+    const float inv_t = rc.inv_t, zmax = rc.zmax;
+    if (n == 0 || n > kMaxCand) {
+      fallback = true;
+    } else if (n <= 64) {
+      if (t < 64) row_cut_wave_list(a, lp, p, b, n, lane < n ? fs.cand[lane] : 0ull, segk);
+    } else if (p.use_k || !row_cut_by_keys(a, lp, s, fs, b, n, tie_ids, segk)) {
+      sort_cand_desc(fs, n);
+      int64_t jcut;
+      if (p.use_k) {
+        // the list is every candidate down to rank k-1 (as topk_boundary)
+        const int64_t total_k = list_mass_prefix(s, fs, n, p.top_k, inv_t, zmax);
+        jcut = (int64_t)p.top_k - 1;
+        if (p.use_p) {
+          const int64_t thr_k = (int64_t)floor((double)p.top_p * (double)total_k);
+          jcut = min(jcut, list_first_exceed(s, fs, n, 0, thr_k, inv_t, zmax));
+        }
+        if (p.use_m && kminp != 0xffffffffu && kminp >= cand_key(fs.cand[n - 1]))
+          jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
+      } else {
+        // the list is the bucket of the earliest cut (as fast_boundary)
+        jcut = kTieAll;
+        if (cut_p) jcut = min(jcut, list_first_exceed(s, fs, n, m_before, thr, inv_t, zmax));
+        if (cut_m) jcut = min(jcut, list_count_ge(s, fs, n, kminp) - 1);
+      }
+      if (jcut >= n) jcut = n - 1;
+      if (jcut < 0) jcut = 0;
+      const unsigned long long edge = fs.cand[jcut];
+      if (p.use_k) {
+        const int64_t M = list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+        const float u = a.uniforms ? a.uniforms[b] : 0.5f;
+        const int64_t found = list_draw(s, fs, (int)jcut + 1, inv_t, zmax, draw_point(u, M));
+        if (t == 0) {
+          a.out_ids[b] = found == kTieAll ? 0 : found;
+          lp.status = kPlanDone;
+        }
+      } else {
+        const int64_t M = m_before + list_mass_prefix(s, fs, n, jcut + 1, inv_t, zmax);
+        for (int i = t; i <= jcut; i += kThreads)
+          atomicAdd(&segk[cand_id(fs.cand[i]) / a.seg_len], (unsigned long long)cand_mass(fs.cand[i], inv_t, zmax));
+        if (t == 0) {
+          lp.key_cut = cand_key(edge);
+          lp.id_cut = cand_id(edge);
+          lp.M = M;
+          lp.status = kPlanDraw;
+        }
+      }
+    }
+    __syncthreads();
+  }
+  if (fallback) {
+    sample_row(s, fs, b, a.logits, a.stride, a.V, a.temps, a.top_ps, a.top_ks, a.min_ps, a.uniforms,
+               a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
+    return;
+  }
+  if (lp.status == kPlanDraw) row_draw(a, s, lp, segk, b);
+}
 }  // namespace
 
 // Workspace: one 128-byte line per row (a 64-bit slot and a 32-bit arrival
-// counter) for the multi-workgroup greedy path, then the per-row plans,
-// per-segment statistics and histograms and the per-row candidate lists of the
-// multi-workgroup sampled path.
+// counter) for the multi-workgroup greedy path, then the per-segment
+// statistics and histograms of the multi-workgroup sampled path, and room for
+// kMaxCand candidates per row, which the top-k path's lists use (it sets how
+// many rows that path takes; the sampled path keeps its candidates in LDS).
 namespace {
 struct SegLayout {
   int R, seg_len;
-  size_t plans, kmax, kmin, minp, best, kept, cnt, mass, cand, total;
+  size_t kmax, kmin, minp, best, kept, cnt, mass, cand, total;
 };
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 SegLayout seg_layout(int batch, int vocab) {
@@ -2145,7 +2362,6 @@ SegLayout seg_layout(int batch, int vocab) {
   L.R = (vocab + L.seg_len - 1) / L.seg_len;
   const size_t B = (size_t)max(batch, 0), BR = B * L.R;
   size_t o = 0;  // offsets within the sampled path's region
-  L.plans = o; o = align256(o + B * sizeof(RowPlan));
   L.kmax = o;  o = align256(o + BR * 4);
   L.kmin = o;  o = align256(o + BR * 4);
   L.minp = o;  o = align256(o + BR * 4);
@@ -2242,7 +2458,6 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     a.V = vocab; a.R = L.R; a.seg_len = L.seg_len; a.flags = flags & ~XV_SAMPLE_ALL_GREEDY;
     a.temps = temperatures; a.top_ps = top_ps; a.top_ks = top_ks; a.min_ps = min_ps; a.uniforms = uniforms;
     a.out_ids = out_ids;
-    a.plans = (RowPlan*)(w + L.plans);
     a.seg_kmax = (uint32_t*)(w + L.kmax);
     a.seg_kmin = (uint32_t*)(w + L.kmin);
     a.seg_minp = (uint32_t*)(w + L.minp);
@@ -2250,20 +2465,12 @@ extern "C" int xv_sample(const void* logits, int64_t logits_stride, int batch, i
     a.seg_kept = (int64_t*)(w + L.kept);
     a.seg_cnt = (uint32_t*)(w + L.cnt);
     a.seg_mass = (unsigned long long*)(w + L.mass);
-    a.cand = (unsigned long long*)(w + L.cand);
-    a.cand_stride = kMaxCand;
     const dim3 segs((unsigned)L.R, (unsigned)batch), rows((unsigned)batch);
     seg_stats_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     seg_hist_kernel<<<segs, kSegThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
-    row_plan_kernel<<<rows, kSegThreads, 0, stream>>>(a);
-    XV_CHECK_LAUNCH();
-    seg_gather_kernel<<<segs, kSegThreads, 0, stream>>>(a);
-    XV_CHECK_LAUNCH();
-    row_cut_kernel<<<rows, kThreads, 0, stream>>>(a);
-    XV_CHECK_LAUNCH();
-    row_draw_kernel<<<rows, kSegThreads, 0, stream>>>(a);
+    row_finish_kernel<<<rows, kThreads, 0, stream>>>(a);
     XV_CHECK_LAUNCH();
     return 0;
   }
