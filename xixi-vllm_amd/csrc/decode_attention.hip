@@ -779,15 +779,10 @@ XV_INLINE int range_pages(const DecodeArgs& a, int64_t total, int max_np) {
   return (int)max((int64_t)max(kMinRangePages, need), per);
 }
 
-// Timing hook for out-of-tree instrumentation builds; empty in the library.
-#ifndef XV_DECODE_TIMESTAMP
-#define XV_DECODE_TIMESTAMP(slot)
-#endif
 
 template <int G, bool F8 = false>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_WPE : XV_DECODE_WPE,
                                                                       F8 ? XV_F8_WPE : XV_DECODE_WPE))) void paged_decode_kernel(DecodeArgs a) {
-  XV_DECODE_TIMESTAMP(0);
   constexpr int NB = kNbufT<G, F8>;
   constexpr int BUF = kBufBytesT<G, F8>;
   constexpr int QOFF = kPageBufBytes<G, F8>;  // the q slot within a page buffer
@@ -826,7 +821,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   const int n = (int)max((int64_t)0, min(f0 + L, total) - f0);  // pages of this wave's range
   if (n == 0) return;
   const LaneOffsets offs = lane_offsets(a.tok_stride, lane);
-  XV_DECODE_TIMESTAMP(1);
 
   // cursor at the range's first page
   Cursor c0;
@@ -929,7 +923,6 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(F8 ? XV_F8_W
   // the last processed buffer's q slot: its q is in registers, and no DMA
   // targets it any more (q only comes with a segment's first page)
   finish(pc, lds + ((n - 1) % NB) * BUF + QOFF);
-  XV_DECODE_TIMESTAMP(2);
 }
 
 // Cascade decode: prefix-pass partials per (sequence, query head).

@@ -38,10 +38,6 @@
 
 #pragma clang fp contract(off)
 
-// Phase timestamps for out-of-tree timing builds; compiled out here.
-#ifndef XV_SAMPLER_TIMESTAMP
-#define XV_SAMPLER_TIMESTAMP(slot)
-#endif
 
 namespace {
 
@@ -749,7 +745,6 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     if (bkt < kBuckets - 1) atomicAdd(&fs.wcnt[w][bkt], 1u);
     else far_c += 1;
   });
-  XV_SAMPLER_TIMESTAMP(5);
   far_c = block_sum_l(s, far_c);
   __syncthreads();
   if (t < kBuckets) {
@@ -771,7 +766,6 @@ XV_INLINE bool topk_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
   if (bk >= kBuckets - 1 || upto > kMaxCand) return false;  // rank k-1 far out or too many: exact row-wide path
   const uint32_t kminp = use_m ? minp_key(s, row, V, vec_ok, inv_t, zmax, min_p) : 0xffffffffu;
   const int n = gather_bucket(fs, row, V, vec_ok, inv_t, zmax, bs, bk, 0);
-  XV_SAMPLER_TIMESTAMP(6);
   if (n > kMaxCand) return false;
   const int64_t total_k = list_mass_prefix(s, fs, n, top_k, inv_t, zmax);
   int64_t jcut = (int64_t)top_k - 1;
@@ -823,7 +817,6 @@ XV_INLINE bool fast_boundary(Shared& s, FastShared& fs, const bf16_t* row, int V
     }
     if (use_m && e >= min_p) kminp = min(kminp, key);
   });
-  XV_SAMPLER_TIMESTAMP(5);
   far_c = block_sum_l(s, far_c);
   far_m = block_sum_l(s, far_m);
   if (use_m) kminp = block_min_u(s, kminp);
@@ -970,7 +963,6 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
     return;
   }
 
-  XV_SAMPLER_TIMESTAMP(0);
   // ---- pass 1: the largest key ----
   uint32_t kmax = 0, kmin = 0xffffffffu;
   for_each_strided(row, V, vec_ok, [&](uint32_t bits, int) {
@@ -990,7 +982,6 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   const bool use_k = top_k > 0 && top_k < V;
   const bool use_p = top_p < 1.0f;
   const bool use_m = min_p > 0.0f;
-  XV_SAMPLER_TIMESTAMP(1);
 
   uint32_t key_cut;
   int64_t id_cut, M;
@@ -1002,9 +993,7 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
     general_boundary(s, row, V, vec_ok, inv_t, zmax, top_k, top_p, min_p, use_k, use_p, use_m, bd, id_cut,
                      M);
     key_cut = bd.key;
-    XV_SAMPLER_TIMESTAMP(3);
   }
-  XV_SAMPLER_TIMESTAMP(2);
 
   // ---- last pass: inverse-CDF draw in ascending id order (exp for kept ids only) ----
   // Thread t owns the contiguous ids [t*C, t*C + C), C a multiple of 8, so one
@@ -1014,7 +1003,6 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   if (list_kept > 0) {
     const int64_t found = list_draw(s, fs, list_kept, inv_t, zmax, rdraw);
     if (t == 0) out_ids[b] = found == kTieAll ? 0 : found;
-    XV_SAMPLER_TIMESTAMP(4);
     return;
   }
   const int C = ((V + kThreads - 1) / kThreads + 7) / 8 * 8;
@@ -1044,7 +1032,6 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   }
   __syncthreads();
   if (t == 0) out_ids[b] = s.b_id >= 0 ? s.b_id : 0;
-  XV_SAMPLER_TIMESTAMP(4);
 }
 
 __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restrict__ logits, int64_t stride, int V,
