@@ -1544,7 +1544,7 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
 // sort's in every other case.
 constexpr int kKeyBins = kWaves * kBuckets;  // the per-wave histograms' LDS, unused here
 constexpr int kTieRank = 512;
-XV_INLINE bool row_cut_by_keys(const SegArgs& a, RowPlan& plan, Shared& s, FastShared& fs, int b, int n,
+XV_INLINE bool row_cut_by_keys(const SegArgs& a, RowPlan& plan, Shared& s, FastShared& fs, int n,
                                uint32_t* tie_ids, unsigned long long* segk) {
   const int t = threadIdx.x;
   const uint32_t klo = plan.klo, khi = plan.khi;
@@ -2276,7 +2276,7 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
       fallback = true;
     } else if (n <= 64) {
       if (t < 64) row_cut_wave_list(a, lp, p, b, n, lane < n ? fs.cand[lane] : 0ull, segk);
-    } else if (p.use_k || !row_cut_by_keys(a, lp, s, fs, b, n, tie_ids, segk)) {
+    } else if (p.use_k || !row_cut_by_keys(a, lp, s, fs, n, tie_ids, segk)) {
       sort_cand_desc(fs, n);
       int64_t jcut;
       if (p.use_k) {
