@@ -1966,12 +1966,13 @@ XV_INLINE uint32_t wave_first_key(P&& pred) {
 // The key transform and the range test run on two logits per 32-bit word (the
 // key of raw bits b is b ^ 0xffff for a negative b, else b ^ 0x8000; a
 // saturating subtract leaves 0 exactly for the keys in range), so a vector
-// without a hit costs a few instructions, and a wave with no hit in a vector
-// skips the per-id work.  Ids with a hit are checked exactly (a NaN's key is
-// 0 there).  The loads of a step go out together: every lane loads whole
-// vectors (vectors past the row's last whole one reload it and are masked),
-// and the ids past the last whole vector are taken one by one at the end.
+// without a hit costs a few instructions.  Ids with a hit are checked exactly
+// (a NaN's key is 0 there).  The loads of a step go out together: every lane
+// loads whole vectors (vectors past the row's last whole one reload it and
+// are masked), and the ids past the last whole vector are taken one by one at
+// the end.
 constexpr int kGatherChunk = 10;  // 16-byte loads in flight per thread (more spill registers)
+constexpr int kGatherRec = 4;     // vectors with a hit a lane records for later
 XV_INLINE void gather_key_range(FastShared& fs, const bf16_t* row, int V, bool vec_ok, uint32_t klo,
                                 uint32_t khi) {
   typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
@@ -1989,6 +1990,29 @@ XV_INLINE void gather_key_range(FastShared& fs, const bf16_t* row, int V, bool v
   const u16x2 lo2 = {(unsigned short)klo, (unsigned short)klo};
   const u16x2 sp2 = {(unsigned short)(khi - klo), (unsigned short)(khi - klo)};
   const u16x2 top2 = {(unsigned short)0x8000u, (unsigned short)0x8000u};
+  auto test = [&](const uint32_t (&wd)[4], uint32_t (&z)[4]) {  // true if some id may be in range
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const u16x2 w2 = __builtin_bit_cast(u16x2, wd[k]);
+      const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
+      z[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat((u16x2)((w2 ^ (sg | top2)) - lo2), sp2));
+    }
+    const u16x2 m2 = __builtin_elementwise_min(
+        __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[0]), __builtin_bit_cast(u16x2, z[1])),
+        __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[2]), __builtin_bit_cast(u16x2, z[3])));
+    return m2.x == 0 || m2.y == 0;
+  };
+  auto hits = [&](const uint32_t (&wd)[4], const uint32_t (&z)[4], int vi) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (((z[k >> 1] >> (16 * (k & 1))) & 0xffffu) == 0u) append((wd[k >> 1] >> (16 * (k & 1))) & 0xffffu, vi * 8 + k);
+  };
+  // Vectors with a hit are recorded (up to kGatherRec per lane, 16-bit indices)
+  // and their ids handled after the scan, so a wave runs the per-id work a few
+  // times instead of in most steps when hits are spread over the row.
+  const bool defer = nfull <= 65536;
+  unsigned long long rec = 0;
+  int nrec = 0;
   for (int c0 = 0; c0 < nfull; c0 += kGatherChunk * kThreads) {
     uint32_t wv[kGatherChunk][4];
 #pragma unroll
@@ -2002,21 +2026,24 @@ XV_INLINE void gather_key_range(FastShared& fs, const bf16_t* row, int V, bool v
     for (int v = 0; v < kGatherChunk; ++v) {
       const int vi = c0 + v * kThreads + t;
       uint32_t z[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const u16x2 w2 = __builtin_bit_cast(u16x2, wv[v][k]);
-        const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
-        z[k] = __builtin_bit_cast(uint32_t, __builtin_elementwise_sub_sat((u16x2)((w2 ^ (sg | top2)) - lo2), sp2));
+      if (test(wv[v], z) && vi < nfull) {
+        if (defer && nrec < kGatherRec) {
+          rec |= (unsigned long long)(uint32_t)vi << (16 * nrec);
+          ++nrec;
+        } else {
+          hits(wv[v], z, vi);
+        }
       }
-      const u16x2 m2 = __builtin_elementwise_min(
-          __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[0]), __builtin_bit_cast(u16x2, z[1])),
-          __builtin_elementwise_min(__builtin_bit_cast(u16x2, z[2]), __builtin_bit_cast(u16x2, z[3])));
-      if (vi < nfull && (m2.x == 0 || m2.y == 0)) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-          if (((z[k >> 1] >> (16 * (k & 1))) & 0xffffu) == 0u)
-            append((wv[v][k >> 1] >> (16 * (k & 1))) & 0xffffu, vi * 8 + k);
-      }
+    }
+  }
+  for (int r = 0; __ballot(nrec > r); ++r) {
+    if (nrec > r) {
+      const int vi = (int)((rec >> (16 * r)) & 0xffffu);
+      const Vec8 x = load_vec8(row + 8u * (uint32_t)vi);
+      const uint32_t wd[4] = {x.w[0], x.w[1], x.w[2], x.w[3]};
+      uint32_t z[4];
+      test(wd, z);
+      hits(wd, z, vi);
     }
   }
   for (int id = nfull * 8 + t; id < V; id += kThreads) append((uint32_t)row[id], id);
