@@ -2184,13 +2184,8 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
     return;
   }
   const uint32_t kminp = wave_min_u(lane < a.R ? minp_l : 0xffffffffu);
-  if (t < kBuckets) {
-    s.cnt[t] = 0u;
-    s.mass[t] = 0ull;
-  }
-  if (t < kMaxSegs) segk[t] = 0ull;
-  __syncthreads();
-  {
+  if (t < kMaxSegs) segk[t] = 0ull;  // (ordered before its atomics by the scan's barriers)
+  {  // each group's partial sums of the buckets, then thread t < kBuckets adds the groups'
     uint32_t c = 0;
     unsigned long long m = 0;
 #pragma unroll
@@ -2199,12 +2194,18 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
         c += hc[j];
         m += hm[j];
       }
-    atomicAdd(&s.cnt[bt], c);
-    if (!p.use_k) atomicAdd(&s.mass[bt], m);
+    fs.wcnt[g][bt] = c;
+    fs.wmass[g][bt] = m;
   }
   __syncthreads();
-  const int64_t cnt = t < kBuckets ? (int64_t)s.cnt[t] : 0;
-  const int64_t mass = (t < kBuckets && !p.use_k) ? (int64_t)s.mass[t] : 0;
+  int64_t cnt = 0, mass = 0;
+  if (t < kBuckets) {
+#pragma unroll
+    for (int gg = 0; gg < kGroups; ++gg) {
+      cnt += fs.wcnt[gg][t];
+      mass += p.use_k ? 0 : (int64_t)fs.wmass[gg][t];
+    }
+  }
   int64_t cnt_excl, mass_excl, cnt_all, total;
   block_excl_scan2(s, cnt, mass, &cnt_excl, &mass_excl, &cnt_all, &total);
   const int64_t cnt_incl = cnt_excl + cnt, mass_incl = mass_excl + mass;
