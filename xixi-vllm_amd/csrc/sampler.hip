@@ -1178,13 +1178,12 @@ enum : int { kPlanDone = 0, kPlanGather = 1, kPlanDraw = 2, kPlanFallback = 3 };
 
 struct __attribute__((aligned(128))) RowPlan {
   int status;
-  int lo, hi;          // bucket range gathered
   int use_k;           // the list is the top-k candidates (draw from the list)
   int cut_p, cut_m;    // the top-p / min-p cut falls in the gathered bucket
   uint32_t kminp;      // min-p key (0xffffffff: none)
   uint32_t key_cut;
   uint32_t klo, khi;   // keys of buckets lo..hi: exactly [klo, khi]
-  float zmax, inv_t, bs;
+  float zmax, inv_t;
   int64_t thr, mp_before, m_before, id_cut, M;
 };
 
@@ -2246,15 +2245,12 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
   bool fallback = status == kPlanFallback;  // the boundary does not fit in LDS
   if (t == 0) {
     lp.status = status;
-    lp.lo = lo;
-    lp.hi = hi;
     lp.use_k = p.use_k;
     lp.cut_p = cut_p;
     lp.cut_m = cut_m;
     lp.kminp = kminp;
     lp.zmax = rc.zmax;
     lp.inv_t = rc.inv_t;
-    lp.bs = rc.bs;
     lp.thr = thr;
     lp.mp_before = m_before;
     lp.m_before = m_before;
