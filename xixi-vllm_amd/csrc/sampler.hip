@@ -1709,17 +1709,56 @@ XV_INLINE unsigned long long merge_top64(unsigned long long x, unsigned long lon
 
 XV_INLINE int wave_incl_scan_i(int x) { return (int)wave_incl_scan_l(x); }
 
+// 32-bit forms of the list operations above, for the segment lists: an entry
+// key << 13 | (8191 - offset of its id in the segment) orders as the 64-bit
+// candidate words do within one segment of at most 8192 ids, and each
+// compare-exchange stage then moves and selects one register, not two.
+XV_INLINE uint32_t xor_lane(uint32_t x, int s) {  // s a constant after unrolling
+  switch (s) {
+    case 1: return xor_lane<1>(x);
+    case 2: return xor_lane<2>(x);
+    case 4: return xor_lane<4>(x);
+    case 8: return xor_lane<8>(x);
+    case 16: return xor_lane<16>(x);
+    default: return xor_lane<32>(x);
+  }
+}
+XV_INLINE uint32_t wave_sort_desc32(uint32_t c) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t o = xor_lane(c, stride);
+      const bool take_max = ((lane & size) == 0) == ((lane & stride) == 0);
+      c = take_max ? max(o, c) : min(o, c);
+    }
+  return c;
+}
+template <int S>
+XV_INLINE uint32_t merge_stage32(uint32_t c) {  // the larger to the lane with bit S clear
+  const uint32_t o = xor_lane<S>(c);
+  return (threadIdx.x & S) ? min(o, c) : max(o, c);
+}
+XV_INLINE uint32_t merge_top64_32(uint32_t x, uint32_t y) {
+  const uint32_t c = max(x, xor_lane<32>(xor_lane<16>(dpp_u<0x140>(y))));  // y[63 - lane]
+  return merge_stage32<1>(merge_stage32<2>(merge_stage32<4>(merge_stage32<8>(merge_stage32<16>(merge_stage32<32>(c))))));
+}
+
 // Each wave selects the top kTopList of its own ids (vectors v * kSegThreads
 // + 64 w + lane of the segment, ids ascending in (v, lane, k) order) with no
 // workgroup barrier: its largest key, a wave-private LDS histogram of the
 // 256 keys below it (keys further down never touch LDS), the threshold key T
 // from a scan of that histogram (a bit-by-bit count over all keys when fewer
-// than kTopList lie that close), then a ballot compaction.  Wave 0 merges the
-// four sorted wave lists into the segment's list.
+// than kTopList lie that close), then a compaction by per-lane masks into a
+// 32-bit list it sorts.  Wave 0 merges the four sorted wave lists and writes
+// the segment's list as 64-bit candidate words.
 __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
   static_assert(kMaxSegs * kTopList <= kMaxCand, "the segment lists fit the row's list");
   __shared__ uint32_t hist[kSegWaves][256];
-  __shared__ unsigned long long wl[kSegWaves][kTopList];
+  static_assert(kTopVecs * 8 * kSegThreads <= 8192, "segment offsets fit the 13 bits of a list entry");
+  __shared__ uint32_t wl[kSegWaves][kTopList];
+  __shared__ uint4 kst[kTopVecs][kSegThreads];  // each thread's keys, packed as in kw
   const int b = blockIdx.y, r = blockIdx.x, t = threadIdx.x, w = t >> 6, lane = t & 63;
   const bf16_t* row = a.logits + (int64_t)b * a.stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
@@ -1749,24 +1788,48 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
                    (base + 2 * k + 1 < end ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
     }
   }
-  // A greedy row is torch.argmax: its NaNs (real ids only) take key 0xffff,
-  // above every value (at most 0xff80, +inf), so the list's first entry is
-  // the lowest NaN id when there is one.  Other rows drop NaN (key 0).
-  const bool greedy = a.temps[b] <= 1e-5f;
-  uint32_t kmax = 0;
+  // Order keys, two per packed 16-bit op: x ^ 0x8000 for a sign bit of 0,
+  // ~x for 1 (order_key's map on non-NaN values).  Finite keys lie in
+  // [0x7f, 0xff80]; NaN bits land outside, as do the padding words (0xffff
+  // gives key 0).  A lane holding any such key redoes them one at a time:
+  // NaN takes key 0 (dropped), except in a greedy row, which is
+  // torch.argmax: its NaNs (real ids only) take key 0xffff, above every value,
+  // so the list's first entry is the lowest NaN id when there is one.
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 top2 = {(unsigned short)0x8000u, (unsigned short)0x8000u};
+  u16x2 hi2 = {(unsigned short)0u, (unsigned short)0u}, lo2 = {(unsigned short)0xffffu, (unsigned short)0xffffu};
 #pragma unroll
   for (int v = 0; v < kTopVecs; ++v)
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      uint32_t k0 = order_key(kw[v][k] & 0xffffu), k1 = order_key(kw[v][k] >> 16);
-      if (greedy) {
-        const int id0 = beg + (v * kSegThreads + t) * 8 + 2 * k;
-        if (!k0 && v < nv && id0 < end) k0 = 0xffffu;
-        if (!k1 && v < nv && id0 + 1 < end) k1 = 0xffffu;
+      if (v >= nv) {
+        kw[v][k] = 0u;
+        continue;
       }
-      kw[v][k] = k0 | k1 << 16;
-      kmax = max(kmax, max(k0, k1));
+      const u16x2 w2 = __builtin_bit_cast(u16x2, kw[v][k]);
+      const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
+      const u16x2 k2 = w2 ^ (sg | top2);
+      kw[v][k] = __builtin_bit_cast(uint32_t, k2);
+      hi2 = __builtin_elementwise_max(hi2, k2);
+      lo2 = __builtin_elementwise_min(lo2, k2);
     }
+  uint32_t kmax = max((uint32_t)hi2.x, (uint32_t)hi2.y);
+  if (kmax > 0xff80u || min((uint32_t)lo2.x, (uint32_t)lo2.y) < 0x7fu) {
+    const bool greedy = a.temps[b] <= 1e-5f;
+    kmax = 0;
+#pragma unroll
+    for (int v = 0; v < kTopVecs; ++v)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        uint32_t k0 = kw[v][k] & 0xffffu, k1 = kw[v][k] >> 16;
+        const int id0 = beg + (v * kSegThreads + t) * 8 + 2 * k;
+        if (k0 > 0xff80u || k0 < 0x7fu) k0 = greedy && v < nv && id0 < end ? 0xffffu : 0u;
+        if (k1 > 0xff80u || k1 < 0x7fu) k1 = greedy && v < nv && id0 + 1 < end ? 0xffffu : 0u;
+        kw[v][k] = k0 | k1 << 16;
+        kmax = max(kmax, max(k0, k1));
+      }
+  }
   auto key_at = [&](int v, int k) { return (kw[v][k >> 1] >> (16 * (k & 1))) & 0xffffu; };
   kmax = wave_max_u(kmax);
   // count of this wave's keys >= x (wave uniform)
@@ -1836,48 +1899,82 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
       }
     }
   }
-  // compaction: keys > T, and keys == T in id order up to need_eq of them
+  // Compaction: keys > T, and keys == T in id order up to need_eq of them.
+  // Each lane marks what it takes in a 32-bit mask (bit 4v + j: key 2j of
+  // vector v, bit 16 + 4v + j: key 2j + 1), two keys per packed 16-bit
+  // compare; one wave scan of the counts gives each lane its slots, and a
+  // lane writes only its own candidates, reading their keys back from LDS.
   const bool rank_eq = n_eq > need_eq;
-  int filled = 0, eq_seen = 0;
+  const u16x2 one2 = {(unsigned short)1u, (unsigned short)1u};
+  uint32_t take = 0;
+  if (T != 0xffffffffu) {
+    // without ranking every key >= T is taken (keys > 0 when T is 0)
+    const uint32_t tg = rank_eq ? T : (T ? T - 1u : 0u);
+    const u16x2 tg2 = {(unsigned short)tg, (unsigned short)tg};
+    const u16x2 t2 = {(unsigned short)T, (unsigned short)T};
+    uint32_t ne = 0, valid = 0;  // ne: keys != T
 #pragma unroll
-  for (int v = 0; v < kTopVecs; ++v) {
-    if (v >= nv) break;
-    int eq_before = 0;  // keys == T at lower ids: earlier vectors, then lower lanes of this one
-    if (rank_eq) {
-      int me = 0;
+    for (int v = 0; v < kTopVecs; ++v) {
+      if (v >= nv) break;
+      valid |= 0x000f000fu << (4 * v);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) me += key_at(v, k) == T ? 1 : 0;
-      const int inc = wave_incl_scan_i(me);
-      eq_before = inc - me;
-      const int tot = __shfl(inc, 63);
-      eq_before += eq_seen;
-      eq_seen += tot;
+      for (int j = 0; j < 4; ++j) {
+        const u16x2 k2 = __builtin_bit_cast(u16x2, kw[v][j]);
+        take |= __builtin_bit_cast(uint32_t, __builtin_elementwise_min(__builtin_elementwise_sub_sat(k2, tg2), one2))
+                << (4 * v + j);
+        if (rank_eq) ne |= __builtin_bit_cast(uint32_t, __builtin_elementwise_min(k2 ^ t2, one2)) << (4 * v + j);
+      }
     }
+    if (rank_eq) {
+      // keys == T (T > 0 here, so never padding), ranked in id order: vector,
+      // then lane, then key.  Per-vector counts in 16-bit fields of one word
+      // (a wave holds at most 512 per vector), one scan for all four.
+      const uint32_t eq = ~ne & valid;
+      uint64_t pc = 0;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t key = key_at(v, k);
-      bool take = key > T && key != 0;
-      if (key == T && key != 0) {
-        take = rank_eq ? eq_before < need_eq : true;
-        ++eq_before;
+      for (int v = 0; v < kTopVecs; ++v) pc |= (uint64_t)__popc(eq & (0x000f000fu << (4 * v))) << (16 * v);
+      const uint64_t inc = (uint64_t)wave_incl_scan_l((int64_t)pc);
+      const uint64_t tot = (uint64_t)__shfl((long long)inc, 63);
+      // first rank of each vector's keys in this lane: the wave's counts in
+      // earlier vectors plus the lower lanes' in this one
+      uint64_t first = inc - pc, run = 0;
+#pragma unroll
+      for (int v = 0; v < kTopVecs; ++v) {
+        first += run << (16 * v);
+        run += (tot >> (16 * v)) & 0xffffu;
       }
-      const unsigned long long m = __ballot(take);
-      if (take) {
-        const int slot = filled + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-        const int id = beg + (v * kSegThreads + t) * 8 + k;
-        wl[w][slot] = ((unsigned long long)key << 32) | (unsigned long long)(0xffffffffu - (uint32_t)id);
+      for (uint32_t m = eq; m; m &= m - 1) {
+        const int bit = __builtin_ctz(m), v = (bit & 15) >> 2, j = bit & 3;
+        // this lane's keys == T of vector v at lower ids: pairs j' < j, and key 2j if this is 2j + 1
+        const uint32_t lower = ((((1u << j) - 1u) * 0x00010001u) << (4 * v)) | ((bit >> 4) ? 1u << (bit & 15) : 0u);
+        const int rank = (int)((first >> (16 * v)) & 0xffffu) + __popc(eq & lower);
+        if (rank < need_eq) take |= 1u << bit;
       }
-      filled += __popcll(m);
     }
   }
-  unsigned long long c = lane < filled ? wl[w][lane] : 0ull;
-  c = wave_sort_desc(c);
+  // this lane's keys, for reading back by position
+#pragma unroll
+  for (int v = 0; v < kTopVecs; ++v)
+    if (v < nv) kst[v][t] = make_uint4(kw[v][0], kw[v][1], kw[v][2], kw[v][3]);
+  const int mine = __popc(take);
+  const int incl = wave_incl_scan_i(mine);
+  const int filled = __shfl(incl, 63);
+  int slot = incl - mine;
+  for (uint32_t m = take; m; m &= m - 1, ++slot) {
+    const int bit = __builtin_ctz(m), v = (bit & 15) >> 2, k = 2 * (bit & 3) + (bit >> 4);
+    const uint32_t key = reinterpret_cast<const unsigned short*>(&kst[v][t])[k];
+    wl[w][slot] = key << 13 | (8191u - (uint32_t)((v * kSegThreads + t) * 8 + k));
+  }
+  uint32_t c = lane < filled ? wl[w][lane] : 0u;
+  c = wave_sort_desc32(c);
   wl[w][lane] = c;
   __syncthreads();
   if (w == 0) {
-    const unsigned long long m01 = merge_top64(c, wl[1][lane]);
-    const unsigned long long m23 = merge_top64(wl[2][lane], wl[3][lane]);
-    a.cand[(int64_t)b * a.cand_stride + (int64_t)r * kTopList + lane] = merge_top64(m01, m23);
+    const uint32_t m = merge_top64_32(merge_top64_32(c, wl[1][lane]), merge_top64_32(wl[2][lane], wl[3][lane]));
+    // back to the row's candidate word (key << 32 | ~id); 0 stays padding
+    const uint32_t id = (uint32_t)beg + (8191u - (m & 8191u));
+    a.cand[(int64_t)b * a.cand_stride + (int64_t)r * kTopList + lane] =
+        m ? ((unsigned long long)(m >> 13) << 32) | (unsigned long long)(0xffffffffu - id) : 0ull;
   }
 }
 
