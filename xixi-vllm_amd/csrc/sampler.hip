@@ -1849,16 +1849,23 @@ __global__ __launch_bounds__(kSegThreads) void seg_topk_kernel(SegArgs a) {
     need_eq = 0;
   } else {
     // histogram of keys kmax - j, j = 0..255, in this wave's LDS row
-    const uint32_t lo = kmax > 255u ? kmax - 255u : 0u;
+    const uint32_t lo = kmax > 256u ? kmax - 255u : 1u;  // key 0 (NaN, padding) never counts
 #pragma unroll
     for (int j = 0; j < 4; ++j) hist[w][lane + 64 * j] = 0u;
+    // distances below kmax two at a time (no wrap: no key exceeds kmax), and
+    // their byte offsets (which wrap only for distances past the range)
+    const uint32_t span = kmax - lo;
+    const u16x2 kmax2 = {(unsigned short)kmax, (unsigned short)kmax};
+    char* const hrow = reinterpret_cast<char*>(&hist[w][0]);
 #pragma unroll
     for (int v = 0; v < kTopVecs; ++v)
       if (v < nv)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t key = key_at(v, k);
-          if (key && key >= lo) atomicAdd(&hist[w][kmax - key], 1u);
+        for (int j = 0; j < 4; ++j) {
+          const u16x2 d2 = kmax2 - __builtin_bit_cast(u16x2, kw[v][j]);
+          const u16x2 o2 = d2 << (unsigned short)2;
+          if (d2.x <= span) atomicAdd(reinterpret_cast<uint32_t*>(hrow + o2.x), 1u);
+          if (d2.y <= span) atomicAdd(reinterpret_cast<uint32_t*>(hrow + o2.y), 1u);
         }
     // lane l holds bins 4l .. 4l + 3 (keys kmax - 4l downwards)
     uint32_t h[4];
