@@ -1465,6 +1465,42 @@ XV_INLINE unsigned long long wave_sort_desc(unsigned long long c) {
     }
   return c;
 }
+// 32-bit forms of the list operations, for lists whose words order as the
+// 64-bit candidate words do (a segment's key << 13 | (8191 - offset of the id
+// in the segment), the row merge's key << 16 | index): each compare-exchange
+// stage then moves and selects one register, not two.
+XV_INLINE uint32_t xor_lane(uint32_t x, int s) {  // s a constant after unrolling
+  switch (s) {
+    case 1: return xor_lane<1>(x);
+    case 2: return xor_lane<2>(x);
+    case 4: return xor_lane<4>(x);
+    case 8: return xor_lane<8>(x);
+    case 16: return xor_lane<16>(x);
+    default: return xor_lane<32>(x);
+  }
+}
+XV_INLINE uint32_t wave_sort_desc32(uint32_t c) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1)
+#pragma unroll
+    for (int stride = size >> 1; stride > 0; stride >>= 1) {
+      const uint32_t o = xor_lane(c, stride);
+      const bool take_max = ((lane & size) == 0) == ((lane & stride) == 0);
+      c = take_max ? max(o, c) : min(o, c);
+    }
+  return c;
+}
+template <int S>
+XV_INLINE uint32_t merge_stage32(uint32_t c) {  // the larger to the lane with bit S clear
+  const uint32_t o = xor_lane<S>(c);
+  return (threadIdx.x & S) ? min(o, c) : max(o, c);
+}
+XV_INLINE uint32_t merge_top64_32(uint32_t x, uint32_t y) {
+  const uint32_t c = max(x, xor_lane<32>(xor_lane<16>(dpp_u<0x140>(y))));  // y[63 - lane]
+  return merge_stage32<1>(merge_stage32<2>(merge_stage32<4>(merge_stage32<8>(merge_stage32<16>(merge_stage32<32>(c))))));
+}
+
 // First lane whose predicate holds, `none` if no lane's does.
 XV_INLINE int64_t wave_first(bool pred, int64_t none) {
   const unsigned long long m = __ballot(pred);
@@ -1473,14 +1509,15 @@ XV_INLINE int64_t wave_first(bool pred, int64_t none) {
 
 // The cut of a list of n <= 64 candidates, wave 0 alone: the same cut, kept
 // mass and draw as the workgroup list functions.
-// c: this lane's candidate (0 past n), in any order.
+// c: this lane's candidate (0 past n), in any order unless `sorted` says the
+// lanes hold the list sorted descending already.
 // segk: per segment in LDS, the kept mass of the buckets before the cut's
 // (rows without top-k; the list's part is added here).
 XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParams& p, int b, int n,
-                                 unsigned long long c, unsigned long long* segk) {
+                                 unsigned long long c, unsigned long long* segk, bool sorted = false) {
   const int lane = threadIdx.x & 63;
   const float inv_t = plan.inv_t, zmax = plan.zmax;
-  c = wave_sort_desc(c);
+  if (!sorted) c = wave_sort_desc(c);
   const int64_t q = lane < n ? cand_mass(c, inv_t, zmax) : 0;
   const int64_t incl = wave_incl_scan_l(q);
   const uint32_t key = cand_key(c);
@@ -1509,15 +1546,29 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
     // the kept list in ascending id order: re-keyed (~id << 32 | key), sorted descending
     const float u = a.uniforms ? a.uniforms[b] : 0.5f;
     const int64_t rdraw = draw_point(u, m_list);
-    unsigned long long e =
-        lane <= jcut ? ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c) : 0ull;
-    e = wave_sort_desc(e);
-    const int64_t qe = lane <= jcut ? mass_of(exp_of(key_to_bits((uint32_t)(e & 0xffffffffu)), inv_t, zmax)) : 0;
-    const int64_t ie = wave_incl_scan_l(qe);
-    const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
-    const unsigned long long ef = __shfl(e, fi < 0 ? 0 : (int)fi);
+    int64_t fid;
+    if (a.V <= (1 << 26)) {
+      // 32-bit words (0x3ffffff - id) << 6 | lane, sorted descending: ids
+      // ascending, each word naming the lane that holds its mass
+      uint32_t e = lane <= jcut ? (0x3ffffffu - (uint32_t)cand_id(c)) << 6 | (uint32_t)lane : 0u;
+      e = wave_sort_desc32(e);
+      const int64_t qe = (int64_t)__shfl((long long)q, (int)(e & 63u));
+      const int64_t ie = wave_incl_scan_l(lane <= jcut ? qe : 0);
+      const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
+      const uint32_t ef = __shfl(e, fi < 0 ? 0 : (int)fi);
+      fid = fi < 0 ? 0 : (int64_t)(0x3ffffffu - (ef >> 6));
+    } else {
+      unsigned long long e =
+          lane <= jcut ? ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c) : 0ull;
+      e = wave_sort_desc(e);
+      const int64_t qe = lane <= jcut ? mass_of(exp_of(key_to_bits((uint32_t)(e & 0xffffffffu)), inv_t, zmax)) : 0;
+      const int64_t ie = wave_incl_scan_l(qe);
+      const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
+      const unsigned long long ef = __shfl(e, fi < 0 ? 0 : (int)fi);
+      fid = fi < 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(ef >> 32));
+    }
     if (lane == 0) {
-      a.out_ids[b] = fi < 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(ef >> 32));
+      a.out_ids[b] = fid;
       plan.status = kPlanDone;
     }
     return;
@@ -1708,42 +1759,6 @@ XV_INLINE unsigned long long merge_top64(unsigned long long x, unsigned long lon
 }
 
 XV_INLINE int wave_incl_scan_i(int x) { return (int)wave_incl_scan_l(x); }
-
-// 32-bit forms of the list operations above, for the segment lists: an entry
-// key << 13 | (8191 - offset of its id in the segment) orders as the 64-bit
-// candidate words do within one segment of at most 8192 ids, and each
-// compare-exchange stage then moves and selects one register, not two.
-XV_INLINE uint32_t xor_lane(uint32_t x, int s) {  // s a constant after unrolling
-  switch (s) {
-    case 1: return xor_lane<1>(x);
-    case 2: return xor_lane<2>(x);
-    case 4: return xor_lane<4>(x);
-    case 8: return xor_lane<8>(x);
-    case 16: return xor_lane<16>(x);
-    default: return xor_lane<32>(x);
-  }
-}
-XV_INLINE uint32_t wave_sort_desc32(uint32_t c) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1)
-#pragma unroll
-    for (int stride = size >> 1; stride > 0; stride >>= 1) {
-      const uint32_t o = xor_lane(c, stride);
-      const bool take_max = ((lane & size) == 0) == ((lane & stride) == 0);
-      c = take_max ? max(o, c) : min(o, c);
-    }
-  return c;
-}
-template <int S>
-XV_INLINE uint32_t merge_stage32(uint32_t c) {  // the larger to the lane with bit S clear
-  const uint32_t o = xor_lane<S>(c);
-  return (threadIdx.x & S) ? min(o, c) : max(o, c);
-}
-XV_INLINE uint32_t merge_top64_32(uint32_t x, uint32_t y) {
-  const uint32_t c = max(x, xor_lane<32>(xor_lane<16>(dpp_u<0x140>(y))));  // y[63 - lane]
-  return merge_stage32<1>(merge_stage32<2>(merge_stage32<4>(merge_stage32<8>(merge_stage32<16>(merge_stage32<32>(c))))));
-}
 
 // Each wave selects the top kTopList of its own ids (vectors v * kSegThreads
 // + 64 w + lane of the segment, ids ascending in (v, lane, k) order) with no
@@ -1996,23 +2011,38 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
                a.flags & ~XV_SAMPLE_ALL_GREEDY, a.out_ids);
     return;
   }
-  unsigned long long* list = a.cand + (int64_t)b * a.cand_stride;
-  // level 0: wave w merges segment lists 2w and 2w + 1 (missing lists are empty)
+  const unsigned long long* list = a.cand + (int64_t)b * a.cand_stride;
+  // The merges run on 32-bit words key << 16 | (0xffff - i), i the entry's
+  // index r * kTopList + j in the row's lists (entry j of segment r's list):
+  // lists are sorted and segments ascend in id, so for equal keys a lower i
+  // is a lower id, and the words order as the candidates do.  The lists are
+  // staged in fs.cand to map the merged words back.  Level 0: wave w merges
+  // segment lists 2w and 2w + 1 (missing lists are empty); later levels
+  // alternate between two halves of a word buffer, one barrier each.
+  static_assert(kMaxSegs * kTopList <= 0x10000 && 2 * kWaves * kTopList <= kWaves * kBuckets, "word layout");
+  uint32_t* ml = &fs.wcnt[0][0];
+  auto word = [&](unsigned long long c, int i) { return c ? cand_key(c) << 16 | (0xffffu - (uint32_t)i) : 0u; };
   {
-    const unsigned long long x = 2 * w < a.R ? list[(2 * w) * kTopList + lane] : 0ull;
-    const unsigned long long y = 2 * w + 1 < a.R ? list[(2 * w + 1) * kTopList + lane] : 0ull;
-    fs.cand[w * kTopList + lane] = merge_top64(x, y);
+    const int i0 = (2 * w) * kTopList + lane, i1 = i0 + kTopList;
+    const unsigned long long x = 2 * w < a.R ? list[i0] : 0ull;
+    const unsigned long long y = 2 * w + 1 < a.R ? list[i1] : 0ull;
+    fs.cand[i0] = x;
+    fs.cand[i1] = y;
+    ml[w * kTopList + lane] = merge_top64_32(word(x, i0), word(y, i1));
   }
   __syncthreads();
+  int src = 0;
   for (int half = kWaves / 2; half >= 1; half >>= 1) {
-    unsigned long long m = 0;
-    if (w < half) m = merge_top64(fs.cand[(2 * w) * kTopList + lane], fs.cand[(2 * w + 1) * kTopList + lane]);
-    __syncthreads();
-    if (w < half) fs.cand[w * kTopList + lane] = m;
+    const int dst = src ^ (kWaves * kTopList);
+    if (w < half)
+      ml[dst + w * kTopList + lane] =
+          merge_top64_32(ml[src + (2 * w) * kTopList + lane], ml[src + (2 * w + 1) * kTopList + lane]);
+    src = dst;
     __syncthreads();
   }
   if (t >= 64) return;
-  const unsigned long long c = fs.cand[lane];
+  const uint32_t mw = ml[src + lane];
+  const unsigned long long c = mw ? fs.cand[0xffffu - (mw & 0xffffu)] : 0ull;
   const int n = __popcll(__ballot(c != 0ull));
   const unsigned long long top = __shfl(c, 0);
   if (p.greedy || n == 0) {  // argmax (NaN first for greedy rows); a sampled row of NaN only: 0
@@ -2029,7 +2059,7 @@ __global__ __launch_bounds__(kThreads) void row_topk_kernel(SegArgs a) {
     if (sampler_exp2(log2_ratio(key_to_bits(key), pl.inv_t, pl.zmax)) >= p.min_p) kminp = key;
   }
   pl.kminp = wave_min_u(kminp);
-  row_cut_wave_list(a, pl, p, b, n, c, nullptr);  // top-k: drawn from the list, no per-segment masses
+  row_cut_wave_list(a, pl, p, b, n, c, nullptr, true);  // top-k: drawn from the list, no per-segment masses
 }
 
 
