@@ -843,6 +843,57 @@ def test_sampler_topk_path_randomized_bitexact(dev):
         assert np.array_equal(got, want), (case, b, v, flags, kind, kmax)
 
 
+@pytest.mark.parametrize("path", ["topk", "chain", "greedy"])
+def test_sampler_unaligned_rows_with_infinities_bitexact(dev, path):
+    """Logit rows that do not start on a 16-byte boundary (a column-offset
+    view with an odd row stride, so every segment kernel takes its id-by-id
+    loads) holding +inf, -inf and NaN: the top-k path, the multi-workgroup
+    chain and the all-greedy path equal the C oracle on every row.  Rows
+    whose largest logit scales to a non-finite value (+inf, -inf, or a
+    finite logit past fp32's range at T 0.45) give every candidate mass 0,
+    and the draw takes the first candidate in rank order."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(4242 + len(path))
+    b, v = 40, 50021
+    base = _sampler_case(g, b, v + 3, std=1.0)
+    base[0, 1 + 7] = float("inf")             # one +inf: it takes all the mass
+    base[1, 1 : 1 + v // 2] = float("-inf")   # half the row at -inf
+    base[2, 1 + 100 : 1 + 200] = float("nan")
+    base[3, 1:] = float("-inf")               # -inf only but one finite logit
+    base[3, 1 + 4321] = 0.5
+    base[4, 1 + 9] = base[4, 1 + 90] = float("inf")  # two +inf: the lower id leads
+    base[5, 1:] = float("nan")                # NaN only
+    base[6, 1 + 40000 :] = float("-inf")
+    base[7, 1 + 555] = base[7, 1 + 556] = 3.0e38  # finite, but past fp32's range once divided by T
+    base[8, 1] = float("nan")                     # -inf only but a NaN in front
+    base[8, 2:] = float("-inf")
+    logits = base.to(dev)[:, 1 : 1 + v]       # rows start 2 bytes past 16-byte alignment
+    assert logits.data_ptr() % 16 != 0 and logits.stride(0) == v + 3
+    bits = base[:, 1 : 1 + v].contiguous().view(torch.int16).numpy().view(np.uint16)
+    temps = torch.rand(b, generator=g) + 0.4
+    tps = torch.rand(b, generator=g) * 0.5 + 0.45
+    tks = torch.randint(1, 65, (b,), generator=g, dtype=torch.int32)
+    mps = torch.rand(b, generator=g) * 0.2
+    u = torch.rand(b, generator=g)
+    temps[7] = 0.45
+    if path == "greedy":
+        temps.zero_()
+        flags, kw = 1, dict(all_greedy=True)
+    elif path == "topk":
+        temps[::6] = 0.0
+        flags, kw = 2 | 4 | 8, dict(use_top_k=True, use_top_p=True, use_min_p=True, max_top_k=64)
+    else:
+        temps[::6] = 0.0
+        flags, kw = 4 | 8, dict(use_top_p=True, use_min_p=True)
+    want = S.sample(bits, temps.numpy(), tps.numpy(), tks.numpy(), mps.numpy(), u.numpy(), flags)
+    got = sample(logits, temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev), **kw)
+    torch.cuda.synchronize()
+    print(f"unaligned rows {path}", flush=True)
+    assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
+
+
 @pytest.mark.parametrize("nbytes,shape", [(16, 0), (4096 * 16 + 48, 0), (4096 * 16 + 48, 1), (3 << 20, 1)])
 def test_stream_copy(dev, nbytes, shape):
     """The benchmark's copy yardstick copies exactly (both launch shapes, a

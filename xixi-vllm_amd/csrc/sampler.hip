@@ -930,6 +930,22 @@ XV_INLINE int64_t draw_point(float u, int64_t M) {
   return r;
 }
 
+// The draw's answer when no candidate has mass.  A scaled row maximum z_max
+// that is not finite (a largest logit of +inf or -inf, or a finite one past
+// fp32's range once divided by the temperature) makes d = z - z_max NaN at
+// the largest key (inf - inf), whose exp2 is 0, and -inf below it: every
+// mass is 0, and the draw takes the first candidate in rank order, the
+// lowest id holding the largest key.  With a finite z_max the largest logit
+// has mass 2^40 and is always kept, so this is the only way the kept mass is 0.
+XV_INLINE int64_t lowest_id_of_key(Shared& s, const bf16_t* row, int V, bool vec_ok, uint32_t key) {
+  uint32_t first = 0xffffffffu;
+  for_each_strided(row, V, vec_ok, [&](uint32_t bits, int id) {
+    if (id < V && order_key(bits) == key) first = min(first, (uint32_t)id);
+  });
+  first = block_min_u(s, first);
+  return first == 0xffffffffu ? 0 : (int64_t)first;
+}
+
 // The whole sampler for row b by one kThreads workgroup.
 XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __restrict__ logits, int64_t stride, int V,
                           const float* __restrict__ temps, const float* __restrict__ top_ps,
@@ -974,6 +990,11 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   kmin = block_min_u(s, kmin);
   const float inv_t = 1.0f / temp;
   const float zmax = bf16_to_f32(key_to_bits(kmax)) * inv_t;
+  if (kmax && !__builtin_isfinite(zmax)) {  // no mass anywhere
+    const int64_t id = lowest_id_of_key(s, row, V, vec_ok, kmax);
+    if (t == 0) out_ids[b] = id;
+    return;
+  }
   const float bs = kmax ? bucket_scale(log2_ratio(key_to_bits(kmin), inv_t, zmax)) : 16.0f;
 
   const int top_k = ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
@@ -1546,6 +1567,8 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
     // the kept list in ascending id order: re-keyed (~id << 32 | key), sorted descending
     const float u = a.uniforms ? a.uniforms[b] : 0.5f;
     const int64_t rdraw = draw_point(u, m_list);
+    // no mass in the list (z_max not finite, see lowest_id_of_key): its first candidate
+    const int64_t first = cand_id(__shfl(c, 0));
     int64_t fid;
     if (a.V <= (1 << 26)) {
       // 32-bit words (0x3ffffff - id) << 6 | lane, sorted descending: ids
@@ -1556,7 +1579,7 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
       const int64_t ie = wave_incl_scan_l(lane <= jcut ? qe : 0);
       const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
       const uint32_t ef = __shfl(e, fi < 0 ? 0 : (int)fi);
-      fid = fi < 0 ? 0 : (int64_t)(0x3ffffffu - (ef >> 6));
+      fid = fi < 0 ? first : (int64_t)(0x3ffffffu - (ef >> 6));
     } else {
       unsigned long long e =
           lane <= jcut ? ((unsigned long long)(0xffffffffu - (uint32_t)cand_id(c)) << 32) | cand_key(c) : 0ull;
@@ -1565,7 +1588,7 @@ XV_INLINE void row_cut_wave_list(const SegArgs& a, RowPlan& plan, const RowParam
       const int64_t ie = wave_incl_scan_l(qe);
       const int64_t fi = wave_first(lane <= jcut && ie > rdraw, -1);
       const unsigned long long ef = __shfl(e, fi < 0 ? 0 : (int)fi);
-      fid = fi < 0 ? 0 : (int64_t)(0xffffffffu - (uint32_t)(ef >> 32));
+      fid = fi < 0 ? first : (int64_t)(0xffffffffu - (uint32_t)(ef >> 32));
     }
     if (lane == 0) {
       a.out_ids[b] = fid;
@@ -2314,6 +2337,12 @@ __global__ __launch_bounds__(kThreads) void row_finish_kernel(SegArgs a) {
   const RowConsts rc = row_consts_of(lane < a.R ? kmax_l : 0u, lane < a.R ? kmin_l : 0xffffffffu, p.temp);
   if (rc.kmax == 0) {  // every logit NaN: nothing has mass
     if (t == 0) a.out_ids[b] = 0;
+    return;
+  }
+  if (!__builtin_isfinite(rc.zmax)) {  // no mass anywhere: the lowest id of the largest key
+    const bf16_t* row = a.logits + (int64_t)b * a.stride;
+    const int64_t id = lowest_id_of_key(s, row, a.V, ((reinterpret_cast<uintptr_t>(row) & 15u) == 0), rc.kmax);
+    if (t == 0) a.out_ids[b] = id;
     return;
   }
   const uint32_t kminp = wave_min_u(lane < a.R ? minp_l : 0xffffffffu);
