@@ -894,6 +894,48 @@ def test_sampler_unaligned_rows_with_infinities_bitexact(dev, path):
     assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
 
 
+@pytest.mark.parametrize("path", ["topk", "chain", "one_workgroup"])
+def test_sampler_parameter_edges_bitexact(dev, path):
+    """Sampling parameters at their edges, row by row: top-p 0, 1e-9 and 1;
+    min-p 1 and 1.5 (only the largest logit reaches it); top-k V, above V,
+    negative and 1; temperatures just above the greedy threshold (1.1e-5) and
+    very large (1e4, near-flat masses); uniforms 0 and just below 1.  Every
+    path equals the C oracle."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(515 + len(path))
+    b, v = 24, 32000
+    logits = _sampler_case(g, b, v, std=1.5)
+    temps = torch.full((b,), 0.8)
+    tps = torch.full((b,), 0.9)
+    tks = torch.full((b,), 40, dtype=torch.int32)
+    mps = torch.full((b,), 0.05)
+    u = torch.rand(b, generator=g)
+    tps[0], tps[1], tps[2] = 0.0, 1e-9, 1.0
+    mps[3], mps[4] = 1.0, 1.5
+    temps[5], temps[6], temps[7] = 1.1e-5, 1e4, 3.0
+    u[8], u[9] = 0.0, float(np.nextafter(np.float32(1), np.float32(0)))
+    tps[10], mps[10] = 1.0, 0.0                       # no cut but top-k
+    logits[11] = logits[11, 0]                        # one value repeated: a single tie group
+    temps[12] = 1e4
+    tps[12] = 0.999
+    if path == "topk":  # every k within the path's bound
+        tks[13], tks[14] = 1, 64
+        flags, kw = 2 | 4 | 8, dict(use_top_k=True, use_top_p=True, use_min_p=True, max_top_k=64)
+    else:
+        tks[13], tks[14], tks[15], tks[16] = v, v + 5, -3, 1
+        flags, kw = 2 | 4 | 8, dict(use_top_k=True, use_top_p=True, use_min_p=True)
+        if path == "one_workgroup":
+            kw["multi_workgroup"] = False
+    want = S.sample(logits.view(torch.int16).numpy().view(np.uint16), temps.numpy(), tps.numpy(), tks.numpy(),
+                    mps.numpy(), u.numpy(), flags)
+    got = sample(logits.to(dev), temps.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev), **kw)
+    torch.cuda.synchronize()
+    print(f"parameter edges {path}", flush=True)
+    assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
+
+
 @pytest.mark.parametrize("nbytes,shape", [(16, 0), (4096 * 16 + 48, 0), (4096 * 16 + 48, 1), (3 << 20, 1)])
 def test_stream_copy(dev, nbytes, shape):
     """The benchmark's copy yardstick copies exactly (both launch shapes, a

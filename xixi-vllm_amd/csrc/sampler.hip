@@ -997,12 +997,13 @@ XV_INLINE void sample_row(Shared& s, FastShared& fs, int b, const bf16_t* __rest
   }
   const float bs = kmax ? bucket_scale(log2_ratio(key_to_bits(kmin), inv_t, zmax)) : 16.0f;
 
-  const int top_k = ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
   const float top_p = ((flags & XV_SAMPLE_USE_TOP_P) && top_ps) ? top_ps[b] : 1.0f;
   const float min_p = ((flags & XV_SAMPLE_USE_MIN_P) && min_ps) ? min_ps[b] : 0.0f;
-  const bool use_k = top_k > 0 && top_k < V;
   const bool use_p = top_p < 1.0f;
   const bool use_m = min_p > 0.0f;
+  // a min-p above 1 keeps the first candidate alone (as row_params)
+  const int top_k = min_p > 1.0f ? 1 : ((flags & XV_SAMPLE_USE_TOP_K) && top_ks) ? top_ks[b] : V;
+  const bool use_k = top_k > 0 && top_k < V;
 
   uint32_t key_cut;
   int64_t id_cut, M;
@@ -1241,6 +1242,10 @@ XV_INLINE RowParams row_params(const SegArgs& a, int b) {
   p.top_k = ((a.flags & XV_SAMPLE_USE_TOP_K) && a.top_ks) ? a.top_ks[b] : a.V;
   p.top_p = ((a.flags & XV_SAMPLE_USE_TOP_P) && a.top_ps) ? a.top_ps[b] : 1.0f;
   p.min_p = ((a.flags & XV_SAMPLE_USE_MIN_P) && a.min_ps) ? a.min_ps[b] : 0.0f;
+  // No candidate reaches a min-p above 1 (the largest logit's ratio is
+  // exactly 1), and the kept set is then the first candidate alone, as a
+  // top-k of 1 keeps it.
+  if (p.min_p > 1.0f) p.top_k = 1;
   p.use_k = p.top_k > 0 && p.top_k < a.V;
   p.use_p = p.top_p < 1.0f;
   p.use_m = p.min_p > 0.0f;
