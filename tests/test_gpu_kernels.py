@@ -936,6 +936,38 @@ def test_sampler_parameter_edges_bitexact(dev, path):
     assert np.array_equal(got.cpu().numpy(), want), f"{got.cpu().numpy()} vs {want}"
 
 
+@pytest.mark.parametrize("v", [1, 2, 7, 9, 33])
+def test_sampler_tiny_vocabularies_bitexact(dev, v):
+    """Vocabularies smaller than one 8-id vector or a few of them: the greedy,
+    top-k, multi-workgroup and one-workgroup paths equal the C oracle."""
+    import oracle.sampler as S
+    from xvllm.sampler import sample
+
+    g = gen(808 + v)
+    b = 6
+    logits = _sampler_case(g, b, v, std=1.0)
+    if v > 2:
+        logits[1, 1] = float("nan")
+    temps = torch.rand(b, generator=g) + 0.5
+    temps[0] = 0.0
+    tps = torch.full((b,), 0.8)
+    tks = torch.full((b,), 3, dtype=torch.int32)
+    mps = torch.full((b,), 0.05)
+    u = torch.rand(b, generator=g)
+    bits = logits.view(torch.int16).numpy().view(np.uint16)
+    cases = [(1, dict(all_greedy=True)),
+             (2 | 4 | 8, dict(use_top_k=True, use_top_p=True, use_min_p=True, max_top_k=3)),
+             (2 | 4 | 8, dict(use_top_k=True, use_top_p=True, use_min_p=True)),
+             (4, dict(use_top_p=True, multi_workgroup=False))]
+    for flags, kw in cases:
+        t = torch.zeros(b) if flags == 1 else temps
+        want = S.sample(bits, t.numpy(), tps.numpy(), tks.numpy(), mps.numpy(), u.numpy(), flags)
+        got = sample(logits.to(dev), t.to(dev), tps.to(dev), tks.to(dev), mps.to(dev), u.to(dev), **kw)
+        torch.cuda.synchronize()
+        print(f"tiny vocabulary {v} {kw}", flush=True)
+        assert np.array_equal(got.cpu().numpy(), want), (kw, got.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("nbytes,shape", [(16, 0), (4096 * 16 + 48, 0), (4096 * 16 + 48, 1), (3 << 20, 1)])
 def test_stream_copy(dev, nbytes, shape):
     """The benchmark's copy yardstick copies exactly (both launch shapes, a
