@@ -379,7 +379,7 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  * flags: XV_SAMPLE_* bits mirroring the reference's host-side switches.
  * workspace: xv_sampler_workspace_size(B, V) bytes, zero-filled before its
  *   first use (each call leaves its greedy counters zero).  With it, all-greedy
- *   calls and calls of up to 128 rows spread each row over several workgroups
+ *   calls and calls of up to 512 rows spread each row over several workgroups
  *   (larger sampled batches take one workgroup per row, which fills the
  *   device); NULL selects one workgroup per row.  Both give identical ids.
  *   The size never decreases with B, and a workspace sized for B rows serves

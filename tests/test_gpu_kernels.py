@@ -679,17 +679,19 @@ def test_sampler_one_workspace_sampled_and_greedy_calls_interleaved(dev):
 
 
 def test_sampler_large_batches_bitexact(dev):
-    """Sampled batches of 129-256 rows (past the multi-workgroup chain's 128:
-    one workgroup per row): seeded top-k / top-p / min-p mixes with greedy
-    rows, flat and tied rows and NaN entries, equal to the C oracle on every
-    row."""
+    """Sampled batches of 129-513 rows (the multi-workgroup chain up to 512
+    rows, one workgroup per row past it): seeded top-k / top-p / min-p mixes
+    with greedy rows, flat and tied rows and NaN entries, equal to the C
+    oracle on every row."""
     import oracle.sampler as S
     from xvllm.sampler import sample
 
     rng = np.random.default_rng(4242)
-    for case, (b, flags, kind) in enumerate([(129, 4, "flat"), (200, 2 | 4, "normal"), (256, 4 | 8, "ties"),
-                                             (256, 2 | 4 | 8, "normal"), (160, 0, "wide"), (256, 4, "massive")]):
-        v = 151936
+    for case, (b, flags, kind, v) in enumerate([(129, 4, "flat", 151936), (200, 2 | 4, "normal", 151936),
+                                                (256, 4 | 8, "ties", 151936), (256, 2 | 4 | 8, "normal", 151936),
+                                                (160, 0, "wide", 151936), (256, 4, "massive", 151936),
+                                                (384, 4 | 8, "normal", 32000), (512, 2 | 4, "ties", 32000),
+                                                (513, 4, "flat", 32000)]):
         std = {"flat": 0.05, "normal": 1.0, "wide": 4.0, "ties": 1.0, "massive": 1.0}[kind]
         x = rng.standard_normal((b, v)).astype(np.float32) * std
         if kind == "ties":
