@@ -75,7 +75,10 @@ XV_INLINE float log2_ratio(uint32_t bits, float inv_t, float zmax) {
   return d * 1.44269502162933349609375f;
 }
 XV_INLINE float exp_of(uint32_t bits, float inv_t, float zmax) { return sampler_exp2(log2_ratio(bits, inv_t, zmax)); }
-XV_INLINE int64_t mass_of(float e) { return (int64_t)(e * 1099511627776.0f); }
+// e is in [0, 1] (exp2 of d <= 0; NaN gives 0), so the product converts as
+// an unsigned value: the same integer, without the signed conversion's sign
+// handling (about half its instructions).
+XV_INLINE int64_t mass_of(float e) { return (int64_t)(uint64_t)(e * 1099511627776.0f); }
 // Bucket of a candidate d below the max: floor(-d * bs), the last bucket
 // holding everything further.  bs is per row (bucket_scale); any bs > 0 keeps
 // the buckets monotone in the key, which is all the boundary search needs.
