@@ -1263,7 +1263,7 @@ XV_INLINE RowParams row_params(const SegArgs& a, int b) {
 // the segment is (c * kSegChunk + v) * kSegThreads + t; ids ascend within a
 // lane; slots outside the segment come as 0xffff (key 0).
 template <typename F>
-XV_INLINE void for_seg(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) {
+XV_INLINE void for_seg_chunks(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) {
   const int nvec = (end - beg + 7) / 8;
   for (int c = 0; c * kSegChunk * kSegThreads < nvec; ++c) {
     uint32_t w[kSegChunk][4];
@@ -1281,13 +1281,32 @@ XV_INLINE void for_seg(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) 
                     (base + 2 * k + 1 < end ? (uint32_t)row[base + 2 * k + 1] : 0xffffu) << 16;
       }
     }
+    f(w, c);
+  }
+}
+template <typename F>
+XV_INLINE void for_seg(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) {
+  for_seg_chunks(row, vec_ok, beg, end, [&](const uint32_t (&w)[kSegChunk][4], int c) {
 #pragma unroll
     for (int v = 0; v < kSegChunk; ++v) {
       const int base = beg + ((c * kSegChunk + v) * kSegThreads + (int)threadIdx.x) * 8;
 #pragma unroll
       for (int k = 0; k < 8; ++k) f((w[v][k >> 1] >> (16 * (k & 1))) & 0xffffu, base + k);
     }
-  }
+  });
+}
+
+// f(word) for every 32-bit word (two ids, the lower in the low half) of the
+// segment's vectors, in for_seg's order; slots outside the segment come as
+// 0xffff halves.
+template <typename F>
+XV_INLINE void for_seg_words(const bf16_t* row, bool vec_ok, int beg, int end, F&& f) {
+  for_seg_chunks(row, vec_ok, beg, end, [&](const uint32_t (&w)[kSegChunk][4], int) {
+#pragma unroll
+    for (int v = 0; v < kSegChunk; ++v)
+#pragma unroll
+      for (int k = 0; k < 4; ++k) f(w[v][k]);
+  });
 }
 
 struct SegRed {
@@ -1398,12 +1417,34 @@ __global__ __launch_bounds__(kSegThreads) void seg_stats_kernel(SegArgs a) {
     if (threadIdx.x == 0) a.seg_best[b * a.R + r] = best;
     return;
   }
-  uint32_t kmax = 0, kmin = 0xffffffffu;
-  for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) {
-    const uint32_t key = order_key(bits);
-    kmax = max(kmax, key);
-    kmin = min(kmin, key ? key : 0xffffffffu);
+  // Order keys two per packed op (x ^ 0x8000, or ~x for a set sign bit):
+  // finite keys lie in [0x7f, 0xff80], padding (0xffff) gives key 0, and
+  // the smallest key is taken as min(key - 1) + 1 so that key 0 wraps above
+  // every other.  NaN bits land outside [0x7f, 0xff80]; a lane that holds
+  // one redoes its ids one at a time with order_key (NaN: key 0).
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 top2 = {(unsigned short)0x8000u, (unsigned short)0x8000u}, one2 = {(unsigned short)1u, (unsigned short)1u};
+  u16x2 hi2 = {(unsigned short)0u, (unsigned short)0u}, lo2 = {(unsigned short)0xffffu, (unsigned short)0xffffu};
+  for_seg_words(row, vec_ok, beg, end, [&](uint32_t wd) {
+    const u16x2 w2 = __builtin_bit_cast(u16x2, wd);
+    const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
+    const u16x2 k2 = w2 ^ (sg | top2);
+    hi2 = __builtin_elementwise_max(hi2, k2);
+    lo2 = __builtin_elementwise_min(lo2, (u16x2)(k2 - one2));
   });
+  uint32_t kmax = max((uint32_t)hi2.x, (uint32_t)hi2.y);
+  const uint32_t km1 = min((uint32_t)lo2.x, (uint32_t)lo2.y);
+  uint32_t kmin = km1 == 0xffffu ? 0xffffffffu : km1 + 1u;
+  if (kmax > 0xff80u || kmin < 0x7fu) {
+    kmax = 0;
+    kmin = 0xffffffffu;
+    for_seg(row, vec_ok, beg, end, [&](uint32_t bits, int) {
+      const uint32_t key = order_key(bits);
+      kmax = max(kmax, key);
+      kmin = min(kmin, key ? key : 0xffffffffu);
+    });
+  }
   kmax = seg_max_u(red, kmax);
   kmin = seg_min_u(red, kmin);
   if (threadIdx.x == 0) {
