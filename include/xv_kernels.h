@@ -394,7 +394,7 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
 /* Every row's top_k is in [1, 64] (the reference's host-side max_top_k,
  * src/compute/batch.py:251, at most 64): with a workspace, a two-launch
  * top-k path that reads the logits once (batches whose B x 32 x 64 candidate
- * lists fit the workspace's sampled region: up to 1500 rows at V 151936).
+ * lists fit the workspace's sampled region: up to 4101 rows at V 151936).
  * Ids are the same with or without it; a row outside the bound is still
  * sampled exactly (one workgroup for that row). */
 #define XV_SAMPLE_TOP_K_LE_64 16
