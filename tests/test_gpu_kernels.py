@@ -970,6 +970,28 @@ def test_sampler_tiny_vocabularies_bitexact(dev, v):
         assert np.array_equal(got.cpu().numpy(), want), (kw, got.cpu().numpy(), want)
 
 
+def test_sampler_topk_path_many_rows_agrees(dev):
+    """1800 rows at V 151936 with max_top_k 64 (past the 1514 rows the top-k
+    path's lists fit while the sampled region was sized for 128 rows): the
+    top-k path gives the ids of the one-workgroup path, which the oracle pins
+    elsewhere."""
+    from xvllm.sampler import sample
+
+    g = gen(1800)
+    b, v = 1800, 151936
+    logits = _sampler_case(g, b, v, std=1.0).to(dev)
+    temps = (torch.rand(b, generator=g) + 0.4).to(dev)
+    tps = (torch.rand(b, generator=g) * 0.5 + 0.45).to(dev)
+    tks = torch.randint(1, 65, (b,), generator=g, dtype=torch.int32).to(dev)
+    u = torch.rand(b, generator=g).to(dev)
+    kw = dict(use_top_k=True, use_top_p=True)
+    got = sample(logits, temps, tps, tks, None, u, **kw, max_top_k=64)
+    want = sample(logits, temps, tps, tks, None, u, **kw, multi_workgroup=False)
+    torch.cuda.synchronize()
+    print("top-k path 1800 rows", flush=True)
+    assert torch.equal(got, want), torch.nonzero(got != want)[:8].flatten().tolist()
+
+
 @pytest.mark.parametrize("nbytes,shape", [(16, 0), (4096 * 16 + 48, 0), (4096 * 16 + 48, 1), (3 << 20, 1)])
 def test_stream_copy(dev, nbytes, shape):
     """The benchmark's copy yardstick copies exactly (both launch shapes, a
