@@ -254,11 +254,6 @@ XV_INLINE unsigned long long wave_max_ull(unsigned long long x) {
   return x;
 }
 
-// x[63 - lane]: row_mirror (lane i of a row reads lane 15 - i), then the row swaps
-XV_INLINE unsigned long long reverse_lanes64(unsigned long long x) {
-  const uint32_t lo = dpp_u<0x140>((uint32_t)x), hi = dpp_u<0x140>((uint32_t)(x >> 32));
-  return xor_lane64<32>(xor_lane64<16>(((unsigned long long)hi << 32) | lo));
-}
 
 // x[lane - S] within the lane's 16-lane row (0 for the first S lanes of a
 // row), and the cross-row broadcasts of lane 15 (into rows 1, 3) and lane 31
@@ -1570,8 +1565,12 @@ XV_INLINE uint32_t merge_stage32(uint32_t c) {  // the larger to the lane with b
   const uint32_t o = xor_lane<S>(c);
   return (threadIdx.x & S) ? min(o, c) : max(o, c);
 }
+// Top 64 of two lists sorted descending (lane j holds element j of each):
+// the elementwise max against the reversed second list is bitonic and holds
+// the top 64; six compare-exchange stages sort it descending.  y[63 - lane]
+// is row_mirror (lane i of a row reads lane 15 - i), then the row swaps.
 XV_INLINE uint32_t merge_top64_32(uint32_t x, uint32_t y) {
-  const uint32_t c = max(x, xor_lane<32>(xor_lane<16>(dpp_u<0x140>(y))));  // y[63 - lane]
+  const uint32_t c = max(x, xor_lane<32>(xor_lane<16>(dpp_u<0x140>(y))));
   return merge_stage32<1>(merge_stage32<2>(merge_stage32<4>(merge_stage32<8>(merge_stage32<16>(merge_stage32<32>(c))))));
 }
 
@@ -1818,21 +1817,6 @@ XV_INLINE bool row_cut_by_keys(const SegArgs& a, RowPlan& plan, Shared& s, FastS
 // the caller's claim.
 constexpr int kTopList = 64;
 constexpr int kTopVecs = 4;  // 8-id vectors per thread in registers: segments of up to 8192 ids
-
-// Top 64 of two lists sorted descending (lane j holds element j of each):
-// the elementwise max against the reversed second list is bitonic and holds
-// the top 64; six compare-exchange stages sort it descending.
-XV_INLINE unsigned long long merge_top64(unsigned long long x, unsigned long long y) {
-  const int lane = threadIdx.x & 63;
-  const unsigned long long yr = reverse_lanes64(y);
-  unsigned long long c = x > yr ? x : yr;
-#pragma unroll
-  for (int stride = 32; stride > 0; stride >>= 1) {
-    const unsigned long long o = xor_lane64(c, stride);
-    c = (lane & stride) ? (o < c ? o : c) : (o > c ? o : c);
-  }
-  return c;
-}
 
 XV_INLINE int wave_incl_scan_i(int x) { return (int)wave_incl_scan_l(x); }
 
