@@ -373,9 +373,12 @@ int xv_silu_and_mul(const void* x, int64_t x_stride, void* out, int64_t out_stri
  * shortest prefix satisfying top-k (top_ks[b] < V), top-p (a candidate is
  * dropped when the mass strictly before it exceeds top_p of the top-k mass)
  * and min-p (dropped when its probability is below min_p times the largest);
- * the first candidate is always kept.  The token is then drawn by inverse CDF
- * over the kept set in ascending id order with the explicit uniform
- * uniforms[b] in [0, 1), masses in 2^-40 fixed point (exact integer sums).
+ * the first candidate is always kept (with min_p above 1 it alone).  The
+ * token is then drawn by inverse CDF over the kept set in ascending id order
+ * with the explicit uniform uniforms[b] in [0, 1), masses in 2^-40 fixed
+ * point (exact integer sums).  NaN logits of sampled rows have no mass; a row
+ * whose scaled maximum is not finite (+inf or -inf, or past fp32's range)
+ * has no mass anywhere and returns its first candidate.
  * flags: XV_SAMPLE_* bits mirroring the reference's host-side switches.
  * workspace: xv_sampler_workspace_size(B, V) bytes, zero-filled before its
  *   first use (each call leaves its greedy counters zero).  With it, all-greedy
