@@ -1069,8 +1069,9 @@ __global__ __launch_bounds__(kThreads) void sample_kernel(const bf16_t* __restri
 // ---------------------------------------------------------------------------
 // All-greedy batches over several workgroups per row (a small batch would
 // leave most CUs idle with one workgroup per row).  A lane keeps the largest
-// logit of its ids and the lowest id holding it (float compares: -0 equals
-// +0), and its lowest NaN id, as the one-workgroup path does.  Each workgroup
+// order key of its ids (-0 folded into +0, which torch.argmax treats as equal)
+// and the lowest id holding it, and its lowest NaN id, as the one-workgroup
+// path does with float compares.  Each workgroup
 // then folds its best into the row's 64-bit slot with one atomic max of
 //   order key << 32 | (2^32 - 1 - id)      (greedy_word: NaN above every value)
 // (as torch.argmax: a NaN wins, then the largest logit, among equals the lowest id) and counts
@@ -1104,29 +1105,74 @@ __global__ __launch_bounds__(kGreedyThreads) void greedy_segment_kernel(const bf
   const bf16_t* row = logits + (int64_t)b * stride;
   const bool vec_ok = ((reinterpret_cast<uintptr_t>(row) & 15u) == 0);
   const int beg = blockIdx.x * seg_len, end = min(V, beg + seg_len);
-  float fm = -INFINITY;
+  // The lane's best as an order key with -0 folded into +0 (torch.argmax
+  // treats them as equal), its lowest id, and its lowest NaN id.  A vector's
+  // keys are computed two per packed op; only a vector whose largest key
+  // beats the lane's best is searched id by id, and a vector holding a NaN
+  // or padding (keys outside [0x7f, 0xff80]) goes id by id as well.
+  typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+  typedef short s16x2 __attribute__((ext_vector_type(2)));
+  const u16x2 top2 = {(unsigned short)0x8000u, (unsigned short)0x8000u}, one2 = {(unsigned short)1u, (unsigned short)1u};
+  uint32_t bk = 0;
   int bid = -1, nid = -1;
   constexpr int step = kGreedyThreads * 8;
   for (int i0 = beg + threadIdx.x * 8; i0 < end; i0 += kGreedyUnroll * step) {
-    uint32_t bits[kGreedyUnroll][8];
+    uint32_t w[kGreedyUnroll][4];
 #pragma unroll
-    for (int u = 0; u < kGreedyUnroll; ++u)
-      if (i0 + u * step < end) load8(row, V, i0 + u * step, vec_ok, bits[u]);
+    for (int u = 0; u < kGreedyUnroll; ++u) {
+      const int i = i0 + u * step;
+      if (i < end && vec_ok && i + 8 <= end) {
+        const Vec8 x = load_vec8(row + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) w[u][k] = x.w[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          w[u][k] = (i + 2 * k < end ? (uint32_t)row[i + 2 * k] : 0xffffu) |
+                    (i + 2 * k + 1 < end ? (uint32_t)row[i + 2 * k + 1] : 0xffffu) << 16;
+      }
+    }
 #pragma unroll
     for (int u = 0; u < kGreedyUnroll; ++u) {
       const int i = i0 + u * step;
       if (i >= end) break;
+      uint32_t kk[4];
+      u16x2 hi2 = {(unsigned short)0u, (unsigned short)0u}, lo2 = {(unsigned short)0xffffu, (unsigned short)0xffffu};
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const float v = bf16_to_f32(bits[u][k]);
-        const bool better = v > fm && i + k < end;  // ids ascend within a lane: keeps the lowest
-        fm = better ? v : fm;
-        bid = better ? i + k : bid;
-        nid = (nid < 0 && i + k < end && !order_key(bits[u][k])) ? i + k : nid;
+      for (int k = 0; k < 4; ++k) {
+        u16x2 w2 = __builtin_bit_cast(u16x2, w[u][k]);
+        w2 = w2 * __builtin_elementwise_min(w2 ^ top2, one2);  // -0 (0x8000) -> +0
+        const u16x2 sg = __builtin_bit_cast(u16x2, (s16x2)(__builtin_bit_cast(s16x2, w2) >> (short)15));
+        const u16x2 k2 = w2 ^ (sg | top2);
+        kk[k] = __builtin_bit_cast(uint32_t, k2);
+        hi2 = __builtin_elementwise_max(hi2, k2);
+        lo2 = __builtin_elementwise_min(lo2, k2);
+      }
+      const uint32_t vmax = max((uint32_t)hi2.x, (uint32_t)hi2.y), vmin = min((uint32_t)lo2.x, (uint32_t)lo2.y);
+      if (vmax > 0xff80u || vmin < 0x7fu) {  // NaN or padding: id by id
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t key = (kk[k >> 1] >> (16 * (k & 1))) & 0xffffu;
+          const bool real = i + k < end;
+          const bool nan = real && (key > 0xff80u || key < 0x7fu);
+          nid = (nid < 0 && nan) ? i + k : nid;
+          const bool better = real && !nan && key > bk;
+          bid = better ? i + k : bid;
+          bk = better ? key : bk;
+        }
+      } else if (vmax > bk) {  // the lowest id holding the vector's largest key
+        int first = 7;
+#pragma unroll
+        for (int k = 7; k >= 0; --k) first = ((kk[k >> 1] >> (16 * (k & 1))) & 0xffffu) == vmax ? k : first;
+        bk = vmax;
+        bid = i + first;
       }
     }
   }
-  unsigned long long best = wave_max_ull(greedy_word(fm, bid, nid));
+  unsigned long long best = 0;
+  if (nid >= 0) best = (0xffffull << 32) | (0xffffffffu - (uint32_t)nid);
+  else if (bid >= 0) best = ((unsigned long long)bk << 32) | (0xffffffffu - (uint32_t)bid);
+  best = wave_max_ull(best);
   __shared__ unsigned long long wbest[kGreedyThreads / 64];
   if ((threadIdx.x & 63) == 0) wbest[threadIdx.x >> 6] = best;
   __syncthreads();
