@@ -10,7 +10,7 @@ def gen(seed: int) -> torch.Generator:
 
 
 def randn_bf16(shape, g, std=1.0, mean=0.0):
-    """fp32 draw then bf16 cast (the survey's synthetic-input convention)."""
+    """fp32 draw then bf16 cast (how every synthetic input here is made)."""
     return (torch.randn(shape, generator=g) * std + mean).to(torch.bfloat16)
 
 
